@@ -1,0 +1,183 @@
+/*
+ * qwentts_amd.h -- C ABI of the MI355X (gfx950) decode kernels for Qwen3-TTS.
+ *
+ * Two persistent HIP kernels each run a full per-token transformer pass in one cooperative
+ * launch:
+ *   - backbone ("talker") kernel: N layers of RMSNorm -> QKV -> interleaved 3D mRoPE -> GQA
+ *     attention over a bf16 KV cache -> SwiGLU MLP, final RMSNorm, optional codec-head logits
+ *     and on-device token selection;
+ *   - code-predictor kernel: N layers with 1D RoPE and an f32 KV cache, stepped once
+ *     (reference entry point) or 16 positions per launch with the 15 lm-heads, on-device
+ *     token selection, embedding gathers and the codebook-embedding combine (frame entry).
+ *
+ * All pointers are device pointers unless stated otherwise. Every entry point returns a
+ * hipError_t (the reference's launchers return void). Errors detected on the device (a wait
+ * that timed out, i.e. a grid that cannot be co-resident or a corrupted workspace) are
+ * latched in the workspace and reported by qtts_workspace_check().
+ *
+ * Dimensions are fixed by the model (reference config.cuh:33-40): hidden 1024, 16 query
+ * heads, 8 KV heads, head_dim 128, intermediate 3072. Layer counts, positions and cache
+ * lengths are runtime arguments.
+ */
+#ifndef QWENTTS_AMD_H
+#define QWENTTS_AMD_H
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Per-layer weight pointers, in the reference's struct order: bf16 tensors, row-major
+ * [out, in] as nn.Linear stores them.
+ * Replaces: TTSLayerWeights   (/root/reference/qwentts_turbo/csrc/fused_decode_tts.cu:22-34)
+ *           CPLayerWeights    (/root/reference/qwentts_turbo/csrc/fused_decode_code_predictor.cu:30-42)
+ * Host mirrors: megakernel_backbone.py:43-55, megakernel_code_predictor.py:47-59. */
+typedef struct TTSLayerWeights {
+    const void* input_layernorm_weight;     /* [1024]        */
+    const void* q_proj_weight;              /* [2048, 1024]  */
+    const void* k_proj_weight;              /* [1024, 1024]  */
+    const void* v_proj_weight;              /* [1024, 1024]  */
+    const void* q_norm_weight;              /* [128]         */
+    const void* k_norm_weight;              /* [128]         */
+    const void* o_proj_weight;              /* [1024, 2048]  */
+    const void* post_attn_layernorm_weight; /* [1024]        */
+    const void* gate_proj_weight;           /* [3072, 1024]  */
+    const void* up_proj_weight;             /* [3072, 1024]  */
+    const void* down_proj_weight;           /* [1024, 3072]  */
+} TTSLayerWeights;
+typedef TTSLayerWeights CPLayerWeights;
+
+/* ---------------------------------------------------------------------------------------
+ * Reference-compatible launchers (same argument lists; hipStream_t; return hipError_t).
+ *
+ * The scratch arguments (hidden_buffer .. g_mlp_intermediate) keep the reference's sizes and
+ * meaning at the boundary: on return hidden_buffer holds the last layer's residual stream
+ * (bf16 [1024] for the backbone, f32 [1024] for the code predictor) and g_normalized the
+ * final-RMSNorm hidden (f32 [1024]). The inter-workgroup exchange buffers these kernels need
+ * live in a library-owned workspace per device (allocated on first use with hipMalloc);
+ * calls that overlap in time on one device share it and therefore race, exactly as the
+ * reference's per-object scratch does.
+ *
+ * k_cache / v_cache: [num_layers, 8, max_seq_len, 128], bf16 (backbone) or f32 (CP).
+ * cache_len must equal position + 1 (the reference passes it that way) and position must be
+ * < max_seq_len; attn_scale is 1/sqrt(128). cos_table / sin_table: bf16 [>= max_seq_len, 128].
+ * ------------------------------------------------------------------------------------- */
+
+/* Replaces: launch_tts_decode (/root/reference/qwentts_turbo/csrc/fused_decode_tts.cu:664-722) */
+hipError_t launch_tts_decode(
+    int input_token_id, const void* embed_weight, const TTSLayerWeights* layer_weights,
+    const void* final_norm_weight, const void* cos_table, const void* sin_table,
+    void* k_cache, void* v_cache, void* hidden_buffer, void* g_activations, void* g_residual,
+    void* g_q, void* g_k, void* g_v, void* g_attn_out, void* g_mlp_intermediate,
+    void* g_normalized, int num_layers, int position, int cache_len, int max_seq_len,
+    float attn_scale, hipStream_t stream);
+
+/* Replaces: launch_tts_decode_with_embedding (/root/reference/qwentts_turbo/csrc/fused_decode_tts.cu:834-890) */
+hipError_t launch_tts_decode_with_embedding(
+    const void* input_embedding, const TTSLayerWeights* layer_weights,
+    const void* final_norm_weight, const void* cos_table, const void* sin_table,
+    void* k_cache, void* v_cache, void* hidden_buffer, void* g_activations, void* g_residual,
+    void* g_q, void* g_k, void* g_v, void* g_attn_out, void* g_mlp_intermediate,
+    void* g_normalized, int num_layers, int position, int cache_len, int max_seq_len,
+    float attn_scale, hipStream_t stream);
+
+/* Replaces: launch_cp_decode_with_embedding (/root/reference/qwentts_turbo/csrc/fused_decode_code_predictor.cu:674-730) */
+hipError_t launch_cp_decode_with_embedding(
+    const void* input_embedding, const CPLayerWeights* layer_weights,
+    const void* final_norm_weight, const void* cos_table, const void* sin_table,
+    void* k_cache, void* v_cache, void* hidden_buffer, void* g_activations, void* g_residual,
+    void* g_q, void* g_k, void* g_v, void* g_attn_out, void* g_mlp_intermediate,
+    void* g_normalized, int num_layers, int position, int cache_len, int max_seq_len,
+    float attn_scale, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Extended API: explicit workspace, 3D rotary positions, fused heads and token selection.
+ * Used by the PyTorch extension (MegakernelTTSDecoder / MegakernelCodePredictorDecoder).
+ * ------------------------------------------------------------------------------------- */
+
+typedef struct QttsWorkspace QttsWorkspace; /* opaque, device-resident */
+
+/* Bytes of device memory a workspace needs; the memory must be zero-filled before first use. */
+size_t qtts_workspace_bytes(void);
+
+/* Validates the device (gfx950, 256 CUs in 8 XCDs, cooperative launch) once per device and
+ * binds a caller-allocated, zero-filled workspace of qtts_workspace_bytes() bytes.
+ * Returns hipErrorInvalidDevice when the device cannot run these kernels. */
+hipError_t qtts_workspace_init(void* workspace, int device);
+
+/* Reads and clears the device-side error word of a workspace (synchronises the stream).
+ * *error_code = 0 when every wait completed; bit 0 = a wait timed out. */
+hipError_t qtts_workspace_check(void* workspace, unsigned int* error_code, hipStream_t stream);
+
+/* Token selection for one head (backbone g0 or a code-predictor group).
+ * Mirrors generator.py:178-207: optional EOS suppression, greedy argmax (lowest index on
+ * ties) or temperature -> top-k (ties with the k-th value kept) -> top-p (a value is kept
+ * when the probability mass of strictly larger values is <= top_p) -> Gumbel-max draw with
+ * Philox-4x64-10 noise keyed by (seed, frame_step, group, vocab id). */
+typedef struct QttsSampling {
+    int do_sample;
+    float temperature;
+    int top_k;
+    float top_p;
+    unsigned long long seed;
+} QttsSampling;
+
+/* One backbone decode step.
+ *   input_embedding: bf16 [1024] (or NULL to gather row input_token_id of embed_weight)
+ *   pos3: rotary positions (t, h, w) for interleaved mRoPE; all equal = 1D RoPE
+ *   position: cache slot written (attends to slots [0, position])
+ *   out_hidden: f32 [1024] final-norm hidden; out_residual: bf16 [1024] (may be NULL)
+ *   codec_head: bf16 [vocab, 1024] or NULL (no logits); out_logits: f32 [vocab] or NULL
+ *   When codec_head != NULL and out_token != NULL the step also selects a token:
+ *     if mask_tail != 0 the ids [vocab-1024, vocab) except eos_id are masked (the
+ *     generator's suppress mask, generator.py:71-75), the repetition penalty is
+ *     applied to the ids in history[0..n_history) (device int array), eos_id is additionally
+ *     masked when suppress_eos != 0, then QttsSampling picks *out_token (device int).
+ *   skip_if: device int or NULL; when it holds a nonzero value the launch does nothing (used
+ *     to stop a queued frame loop after EOS without a host round trip). */
+hipError_t qtts_backbone_step(
+    void* workspace, const TTSLayerWeights* layer_weights, int num_layers,
+    const void* final_norm_weight, const void* cos_table, const void* sin_table,
+    void* k_cache, void* v_cache, int max_seq_len, int position, const int pos3[3],
+    const void* input_embedding, const void* embed_weight, int input_token_id,
+    float* out_hidden, void* out_residual,
+    const void* codec_head, int vocab, float* out_logits,
+    int* out_token, int mask_tail, const int* history, int n_history, float repetition_penalty,
+    int eos_id, int suppress_eos, const QttsSampling* sampling, int frame_step,
+    const int* skip_if, hipStream_t stream);
+
+/* One code-predictor step (no head): the reference's CP decode with a workspace. */
+hipError_t qtts_cp_step(
+    void* workspace, const CPLayerWeights* layer_weights, int num_layers,
+    const void* final_norm_weight, const void* cos_table, const void* sin_table,
+    void* k_cache, void* v_cache, int max_seq_len, int position,
+    const void* input_embedding, float* out_hidden, float* out_residual, hipStream_t stream);
+
+/* Whole code-predictor frame in one launch (generator.py:309-362 moved on-device):
+ *   position 0 input = bf16(bb_hidden) (f32 [1024]), position 1 input = bb_embedding[*g0],
+ *   then for g = 0..n_groups-1: logits_g = lm_heads[g] . bf16(h), token g+1 selected with
+ *   `sampling` (group g+1), next input = cp_embeddings[g][token];
+ *   writes out_tokens[0] = *g0, out_tokens[1..n_groups] = the selected ids, and
+ *   out_combined (bf16 [1024]) = bf16 running sum of bb_embedding[g0] and the n_groups
+ *   code-predictor embeddings, plus text_row (bf16 [1024], may be NULL).
+ *   lm_heads / cp_embeddings: device arrays of n_groups pointers to bf16 [cp_vocab, 1024].
+ *   g0_history_slot: device int or NULL; receives *g0 (the repetition-penalty history).
+ *   If *g0 == eos_id (eos_id >= 0) nothing is computed and *done is set to 1.
+ *   k_cache / v_cache: f32 [num_layers, 8, >= n_groups + 1, 128]. */
+hipError_t qtts_cp_frame(
+    void* workspace, const CPLayerWeights* layer_weights, int num_layers,
+    const void* final_norm_weight, const void* cos_table, const void* sin_table,
+    void* k_cache, void* v_cache, int max_seq_len,
+    const float* bb_hidden, const int* g0, const void* bb_embedding,
+    const void* const* lm_heads, const void* const* cp_embeddings, int n_groups, int cp_vocab,
+    const void* text_row, int* out_tokens, void* out_combined, int* g0_history_slot,
+    int eos_id, int* done, const QttsSampling* sampling, int frame_step, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWENTTS_AMD_H */

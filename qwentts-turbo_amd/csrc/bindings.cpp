@@ -1,0 +1,419 @@
+// PyTorch-ROCm extension: the reference's pybind classes over the C ABI of libqwentts_amd.
+//
+// MegakernelTTSDecoder           -- /root/reference/qwentts_turbo/megakernel_backbone.py:109-332
+// MegakernelCodePredictorDecoder -- /root/reference/qwentts_turbo/megakernel_code_predictor.py:86-242
+//
+// Same constructor arguments, method names and return conventions as the reference (outputs
+// are fresh tensors; KV getters alias the internal caches). Differences: shapes, dtypes,
+// devices and positions are validated (the reference checks nothing), launch errors raise,
+// and extra methods expose the fused head / token-selection / frame entry points.
+#include <torch/extension.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+#include <hip/hip_runtime_api.h>
+#include <cmath>
+#include <vector>
+#include "qwentts_amd.h"
+
+namespace {
+
+constexpr int kHidden = 1024, kKVHeads = 8, kHeadDim = 128, kInter = 3072, kQ = 2048;
+
+hipStream_t cur_stream() { return c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream(); }
+
+void hip_check(hipError_t e, const char* what) {
+  TORCH_CHECK(e == hipSuccess, what, " failed: ", hipGetErrorString(e));
+}
+
+void check_bf16(const torch::Tensor& t, std::vector<int64_t> shape, const char* name) {
+  TORCH_CHECK(t.is_cuda(), name, " must be a GPU tensor");
+  TORCH_CHECK(t.scalar_type() == torch::kBFloat16, name, " must be bfloat16, got ", t.scalar_type());
+  TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
+  TORCH_CHECK(t.sizes().vec() == shape, name, " has shape ", t.sizes(), ", expected ", c10::IntArrayRef(shape));
+}
+
+// Layer weights in the reference's struct order (11 per layer).
+std::vector<TTSLayerWeights> pack_layers(const std::vector<torch::Tensor>& flat, int num_layers) {
+  TORCH_CHECK((int)flat.size() == num_layers * 11, "expected ", num_layers * 11, " layer weights, got ", flat.size());
+  const std::vector<std::vector<int64_t>> shapes = {
+      {kHidden}, {kQ, kHidden}, {kKVHeads * kHeadDim, kHidden}, {kKVHeads * kHeadDim, kHidden},
+      {kHeadDim}, {kHeadDim}, {kHidden, kQ}, {kHidden}, {kInter, kHidden}, {kInter, kHidden}, {kHidden, kInter}};
+  std::vector<TTSLayerWeights> out(num_layers);
+  for (int i = 0; i < num_layers; ++i) {
+    const void** p = reinterpret_cast<const void**>(&out[i]);
+    for (int j = 0; j < 11; ++j) {
+      const auto& t = flat[i * 11 + j];
+      check_bf16(t, shapes[j], "layer weight");
+      TORCH_CHECK((reinterpret_cast<uintptr_t>(t.data_ptr()) & 15u) == 0, "layer weights must be 16-byte aligned");
+      p[j] = t.data_ptr();
+    }
+  }
+  return out;
+}
+
+torch::Tensor upload_struct(const void* data, size_t bytes, const torch::Device& dev) {
+  auto t = torch::empty({(int64_t)bytes}, torch::dtype(torch::kUInt8).device(dev));
+  hip_check(hipMemcpy(t.data_ptr(), data, bytes, hipMemcpyHostToDevice), "hipMemcpy");
+  return t;
+}
+
+torch::Tensor make_workspace(const torch::Device& dev) {
+  auto ws = torch::zeros({(int64_t)qtts_workspace_bytes()}, torch::dtype(torch::kUInt8).device(dev));
+  hip_check(qtts_workspace_init(ws.data_ptr(), dev.index()), "qtts_workspace_init (needs an MI355X: gfx950, 256 CUs)");
+  return ws;
+}
+
+torch::Tensor as_bf16_vec(torch::Tensor e, const torch::Device& dev) {
+  if (e.dim() == 2) e = e.squeeze(0);
+  TORCH_CHECK(e.dim() == 1 && e.size(0) == kHidden, "input embedding must be [1024] or [1, 1024], got ", e.sizes());
+  TORCH_CHECK(e.device() == dev, "input embedding must be on ", dev);
+  return e.to(torch::kBFloat16).contiguous();
+}
+
+QttsSampling sampling(bool do_sample, double temperature, int64_t top_k, double top_p, int64_t seed) {
+  TORCH_CHECK(!do_sample || temperature > 0.0, "temperature must be > 0");
+  QttsSampling s;
+  s.do_sample = do_sample ? 1 : 0;
+  s.temperature = (float)temperature;
+  s.top_k = (int)top_k;
+  s.top_p = (float)top_p;
+  s.seed = (unsigned long long)seed;
+  return s;
+}
+
+void check_device_error(const torch::Tensor& ws) {
+  unsigned int code = 0;
+  hip_check(qtts_workspace_check(ws.data_ptr(), &code, cur_stream()), "qtts_workspace_check");
+  TORCH_CHECK(code == 0, "decode kernel reported a device-side wait timeout (error word ", code, ")");
+}
+
+// ---------------------------------------------------------------------------------------
+class MegakernelTTSDecoder {
+ public:
+  MegakernelTTSDecoder(torch::Tensor embed_weight, std::vector<torch::Tensor> layer_weights_flat,
+                       torch::Tensor final_norm_weight, torch::Tensor codec_head_weight, torch::Tensor cos_table,
+                       torch::Tensor sin_table, int64_t num_layers, int64_t max_seq_len)
+      : num_layers_((int)num_layers), max_seq_len_((int)max_seq_len), dev_(embed_weight.device()) {
+    TORCH_CHECK(num_layers >= 1, "num_layers must be >= 1");
+    TORCH_CHECK(max_seq_len >= 1, "max_seq_len must be >= 1");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(dev_);
+    TORCH_CHECK(embed_weight.dim() == 2 && embed_weight.size(1) == kHidden, "embed_weight must be [vocab, 1024]");
+    check_bf16(embed_weight, {embed_weight.size(0), kHidden}, "embed_weight");
+    check_bf16(codec_head_weight, {codec_head_weight.size(0), kHidden}, "codec_head_weight");
+    check_bf16(final_norm_weight, {kHidden}, "final_norm_weight");
+    TORCH_CHECK(cos_table.size(0) >= max_seq_len && sin_table.size(0) >= max_seq_len, "RoPE tables shorter than max_seq_len");
+    check_bf16(cos_table, {cos_table.size(0), kHeadDim}, "cos_table");
+    check_bf16(sin_table, {sin_table.size(0), kHeadDim}, "sin_table");
+    embed_weight_ = embed_weight;
+    final_norm_weight_ = final_norm_weight;
+    codec_head_weight_ = codec_head_weight;
+    cos_table_ = cos_table;
+    sin_table_ = sin_table;
+    layer_weights_tensors_ = layer_weights_flat;
+    auto host = pack_layers(layer_weights_flat, num_layers_);
+    d_layer_weights_ = upload_struct(host.data(), host.size() * sizeof(TTSLayerWeights), dev_);
+    auto bf = torch::dtype(torch::kBFloat16).device(dev_);
+    auto f32 = torch::dtype(torch::kFloat32).device(dev_);
+    k_cache_ = torch::zeros({num_layers, kKVHeads, max_seq_len, kHeadDim}, bf);
+    v_cache_ = torch::zeros({num_layers, kKVHeads, max_seq_len, kHeadDim}, bf);
+    hidden_buffer_ = torch::zeros({kHidden}, bf);
+    g_normalized_ = torch::zeros({kHidden}, f32);
+    logits_ = torch::zeros({codec_head_weight.size(0)}, f32);
+    token_ = torch::zeros({1}, torch::dtype(torch::kInt32).device(dev_));
+    ws_ = make_workspace(dev_);
+    position_ = 0;
+  }
+
+  torch::Tensor decode_step(int64_t input_token_id) {
+    TORCH_CHECK(input_token_id >= 0 && input_token_id < embed_weight_.size(0), "token id out of range");
+    run(nullptr, (int)input_token_id, nullptr, false, nullptr, 0, 1.0, -1, false, sampling(false, 1.0, 0, 1.0, 0), 0);
+    return g_normalized_.clone();
+  }
+
+  int64_t decode_step_with_argmax(int64_t input_token_id) {
+    TORCH_CHECK(input_token_id >= 0 && input_token_id < embed_weight_.size(0), "token id out of range");
+    run(nullptr, (int)input_token_id, nullptr, true, nullptr, 0, 1.0, -1, false, sampling(false, 1.0, 0, 1.0, 0), 0,
+        /*no_mask=*/true);
+    return token_.item<int>();
+  }
+
+  torch::Tensor decode_step_with_embedding(torch::Tensor input_embedding) {
+    auto e = as_bf16_vec(input_embedding, dev_);
+    run(e.data_ptr(), 0, nullptr, false, nullptr, 0, 1.0, -1, false, sampling(false, 1.0, 0, 1.0, 0), 0);
+    return g_normalized_.clone();
+  }
+
+  // Extended: one step with 3D rotary positions (t, h, w); returns the final hidden.
+  torch::Tensor decode_step_3d(torch::Tensor input_embedding, std::vector<int64_t> pos3) {
+    TORCH_CHECK(pos3.size() == 3, "pos3 must be (t, h, w)");
+    auto e = as_bf16_vec(input_embedding, dev_);
+    int p3[3] = {(int)pos3[0], (int)pos3[1], (int)pos3[2]};
+    run(e.data_ptr(), 0, p3, false, nullptr, 0, 1.0, -1, false, sampling(false, 1.0, 0, 1.0, 0), 0);
+    return g_normalized_.clone();
+  }
+
+  // Extended: step + fused codec head + on-device selection. Writes the token to
+  // out_token (int32 [1] device); keeps hidden / logits in the internal buffers.
+  void decode_step_select(torch::Tensor input_embedding, torch::Tensor out_token, torch::Tensor history,
+                          int64_t n_history, double repetition_penalty, int64_t eos_id, bool suppress_eos,
+                          bool do_sample, double temperature, int64_t top_k, double top_p, int64_t seed,
+                          int64_t frame_step, c10::optional<std::vector<int64_t>> pos3, c10::optional<torch::Tensor> skip_if) {
+    auto e = as_bf16_vec(input_embedding, dev_);
+    TORCH_CHECK(out_token.is_cuda() && out_token.scalar_type() == torch::kInt32 && out_token.numel() >= 1,
+                "out_token must be an int32 GPU tensor");
+    TORCH_CHECK(history.is_cuda() && history.scalar_type() == torch::kInt32 && history.numel() >= n_history,
+                "history must be an int32 GPU tensor with >= n_history entries");
+    int p3[3];
+    int* p3p = nullptr;
+    if (pos3.has_value()) {
+      TORCH_CHECK(pos3->size() == 3, "pos3 must be (t, h, w)");
+      for (int i = 0; i < 3; ++i) p3[i] = (int)(*pos3)[i];
+      p3p = p3;
+    }
+    const int* skip = nullptr;
+    if (skip_if.has_value()) {
+      TORCH_CHECK(skip_if->is_cuda() && skip_if->scalar_type() == torch::kInt32, "skip_if must be an int32 GPU tensor");
+      skip = skip_if->data_ptr<int>();
+    }
+    run(e.data_ptr(), 0, p3p, true, history.data_ptr<int>(), (int)n_history, repetition_penalty, (int)eos_id, suppress_eos,
+        sampling(do_sample, temperature, top_k, top_p, seed), (int)frame_step, false, out_token.data_ptr<int>(), skip);
+  }
+
+  void reset() {
+    position_ = 0;
+    k_cache_.zero_();
+    v_cache_.zero_();
+  }
+  int64_t position() const { return position_; }
+  void set_position(int64_t pos) {
+    TORCH_CHECK(pos >= 0 && pos <= max_seq_len_, "position ", pos, " outside [0, ", max_seq_len_, "]");
+    position_ = (int)pos;
+  }
+  torch::Tensor get_hidden_states() const { return g_normalized_.clone(); }
+  torch::Tensor get_k_cache() const { return k_cache_; }
+  torch::Tensor get_v_cache() const { return v_cache_; }
+  torch::Tensor hidden_state_buffer() const { return g_normalized_; }
+  torch::Tensor residual_buffer() const { return hidden_buffer_; }
+  torch::Tensor logits_buffer() const { return logits_; }
+  void check_error() const { check_device_error(ws_); }
+
+  void set_kv_cache(torch::Tensor k_cache, torch::Tensor v_cache) {
+    TORCH_CHECK(k_cache.dim() == 4 && k_cache.sizes() == v_cache.sizes(), "k/v must be [layers, 8, seq, 128]");
+    TORCH_CHECK(k_cache.size(0) == num_layers_ && k_cache.size(1) == kKVHeads && k_cache.size(3) == kHeadDim,
+                "k/v must be [", num_layers_, ", 8, seq, 128], got ", k_cache.sizes());
+    TORCH_CHECK(k_cache.size(2) <= max_seq_len_, "k/v longer than max_seq_len");
+    using namespace torch::indexing;
+    k_cache_.index_put_({Slice(), Slice(), Slice(0, k_cache.size(2)), Slice()}, k_cache.to(dev_, torch::kBFloat16));
+    v_cache_.index_put_({Slice(), Slice(), Slice(0, v_cache.size(2)), Slice()}, v_cache.to(dev_, torch::kBFloat16));
+  }
+
+ private:
+  void run(const void* emb, int token, const int* pos3, bool with_head, const int* history, int n_history,
+           double rep_penalty, int eos_id, bool suppress_eos, QttsSampling samp, int frame_step, bool no_mask = false,
+           int* out_token = nullptr, const int* skip = nullptr) {
+    TORCH_CHECK(position_ < max_seq_len_, "position ", position_, " >= max_seq_len ", max_seq_len_, " (KV cache full)");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(dev_);
+    const int vocab = (int)codec_head_weight_.size(0);
+    int* tok = out_token ? out_token : token_.data_ptr<int>();
+    hipError_t e = qtts_backbone_step(
+        ws_.data_ptr(), reinterpret_cast<const TTSLayerWeights*>(d_layer_weights_.data_ptr()), num_layers_,
+        final_norm_weight_.data_ptr(), cos_table_.data_ptr(), sin_table_.data_ptr(), k_cache_.data_ptr(),
+        v_cache_.data_ptr(), max_seq_len_, position_, pos3, emb, emb ? nullptr : embed_weight_.data_ptr(), token,
+        g_normalized_.data_ptr<float>(), hidden_buffer_.data_ptr(), with_head ? codec_head_weight_.data_ptr() : nullptr,
+        vocab, with_head ? logits_.data_ptr<float>() : nullptr, with_head ? tok : nullptr, no_mask ? 0 : 1, history,
+        n_history, (float)rep_penalty, eos_id, suppress_eos ? 1 : 0, &samp, frame_step, skip,
+        cur_stream());
+    hip_check(e, "qtts_backbone_step");
+    position_++;
+  }
+
+  int num_layers_, max_seq_len_, position_;
+  torch::Device dev_;
+  torch::Tensor embed_weight_, final_norm_weight_, codec_head_weight_, cos_table_, sin_table_, d_layer_weights_;
+  std::vector<torch::Tensor> layer_weights_tensors_;
+  torch::Tensor k_cache_, v_cache_, hidden_buffer_, g_normalized_, logits_, token_, ws_;
+};
+
+// ---------------------------------------------------------------------------------------
+class MegakernelCodePredictorDecoder {
+ public:
+  MegakernelCodePredictorDecoder(std::vector<torch::Tensor> layer_weights_flat, torch::Tensor final_norm_weight,
+                                 torch::Tensor cos_table, torch::Tensor sin_table, int64_t num_layers,
+                                 int64_t max_seq_len)
+      : num_layers_((int)num_layers), max_seq_len_((int)max_seq_len), dev_(final_norm_weight.device()) {
+    TORCH_CHECK(num_layers >= 1 && max_seq_len >= 1, "num_layers and max_seq_len must be >= 1");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(dev_);
+    check_bf16(final_norm_weight, {kHidden}, "final_norm_weight");
+    TORCH_CHECK(cos_table.size(0) >= max_seq_len && sin_table.size(0) >= max_seq_len, "RoPE tables shorter than max_seq_len");
+    check_bf16(cos_table, {cos_table.size(0), kHeadDim}, "cos_table");
+    check_bf16(sin_table, {sin_table.size(0), kHeadDim}, "sin_table");
+    final_norm_weight_ = final_norm_weight;
+    cos_table_ = cos_table;
+    sin_table_ = sin_table;
+    layer_weights_tensors_ = layer_weights_flat;
+    auto host = pack_layers(layer_weights_flat, num_layers_);
+    d_layer_weights_ = upload_struct(host.data(), host.size() * sizeof(TTSLayerWeights), dev_);
+    auto f32 = torch::dtype(torch::kFloat32).device(dev_);
+    k_cache_ = torch::zeros({num_layers, kKVHeads, max_seq_len, kHeadDim}, f32);
+    v_cache_ = torch::zeros({num_layers, kKVHeads, max_seq_len, kHeadDim}, f32);
+    hidden_buffer_ = torch::zeros({kHidden}, f32);
+    g_normalized_ = torch::zeros({kHidden}, f32);
+    ws_ = make_workspace(dev_);
+    position_ = 0;
+  }
+
+  torch::Tensor decode_step_with_embedding(torch::Tensor input_embedding) {
+    TORCH_CHECK(position_ < max_seq_len_, "position ", position_, " >= max_seq_len ", max_seq_len_, " (KV cache full)");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(dev_);
+    auto e = as_bf16_vec(input_embedding, dev_);
+    hip_check(qtts_cp_step(ws_.data_ptr(), reinterpret_cast<const CPLayerWeights*>(d_layer_weights_.data_ptr()),
+                           num_layers_, final_norm_weight_.data_ptr(), cos_table_.data_ptr(), sin_table_.data_ptr(),
+                           k_cache_.data_ptr(), v_cache_.data_ptr(), max_seq_len_, position_, e.data_ptr(),
+                           g_normalized_.data_ptr<float>(), hidden_buffer_.data_ptr<float>(),
+                           cur_stream()),
+              "qtts_cp_step");
+    position_++;
+    return g_normalized_.clone();
+  }
+
+  // Extended: bind the 15 lm-heads, the 15 codebook embedding tables and the backbone codec
+  // embedding used by frame().
+  void set_heads(std::vector<torch::Tensor> lm_heads, std::vector<torch::Tensor> embeddings, torch::Tensor bb_embedding) {
+    TORCH_CHECK(!lm_heads.empty() && lm_heads.size() == embeddings.size(), "need as many lm-heads as embedding tables");
+    const int64_t v = lm_heads[0].size(0);
+    std::vector<const void*> hp, ep;
+    for (size_t g = 0; g < lm_heads.size(); ++g) {
+      check_bf16(lm_heads[g], {v, kHidden}, "lm_head");
+      check_bf16(embeddings[g], {embeddings[g].size(0), kHidden}, "codec embedding");
+      TORCH_CHECK(embeddings[g].size(0) >= v, "codec embedding ", g, " has fewer rows than the lm-head vocabulary");
+      hp.push_back(lm_heads[g].data_ptr());
+      ep.push_back(embeddings[g].data_ptr());
+    }
+    check_bf16(bb_embedding, {bb_embedding.size(0), kHidden}, "backbone codec embedding");
+    bb_vocab_ = bb_embedding.size(0);
+    heads_ = lm_heads;
+    embs_ = embeddings;
+    bb_emb_ = bb_embedding;
+    cp_vocab_ = (int)v;
+    d_heads_ = upload_struct(hp.data(), hp.size() * sizeof(void*), dev_);
+    d_embs_ = upload_struct(ep.data(), ep.size() * sizeof(void*), dev_);
+  }
+
+  // Extended: one whole frame (2-token prefill + 14 decode steps + 15 heads + combine).
+  void frame(torch::Tensor bb_hidden, torch::Tensor g0, c10::optional<torch::Tensor> text_row, torch::Tensor out_tokens,
+             torch::Tensor out_combined, int64_t eos_id, torch::Tensor done, bool do_sample, double temperature,
+             int64_t top_k, double top_p, int64_t seed, int64_t frame_step, c10::optional<torch::Tensor> history_slot) {
+    TORCH_CHECK(!heads_.empty(), "call set_heads() before frame()");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(dev_);
+    TORCH_CHECK(bb_hidden.is_cuda() && bb_hidden.scalar_type() == torch::kFloat32 && bb_hidden.numel() == kHidden &&
+                    bb_hidden.is_contiguous(), "bb_hidden must be a contiguous f32 GPU tensor of 1024 values");
+    TORCH_CHECK(g0.is_cuda() && g0.scalar_type() == torch::kInt32, "g0 must be an int32 GPU tensor");
+    TORCH_CHECK(out_tokens.is_cuda() && out_tokens.scalar_type() == torch::kInt32 &&
+                    out_tokens.numel() >= (int64_t)heads_.size() + 1, "out_tokens must be int32 GPU with >= groups+1 entries");
+    TORCH_CHECK(out_combined.is_cuda() && out_combined.scalar_type() == torch::kBFloat16 && out_combined.numel() == kHidden,
+                "out_combined must be a bf16 GPU tensor of 1024 values");
+    TORCH_CHECK(done.is_cuda() && done.scalar_type() == torch::kInt32, "done must be an int32 GPU tensor");
+    TORCH_CHECK((int)heads_.size() + 1 <= max_seq_len_, "max_seq_len too small for a frame");
+    const void* tr = nullptr;
+    if (text_row.has_value()) {
+      TORCH_CHECK(text_row->is_cuda() && text_row->scalar_type() == torch::kBFloat16 && text_row->numel() == kHidden &&
+                      text_row->is_contiguous(), "text_row must be a contiguous bf16 GPU tensor of 1024 values");
+      tr = text_row->data_ptr();
+    }
+    int* hs = nullptr;
+    if (history_slot.has_value()) {
+      TORCH_CHECK(history_slot->is_cuda() && history_slot->scalar_type() == torch::kInt32 && history_slot->numel() >= 1,
+                  "history_slot must be an int32 GPU tensor");
+      hs = history_slot->data_ptr<int>();
+    }
+    QttsSampling s = sampling(do_sample, temperature, top_k, top_p, seed);
+    hip_check(qtts_cp_frame(ws_.data_ptr(), reinterpret_cast<const CPLayerWeights*>(d_layer_weights_.data_ptr()),
+                            num_layers_, final_norm_weight_.data_ptr(), cos_table_.data_ptr(), sin_table_.data_ptr(),
+                            k_cache_.data_ptr(), v_cache_.data_ptr(), max_seq_len_, bb_hidden.data_ptr<float>(),
+                            g0.data_ptr<int>(), bb_emb_.data_ptr(), reinterpret_cast<const void* const*>(d_heads_.data_ptr()),
+                            reinterpret_cast<const void* const*>(d_embs_.data_ptr()), (int)heads_.size(), cp_vocab_, tr,
+                            out_tokens.data_ptr<int>(), out_combined.data_ptr(), hs, (int)eos_id, done.data_ptr<int>(), &s,
+                            (int)frame_step, cur_stream()),
+              "qtts_cp_frame");
+  }
+
+  void reset() {
+    position_ = 0;
+    k_cache_.zero_();
+    v_cache_.zero_();
+  }
+  int64_t position() const { return position_; }
+  void set_position(int64_t pos) {
+    TORCH_CHECK(pos >= 0 && pos <= max_seq_len_, "position ", pos, " outside [0, ", max_seq_len_, "]");
+    position_ = (int)pos;
+  }
+  torch::Tensor get_hidden_states() const { return g_normalized_.clone(); }
+  torch::Tensor get_k_cache() const { return k_cache_; }
+  torch::Tensor get_v_cache() const { return v_cache_; }
+  void check_error() const { check_device_error(ws_); }
+
+  void set_kv_cache(torch::Tensor k_cache, torch::Tensor v_cache) {
+    TORCH_CHECK(k_cache.dim() == 4 && k_cache.sizes() == v_cache.sizes(), "k/v must be [layers, 8, seq, 128]");
+    TORCH_CHECK(k_cache.size(0) == num_layers_ && k_cache.size(1) == kKVHeads && k_cache.size(3) == kHeadDim,
+                "k/v must be [", num_layers_, ", 8, seq, 128], got ", k_cache.sizes());
+    TORCH_CHECK(k_cache.size(2) <= max_seq_len_, "k/v longer than max_seq_len");
+    using namespace torch::indexing;
+    k_cache_.index_put_({Slice(), Slice(), Slice(0, k_cache.size(2)), Slice()}, k_cache.to(dev_, torch::kFloat32));
+    v_cache_.index_put_({Slice(), Slice(), Slice(0, v_cache.size(2)), Slice()}, v_cache.to(dev_, torch::kFloat32));
+  }
+
+ private:
+  int num_layers_, max_seq_len_, position_, cp_vocab_ = 0;
+  int64_t bb_vocab_ = 0;
+  torch::Device dev_;
+  torch::Tensor final_norm_weight_, cos_table_, sin_table_, d_layer_weights_;
+  std::vector<torch::Tensor> layer_weights_tensors_, heads_, embs_;
+  torch::Tensor bb_emb_, d_heads_, d_embs_;
+  torch::Tensor k_cache_, v_cache_, hidden_buffer_, g_normalized_, ws_;
+};
+
+}  // namespace
+
+PYBIND11_MODULE(_qwentts_amd_C, m) {
+  m.doc() = "MI355X decode kernels for Qwen3-TTS (backbone + code predictor)";
+  m.def("workspace_bytes", []() { return (int64_t)qtts_workspace_bytes(); });
+  py::class_<MegakernelTTSDecoder>(m, "MegakernelTTSDecoder")
+      .def(py::init<torch::Tensor, std::vector<torch::Tensor>, torch::Tensor, torch::Tensor, torch::Tensor, torch::Tensor,
+                    int64_t, int64_t>())
+      .def("decode_step", &MegakernelTTSDecoder::decode_step)
+      .def("decode_step_with_argmax", &MegakernelTTSDecoder::decode_step_with_argmax)
+      .def("decode_step_with_embedding", &MegakernelTTSDecoder::decode_step_with_embedding)
+      .def("decode_step_3d", &MegakernelTTSDecoder::decode_step_3d)
+      .def("decode_step_select", &MegakernelTTSDecoder::decode_step_select, py::arg("input_embedding"),
+           py::arg("out_token"), py::arg("history"), py::arg("n_history"), py::arg("repetition_penalty"),
+           py::arg("eos_id"), py::arg("suppress_eos"), py::arg("do_sample"), py::arg("temperature"), py::arg("top_k"),
+           py::arg("top_p"), py::arg("seed"), py::arg("frame_step"), py::arg("pos3") = py::none(),
+           py::arg("skip_if") = py::none())
+      .def("reset", &MegakernelTTSDecoder::reset)
+      .def("position", &MegakernelTTSDecoder::position)
+      .def("set_position", &MegakernelTTSDecoder::set_position)
+      .def("get_hidden_states", &MegakernelTTSDecoder::get_hidden_states)
+      .def("get_k_cache", &MegakernelTTSDecoder::get_k_cache)
+      .def("get_v_cache", &MegakernelTTSDecoder::get_v_cache)
+      .def("set_kv_cache", &MegakernelTTSDecoder::set_kv_cache)
+      .def("hidden_state_buffer", &MegakernelTTSDecoder::hidden_state_buffer)
+      .def("residual_buffer", &MegakernelTTSDecoder::residual_buffer)
+      .def("logits_buffer", &MegakernelTTSDecoder::logits_buffer)
+      .def("check_error", &MegakernelTTSDecoder::check_error);
+  py::class_<MegakernelCodePredictorDecoder>(m, "MegakernelCodePredictorDecoder")
+      .def(py::init<std::vector<torch::Tensor>, torch::Tensor, torch::Tensor, torch::Tensor, int64_t, int64_t>())
+      .def("decode_step_with_embedding", &MegakernelCodePredictorDecoder::decode_step_with_embedding)
+      .def("set_heads", &MegakernelCodePredictorDecoder::set_heads)
+      .def("frame", &MegakernelCodePredictorDecoder::frame, py::arg("bb_hidden"), py::arg("g0"), py::arg("text_row"),
+           py::arg("out_tokens"), py::arg("out_combined"), py::arg("eos_id"), py::arg("done"), py::arg("do_sample"),
+           py::arg("temperature"), py::arg("top_k"), py::arg("top_p"), py::arg("seed"), py::arg("frame_step"),
+           py::arg("history_slot") = py::none())
+      .def("reset", &MegakernelCodePredictorDecoder::reset)
+      .def("position", &MegakernelCodePredictorDecoder::position)
+      .def("set_position", &MegakernelCodePredictorDecoder::set_position)
+      .def("get_hidden_states", &MegakernelCodePredictorDecoder::get_hidden_states)
+      .def("get_k_cache", &MegakernelCodePredictorDecoder::get_k_cache)
+      .def("get_v_cache", &MegakernelCodePredictorDecoder::get_v_cache)
+      .def("set_kv_cache", &MegakernelCodePredictorDecoder::set_kv_cache)
+      .def("check_error", &MegakernelCodePredictorDecoder::check_error);
+}

@@ -1,0 +1,179 @@
+// Device-side building blocks shared by the decode kernels (gfx950 / CDNA4, wave64).
+//
+// Terminology:
+//   XCD      one of the 8 accelerator dies of MI355X; each has 32 CUs and its own L2.
+//   slot     an 8-byte exchange word {f32 value, u32 tag}. A producer publishes a value by
+//            storing the word; a consumer polls the word until the tag equals the tag of the
+//            current exchange. The tag travels with the value, so no fence or counter is
+//            needed and a stale word can never be mistaken for a fresh one.
+//   local    exchange between workgroups of one XCD: plain stores land in that XCD's L2 and
+//            sc1 loads read them there (~0.5 us round).
+//   cross    exchange between XCDs: sc1 stores write through to memory and sc1 loads re-read
+//            it (~1.5 us round).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qtts {
+
+constexpr int HID = 1024;         // hidden size
+constexpr int INTER = 3072;       // SwiGLU intermediate size
+constexpr int NQH = 16;           // query heads
+constexpr int NKVH = 8;           // key/value heads
+constexpr int HDIM = 128;         // head dim
+constexpr int NXCD = 8;           // XCDs, one KV head each
+constexpr int WPX = 32;           // workgroups per XCD
+constexpr int NWG = NXCD * WPX;   // grid size (one workgroup per CU)
+constexpr int NMATH = 4;          // math waves per workgroup
+constexpr int NTHR = 64 * (NMATH + 1);  // + 1 poller wave
+constexpr int LROWS = 512;        // q(256) + k(128) + v(128) rows owned by one XCD
+constexpr int XI = INTER / NXCD;  // 384 intermediate rows per XCD
+constexpr int MAXC = 8;           // max attention chunks per KV head
+constexpr int APS = 260;          // attention partial: 2 heads x (m, l, acc[128])
+constexpr int SUBP = 64;          // positions per prefetched attention sub-block
+constexpr int MAXV = 3072;        // max vocabulary of a selection head
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint16_t bf16_t;
+
+// ---------------------------------------------------------------------------------------
+// bf16 helpers (round-to-nearest-even, as torch's f32 -> bf16 cast)
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ float bflo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bfhi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf2f(bf16_t b) { return __uint_as_float((uint32_t)b << 16); }
+__device__ __forceinline__ bf16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (bf16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+
+// 8 bf16 weights (one 16-byte piece) dot 8 activations, accumulated in f64 (each product is
+// exact in f64; only the accumulation rounds, at ~1e-16 relative).
+__device__ __forceinline__ double dot8d(const u32x4 w, const double* x, double acc) {
+  acc = fma((double)bflo(w.x), x[0], acc);
+  acc = fma((double)bfhi(w.x), x[1], acc);
+  acc = fma((double)bflo(w.y), x[2], acc);
+  acc = fma((double)bfhi(w.y), x[3], acc);
+  acc = fma((double)bflo(w.z), x[4], acc);
+  acc = fma((double)bfhi(w.z), x[5], acc);
+  acc = fma((double)bflo(w.w), x[6], acc);
+  acc = fma((double)bfhi(w.w), x[7], acc);
+  return acc;
+}
+
+__device__ __forceinline__ u32x4 ldw(const bf16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ u32x4 ldw_nt(const bf16_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+// ---------------------------------------------------------------------------------------
+// wave64 reductions
+// ---------------------------------------------------------------------------------------
+template <int WIDTH, typename T>
+__device__ __forceinline__ T group_sum(T v) {
+#pragma unroll
+  for (int o = 1; o < WIDTH; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+template <int WIDTH, typename T>
+__device__ __forceinline__ T group_max(T v) {
+#pragma unroll
+  for (int o = 1; o < WIDTH; o <<= 1) { const T u = __shfl_xor(v, o, 64); v = u > v ? u : v; }
+  return v;
+}
+__device__ __forceinline__ double wave_sum_d(double v) { return group_sum<64>(v); }
+
+// ---------------------------------------------------------------------------------------
+// exchange slots
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t slot_pack(float v, uint32_t tag) {
+  return ((uint64_t)tag << 32) | (uint64_t)__float_as_uint(v);
+}
+// XCD-local publish: a plain 8-byte store (lands in the XCD's L2).
+__device__ __forceinline__ void put_local(uint64_t* p, float v, uint32_t tag) {
+  *p = slot_pack(v, tag);
+}
+// cross-XCD publish: write-through to memory (sc1).
+__device__ __forceinline__ void put_cross(uint64_t* p, float v, uint32_t tag) {
+  __hip_atomic_store(p, slot_pack(v, tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+struct ErrCtl {
+  uint32_t* err;
+  uint32_t spin_cap;
+};
+
+__device__ __forceinline__ bool err_set(const ErrCtl& c) {
+  return __hip_atomic_load(c.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+}
+
+// Poll `n` slots (n even, buf 16-byte aligned) until every tag equals `tag`; store the values
+// to dst[0..n). Executed by one wave. 16-byte sc1 buffer loads fetch two slots each; every
+// 8-byte half carries its own tag. Returns false (and latches the error word) on timeout.
+template <int MAXPAIRS_PER_LANE>
+__device__ bool poll_slots(const uint64_t* buf, int n, uint32_t tag, float* dst, const ErrCtl& c) {
+  const int lane = threadIdx.x & 63;
+  const int npair = n >> 1;
+  __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(buf), (short)0, n * 8, 0x00020000);
+  uint32_t pending = 0;
+#pragma unroll
+  for (int k = 0; k < MAXPAIRS_PER_LANE; ++k)
+    if (lane + 64 * k < npair) pending |= 1u << k;
+  uint32_t spins = 0;
+  for (;;) {
+    u32x4 v[MAXPAIRS_PER_LANE];
+#pragma unroll
+    for (int k = 0; k < MAXPAIRS_PER_LANE; ++k)
+      if (pending & (1u << k)) v[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, (lane + 64 * k) * 16, 0, 16);
+#pragma unroll
+    for (int k = 0; k < MAXPAIRS_PER_LANE; ++k) {
+      if ((pending & (1u << k)) && v[k].y == tag && v[k].w == tag) {
+        const int i = (lane + 64 * k) * 2;
+        dst[i] = __uint_as_float(v[k].x);
+        dst[i + 1] = __uint_as_float(v[k].z);
+        pending &= ~(1u << k);
+      }
+    }
+    if (__ballot(pending != 0u) == 0ull) return true;
+    ++spins;
+    if ((spins & 63u) == 0u && (spins > c.spin_cap || err_set(c))) {
+      if (lane == 0) atomicOr(c.err, 1u);
+      return false;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Philox-4x64-10 (Salmon et al., SC'11) and the sampler's uniform draw.
+// Stream layout: key = (seed, "QTTSAFMP"), counter = (vocab_id / 4, frame_step, group, 0),
+// word = vocab_id % 4, u = ((word >> 11) + 0.5) * 2^-53.
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ void philox4x64_10(uint64_t c[4], uint64_t k0, uint64_t k1) {
+  const uint64_t M0 = 0xD2E7470EE14C6C93ull, M1 = 0xCA5A826395121157ull;
+  const uint64_t W0 = 0x9E3779B97F4A7C15ull, W1 = 0xBB67AE8584CAA73Bull;
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    if (r) { k0 += W0; k1 += W1; }
+    const uint64_t lo0 = M0 * c[0], hi0 = __umul64hi(M0, c[0]);
+    const uint64_t lo1 = M1 * c[2], hi1 = __umul64hi(M1, c[2]);
+    const uint64_t n0 = hi1 ^ c[1] ^ k0, n2 = hi0 ^ c[3] ^ k1;
+    c[0] = n0; c[1] = lo1; c[2] = n2; c[3] = lo0;
+  }
+}
+__device__ __forceinline__ double sampler_uniform(uint64_t seed, int frame_step, int group, int vid) {
+  uint64_t c[4] = {(uint64_t)(vid >> 2), (uint64_t)(uint32_t)frame_step, (uint64_t)(uint32_t)group, 0ull};
+  philox4x64_10(c, seed, 0x5154545341464D50ull);
+  return ((double)(c[vid & 3] >> 11) + 0.5) * (1.0 / 9007199254740992.0);
+}
+
+// Order-preserving map float -> uint32 (larger float, larger key).
+__device__ __forceinline__ uint32_t fkey(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+}  // namespace qtts

@@ -1,0 +1,1231 @@
+// Persistent decode kernels for Qwen3-TTS on MI355X (gfx950).
+//
+// Semantics follow the reference megakernels:
+//   backbone:       /root/reference/qwentts_turbo/csrc/fused_decode_tts.cu:728-831
+//   code predictor: /root/reference/qwentts_turbo/csrc/fused_decode_code_predictor.cu:565-668
+// with the interleaved 3D mRoPE of rope_multimodal.cuh:9-54 (t, h, w may differ) and the
+// frame glue of generator.py:116-174, 178-207, 309-362 moved on-device.
+//
+// Work decomposition (one cooperative launch of 256 workgroups, one per CU):
+//   * Tensor-parallel over the 8 XCDs. XCD x owns KV head x with query heads 2x, 2x+1
+//     (512 rows of Wq|Wk|Wv), intermediate rows [384x, 384x+384) of Wgate/Wup, and the
+//     matching column slices of Wo ([:, 256x:256x+256]) and Wdown ([:, 384x:384x+384]).
+//     Each XCD therefore produces a partial of the O and down projections; two cross-XCD
+//     reductions per layer sum them (every XCD adds the 8 partials in the same order, so all
+//     XCDs hold bit-identical activations).
+//   * Inside an XCD the 32 workgroups split rows evenly: 16 QKV rows, 32 O rows, 12 gate +
+//     12 up rows, 32 down rows each, so every weight byte is read exactly once per step.
+//   * Attention of the XCD's KV head is split over C sequence chunks (one per workgroup);
+//     the chunk partials (m, l, acc) are merged by every O-projection workgroup.
+//   * Each workgroup = 4 math waves + 1 poller wave. Math waves hold their weight slices in
+//     VGPRs, prefetched two stages ahead, and run the GEMVs and attention. The poller wave
+//     waits for the inputs of the next stage (tagged exchange slots, see qtts_common.h),
+//     applies the vector work (RMSNorm, q/k-norm + RoPE, KV write, split-K merge, the
+//     cross-XCD sums + residuals, token selection) and leaves ready operands in LDS. Keeping
+//     the polls on their own wave keeps them out of the math waves' in-order load queue.
+#include <hip/hip_runtime.h>
+#include <cstring>
+#include <mutex>
+#include <unordered_map>
+#include "qtts_common.h"
+#include "qtts_select.h"
+#include "qwentts_amd.h"
+
+namespace qtts {
+
+// ---------------------------------------------------------------------------------------
+// Workspace (device): exchange slots, double-buffered by layer-pass parity.
+// ---------------------------------------------------------------------------------------
+struct Workspace {
+  uint64_t qkv[NXCD][2][LROWS];
+  uint64_t attp[NXCD][2][MAXC * APS];
+  uint64_t h1[NXCD][2][HID];
+  uint64_t inter[NXCD][2][XI];
+  uint64_t xl[NXCD][2][HID];
+  uint64_t opart[2][NXCD][HID];
+  uint64_t dpart[2][NXCD][HID];
+  uint64_t logits[2][MAXV];
+  uint32_t err;
+  uint32_t pad[63];
+};
+
+enum TagSlot { T_QKV = 0, T_ATT, T_OPART, T_H1, T_INTER, T_DPART, T_XL, T_NSLOT = 8 };
+constexpr uint32_t TAG_HEAD = 3584;   // head logits tags: TAG_HEAD + position index
+constexpr int MAX_LAYER_PASSES = 440; // layer passes per launch: 8 * 440 < TAG_HEAD
+
+// Per-launch arguments (passed by value).
+struct KArgs {
+  const TTSLayerWeights* layers;
+  int num_layers;
+  const bf16_t* final_norm;
+  const bf16_t* cos_t;
+  const bf16_t* sin_t;
+  void* kc;
+  void* vc;
+  int max_seq;
+  float scale;
+  Workspace* ws;
+  uint32_t tag_base;
+  uint32_t spin_cap;
+  int pos0;        // cache slot of the first position
+  int n_pos;       // positions processed by this launch
+  int pos3[3];     // rotary (t, h, w) of a single backbone position
+  const bf16_t* in_emb;    // bf16 [1024] input of the first position
+  const bf16_t* embed_w;   // token-id gather when in_emb == nullptr
+  int in_tok;
+  float* out_hidden;       // f32 [1024] final-norm hidden
+  void* out_residual;      // bf16 (backbone) / f32 (CP) [1024], may be null
+  // backbone codec head + selection
+  const bf16_t* head;
+  int vocab;
+  float* out_logits;
+  int* out_token;
+  int mask_tail;
+  const int* history;
+  int n_history;
+  float rep_penalty;
+  int eos_id;
+  int suppress_eos;
+  const int* skip;
+  // code-predictor frame
+  int cp_frame;
+  const float* bb_hidden;
+  const int* g0;
+  const bf16_t* bb_emb;
+  const bf16_t* const* cp_heads;
+  const bf16_t* const* cp_embs;
+  int n_groups;
+  int cp_vocab;
+  const bf16_t* text_row;
+  int* out_tokens;
+  int* hist_slot;
+  bf16_t* out_combined;
+  int* done;
+  SelParams sel;
+};
+
+// LDS of one workgroup.
+struct Lds {
+  float xres[HID];
+  float xn[HID];
+  float h1res[HID];
+  float hn[HID];
+  float q[2][HDIM];
+  float knew[HDIM];
+  float vnew[HDIM];
+  float attn[2 * HDIM];
+  float inter[XI];
+  float hb[HID];
+  float stage[MAXC * APS > MAXV ? MAXC * APS : MAXV];
+  double red[NMATH][2][HDIM + 4];
+  SelScratch sel;
+  uint32_t pen_bits[MAXV / 32];
+  int tok[32];
+  uint32_t mbar;          // math-wave barrier counter
+};
+
+// ---------------------------------------------------------------------------------------
+// Math-wave register tiles
+// ---------------------------------------------------------------------------------------
+struct TileQKV { u32x4 p[8]; };
+struct TileO { u32x4 p[4]; };
+struct TileGU { u32x4 g[6]; u32x4 u[6]; };
+struct TileD { u32x4 p[6]; };
+struct TileKV { u32x4 k[4]; u32x4 v[4]; };
+
+enum { W_LNIN = 0, W_Q, W_K, W_V, W_QN, W_KN, W_O, W_LNPOST, W_GATE, W_UP, W_DOWN };
+__device__ __forceinline__ const bf16_t* lw(const TTSLayerWeights* layers, int layer, int i) {
+  const void* const* p = reinterpret_cast<const void* const*>(layers + layer);
+  return reinterpret_cast<const bf16_t*>(p[i]);
+}
+
+// KV geometry. bf16 cache (backbone): a position is 16 pieces of 8 dims; per wave 16
+// positions = 4 steps (jj) of 4 positions (one per 16-lane group). f32 cache (code predictor):
+// a position is 32 pieces of 4 dims; per wave 8 positions = 2 steps of 4 positions, each
+// lane holding 2 pieces (8 dims) per position.
+template <bool BB> struct KVGeo;
+template <> struct KVGeo<true> { static constexpr int JJ = 4, PPP = 1, SUB = 64; };
+template <> struct KVGeo<false> { static constexpr int JJ = 2, PPP = 2, SUB = 32; };
+
+template <bool BB>
+__device__ __forceinline__ void chunking(int L, int& C, int& P) {
+  constexpr int SUB = KVGeo<BB>::SUB;
+  int c0 = (L + SUB - 1) / SUB;
+  if (c0 > MAXC) c0 = MAXC;
+  if (c0 < 1) c0 = 1;
+  P = (L + c0 - 1) / c0;
+  C = (L + P - 1) / P;
+}
+
+template <bool BB>
+__device__ __forceinline__ u32x4 wload(const bf16_t* p) {
+  if constexpr (BB) return ldw_nt(p); else return ldw(p);
+}
+
+template <bool BB>
+__device__ __forceinline__ void load_qkv(TileQKV& t, const TTSLayerWeights* L, int layer, int xcd, int li, int mw, int lane) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int lr = 16 * li + 4 * mw + r;   // local row of the XCD's 512
+    const bf16_t* row;
+    if (lr < 256) row = lw(L, layer, W_Q) + (size_t)(256 * xcd + lr) * HID;
+    else if (lr < 384) row = lw(L, layer, W_K) + (size_t)(128 * xcd + lr - 256) * HID;
+    else row = lw(L, layer, W_V) + (size_t)(128 * xcd + lr - 384) * HID;
+    t.p[2 * r] = wload<BB>(row + 8 * lane);
+    t.p[2 * r + 1] = wload<BB>(row + 512 + 8 * lane);
+  }
+}
+template <bool BB>
+__device__ __forceinline__ void load_o(TileO& t, const TTSLayerWeights* L, int layer, int xcd, int li, int mw, int lane) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = 32 * li + 8 * mw + 2 * j + (lane >> 5);
+    t.p[j] = wload<BB>(lw(L, layer, W_O) + (size_t)row * (NQH * HDIM) + 256 * xcd + 8 * (lane & 31));
+  }
+}
+template <bool BB>
+__device__ __forceinline__ void load_gu(TileGU& t, const TTSLayerWeights* L, int layer, int xcd, int li, int mw, int lane) {
+#pragma unroll
+  for (int r = 0; r < 3; ++r) {
+    const size_t row = (size_t)(XI * xcd + 12 * li + 3 * mw + r) * HID;
+    t.g[2 * r] = wload<BB>(lw(L, layer, W_GATE) + row + 8 * lane);
+    t.g[2 * r + 1] = wload<BB>(lw(L, layer, W_GATE) + row + 512 + 8 * lane);
+    t.u[2 * r] = wload<BB>(lw(L, layer, W_UP) + row + 8 * lane);
+    t.u[2 * r + 1] = wload<BB>(lw(L, layer, W_UP) + row + 512 + 8 * lane);
+  }
+}
+template <bool BB>
+__device__ __forceinline__ void load_d(TileD& t, const TTSLayerWeights* L, int layer, int xcd, int li, int mw, int lane) {
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const int row = 32 * li + 8 * mw + 4 * g + (lane >> 4);
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+      t.p[3 * g + j] = wload<BB>(lw(L, layer, W_DOWN) + (size_t)row * INTER + XI * xcd + 8 * ((lane & 15) + 16 * j));
+  }
+}
+// rows [row0 + 0 .. nrows) of a [*, 1024] head, nrows <= 3 per wave (into the QKV tile's registers)
+template <bool BB>
+__device__ __forceinline__ void load_head(TileQKV& t, const bf16_t* W, int row0, int nrows, int lane) {
+#pragma unroll
+  for (int r = 0; r < 3; ++r) {
+    if (r < nrows) {
+      t.p[2 * r] = wload<BB>(W + (size_t)(row0 + r) * HID + 8 * lane);
+      t.p[2 * r + 1] = wload<BB>(W + (size_t)(row0 + r) * HID + 512 + 8 * lane);
+    }
+  }
+}
+
+// KV sub-block [b0, b0 + SUB) of the chunk, restricted to old positions (< min(bend, Lold)).
+template <bool BB>
+__device__ __forceinline__ void load_kv(TileKV& t, const KArgs& a, int layer, int kvh, int b0, int lim, int mw, int lane) {
+  constexpr int JJ = KVGeo<BB>::JJ, PPP = KVGeo<BB>::PPP;
+  const size_t head_base = ((size_t)layer * NKVH + kvh) * (size_t)a.max_seq;
+#pragma unroll
+  for (int jj = 0; jj < JJ; ++jj) {
+    const int pos0_ = b0 + 4 * JJ * mw + 4 * jj + (lane >> 4);
+    const bool ok = pos0_ < lim;
+    const int pos = ok ? pos0_ : 0;   // every address stays inside the cache
+#pragma unroll
+    for (int pp = 0; pp < PPP; ++pp) {
+      if constexpr (BB) {
+        const size_t off = (head_base + (size_t)pos) * HDIM + 8 * (lane & 15);
+        t.k[jj] = ok ? ldw(reinterpret_cast<const bf16_t*>(a.kc) + off) : u32x4{0, 0, 0, 0};
+        t.v[jj] = ok ? ldw(reinterpret_cast<const bf16_t*>(a.vc) + off) : u32x4{0, 0, 0, 0};
+      } else {
+        const size_t off = (head_base + (size_t)pos) * HDIM + 8 * (lane & 15) + 4 * pp;
+        t.k[PPP * jj + pp] = ok ? *reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(a.kc) + off) : u32x4{0, 0, 0, 0};
+        t.v[PPP * jj + pp] = ok ? *reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(a.vc) + off) : u32x4{0, 0, 0, 0};
+      }
+    }
+  }
+}
+template <bool BB>
+__device__ __forceinline__ void unpack8(const TileKV& t, bool key, int jj, float* o) {
+  if constexpr (BB) {
+    const u32x4 w = key ? t.k[jj] : t.v[jj];
+    o[0] = bflo(w.x); o[1] = bfhi(w.x); o[2] = bflo(w.y); o[3] = bfhi(w.y);
+    o[4] = bflo(w.z); o[5] = bfhi(w.z); o[6] = bflo(w.w); o[7] = bfhi(w.w);
+  } else {
+    const u32x4 w0 = key ? t.k[2 * jj] : t.v[2 * jj];
+    const u32x4 w1 = key ? t.k[2 * jj + 1] : t.v[2 * jj + 1];
+    o[0] = __uint_as_float(w0.x); o[1] = __uint_as_float(w0.y); o[2] = __uint_as_float(w0.z); o[3] = __uint_as_float(w0.w);
+    o[4] = __uint_as_float(w1.x); o[5] = __uint_as_float(w1.y); o[6] = __uint_as_float(w1.z); o[7] = __uint_as_float(w1.w);
+  }
+}
+
+// Barrier among the 4 math waves only (the poller wave keeps running). Bounded: after ~2^24
+// sleeps the wait is abandoned and the error word latched.
+__device__ __forceinline__ void math_barrier(Lds& s, uint32_t& gen, uint32_t* err) {
+  gen += NMATH;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  if ((threadIdx.x & 63) == 0) atomicAdd(&s.mbar, 1u);
+  uint32_t n = 0;
+  while (__hip_atomic_load(&s.mbar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < gen) {
+    __builtin_amdgcn_s_sleep(1);
+    if (++n > (1u << 24)) {
+      if ((threadIdx.x & 63) == 0) atomicOr(err, 2u);
+      break;
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// ---------------------------------------------------------------------------------------
+// Poller helpers
+// ---------------------------------------------------------------------------------------
+struct Poll {
+  __amdgpu_buffer_rsrc_t rs;   // covers the whole workspace
+  const Workspace* base;
+  ErrCtl ec;
+};
+
+__device__ __forceinline__ uint32_t ws_off(const Poll& P, const void* p) {
+  return (uint32_t)(reinterpret_cast<const char*>(p) - reinterpret_cast<const char*>(P.base));
+}
+
+// Poll npair 16-byte pairs; pair i lives at byte offset off(i) of the workspace.
+template <int MAXP, typename OffF>
+__device__ bool poll_pairs(const Poll& P, int npair, uint32_t tag, float* dst, OffF off) {
+  const int lane = threadIdx.x & 63;
+  uint32_t pending = 0;
+#pragma unroll
+  for (int k = 0; k < MAXP; ++k)
+    if (lane + 64 * k < npair) pending |= 1u << k;
+  uint32_t spins = 0;
+  for (;;) {
+    u32x4 v[MAXP];
+#pragma unroll
+    for (int k = 0; k < MAXP; ++k)
+      if (pending & (1u << k)) v[k] = __builtin_amdgcn_raw_buffer_load_b128(P.rs, off(lane + 64 * k), 0, 16);
+#pragma unroll
+    for (int k = 0; k < MAXP; ++k) {
+      if ((pending & (1u << k)) && v[k].y == tag && v[k].w == tag) {
+        const int i = 2 * (lane + 64 * k);
+        dst[i] = __uint_as_float(v[k].x);
+        dst[i + 1] = __uint_as_float(v[k].z);
+        pending &= ~(1u << k);
+      }
+    }
+    if (__ballot(pending != 0u) == 0ull) return true;
+    ++spins;
+    if ((spins & 63u) == 0u && (spins > P.ec.spin_cap || err_set(P.ec))) {
+      if (lane == 0) atomicOr(P.ec.err, 1u);
+      return false;
+    }
+  }
+}
+// contiguous n slots (n even) starting at p
+template <int MAXP>
+__device__ __forceinline__ bool poll_vec(const Poll& P, const uint64_t* p, int n, uint32_t tag, float* dst) {
+  const uint32_t o = ws_off(P, p);
+  return poll_pairs<MAXP>(P, n >> 1, tag, dst, [o](int i) { return o + 16u * (uint32_t)i; });
+}
+// the 8 XCD partials of rows [r0, r0 + 32): dst[32 x + r]
+__device__ __forceinline__ bool poll_parts(const Poll& P, const uint64_t (*part)[HID], int r0, uint32_t tag, float* dst) {
+  const uint32_t o = ws_off(P, &part[0][r0]);
+  return poll_pairs<2>(P, 128, tag, dst, [o](int i) { return o + (uint32_t)(i >> 4) * (HID * 8u) + 16u * (uint32_t)(i & 15); });
+}
+
+// RMSNorm epsilon: the f32 constant 1e-6f of the reference, used in f64 arithmetic.
+constexpr double EPSD = (double)1e-6f;
+
+// one-wave RMSNorm statistic of v[0..1024): 1 / sqrt(mean(v^2) + eps), in f64
+__device__ __forceinline__ double wave_rstd(const float* v) {
+  const int lane = threadIdx.x & 63;
+  double ss = 0.0;
+#pragma unroll
+  for (int j = 0; j < HID / 64; ++j) { const double x = (double)v[lane + 64 * j]; ss = fma(x, x, ss); }
+  ss = group_sum<64>(ss);
+  return 1.0 / sqrt(ss / (double)HID + EPSD);
+}
+// normalized value (x * rstd) * gain, computed in f64 and stored as f32
+__device__ __forceinline__ float norm_f32(float x, double rstd, bf16_t g) {
+  return (float)(((double)x * rstd) * (double)bf2f(g));
+}
+
+// Workgroup barrier at a step boundary: makes the LDS operands one role wrote visible to the
+// other role. Both roles reach it the same number of times (see the step walker).
+__device__ __forceinline__ void step_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// ---------------------------------------------------------------------------------------
+// The kernel
+// ---------------------------------------------------------------------------------------
+template <bool BB>
+__global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
+  __shared__ Lds s;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const bool poller = wave == NMATH;
+  const int mw = __builtin_amdgcn_readfirstlane(wave);   // wave-uniform: row bases stay in SGPRs
+  const int xcd = (int)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15u);  // HW_REG_XCC_ID
+  const int li = blockIdx.x >> 3;
+  const int wg = blockIdx.x;
+  Workspace* ws = a.ws;
+
+  if (a.skip != nullptr && *a.skip != 0) return;
+  int g0 = 0;
+  if (a.cp_frame) {
+    g0 = *a.g0;
+    if (a.eos_id >= 0 && g0 == a.eos_id) {
+      if (wg == 0 && threadIdx.x == 0) *a.done = 1;
+      return;
+    }
+  }
+  if (threadIdx.x == 0) s.mbar = 0;
+  uint32_t mgen = 0;
+  __syncthreads();
+
+  Poll P;
+  P.rs = __builtin_amdgcn_make_buffer_rsrc(ws, (short)0, (int)sizeof(Workspace), 0x00020000);
+  P.base = ws;
+  P.ec.err = &ws->err;
+  P.ec.spin_cap = a.spin_cap;
+  const TTSLayerWeights* LW = a.layers;
+  const int NL = a.num_layers;
+
+  TileQKV tq;
+  TileO to;
+  TileGU tgu;
+  TileD td;
+  TileKV tk;
+
+  auto tag_of = [&](int lp, int slot) -> uint32_t { return a.tag_base + (uint32_t)(lp * T_NSLOT + slot); };
+  auto has_head = [&](int pi) -> bool { return a.cp_frame ? pi >= 1 : (a.head != nullptr && pi == a.n_pos - 1); };
+
+  // rotary row of channel c (c < 64) at position pos
+  auto rot_row = [&](int c, int pos) -> int {
+    if constexpr (BB) {
+      const int sec = (c < 60 && c % 3 == 1) ? 1 : ((c < 60 && c % 3 == 2) ? 2 : 0);
+      return a.n_pos == 1 ? a.pos3[sec] : pos;
+    } else {
+      return pos;
+    }
+  };
+
+  // ---- poller: input of layer 0 of position pi (embedding source) -> xres, xn
+  auto prep_input0 = [&](int pi) {
+    const bf16_t* src = nullptr;
+    if (a.cp_frame) {
+      if (pi == 0) {
+        for (int i = lane; i < HID; i += 64) s.xres[i] = rbf(a.bb_hidden[i]);
+      } else if (pi == 1) {
+        src = a.bb_emb + (size_t)g0 * HID;
+      } else {
+        src = a.cp_embs[pi - 2] + (size_t)s.tok[pi - 2] * HID;
+      }
+    } else {
+      src = a.in_emb != nullptr ? a.in_emb : a.embed_w + (size_t)a.in_tok * HID;
+    }
+    if (src != nullptr)
+      for (int i = lane; i < HID; i += 64) s.xres[i] = bf2f(src[i]);
+    const double rstd = wave_rstd(s.xres);
+    const bf16_t* g = lw(LW, 0, W_LNIN);
+    for (int i = lane; i < HID; i += 64) s.xn[i] = norm_f32(s.xres[i], rstd, g[i]);
+  };
+
+  // ---- poller: AR2 of layer pass lp (down partials + residual) -> xl slots
+  auto ar2 = [&](int lp) {
+    const int par = lp & 1;
+    poll_parts(P, ws->dpart[par], 32 * li, tag_of(lp, T_DPART), s.stage);
+    if (lane < 32) {
+      // x' = h1 + sum of the 8 XCD partials, added in this order in f64
+      double acc = (double)s.h1res[32 * li + lane];
+#pragma unroll
+      for (int x = 0; x < NXCD; ++x) acc += (double)s.stage[32 * x + lane];
+      float xo = (float)acc;
+      if constexpr (BB) xo = rbf(xo);
+      put_local(&ws->xl[xcd][par][32 * li + lane], xo, tag_of(lp, T_XL));
+    }
+  };
+  // ---- poller: next layer input (after ar2 of lp) -> xres, xn
+  auto prep_input_next = [&](int lp, int next_layer) {
+    poll_vec<8>(P, ws->xl[xcd][lp & 1], HID, tag_of(lp, T_XL), s.xres);
+    const double rstd = wave_rstd(s.xres);
+    const bf16_t* g = lw(LW, next_layer, W_LNIN);
+    for (int i = lane; i < HID; i += 64) s.xn[i] = norm_f32(s.xres[i], rstd, g[i]);
+  };
+  // ---- poller: final norm (after ar2 of lp) -> hb (bf16-rounded), outputs
+  auto prep_final = [&](int lp) {
+    poll_vec<8>(P, ws->xl[xcd][lp & 1], HID, tag_of(lp, T_XL), s.xres);
+    const double rstd = wave_rstd(s.xres);
+    for (int i = lane; i < HID; i += 64) {
+      const float h = norm_f32(s.xres[i], rstd, a.final_norm[i]);
+      s.hb[i] = rbf(h);
+      if (wg == 0) {
+        if (a.out_hidden) a.out_hidden[i] = h;
+        if (a.out_residual) {
+          if constexpr (BB) reinterpret_cast<bf16_t*>(a.out_residual)[i] = f2bf(s.xres[i]);
+          else reinterpret_cast<float*>(a.out_residual)[i] = s.xres[i];
+        }
+      }
+    }
+  };
+  // ---- poller: q/k norm, RoPE, KV write for layer `layer` at position pos
+  auto prep_att = [&](int lp, int layer, int pos, int C) {
+    const int par = lp & 1;
+    poll_vec<4>(P, ws->qkv[xcd][par], LROWS, tag_of(lp, T_QKV), s.stage);
+    const bf16_t* qn = lw(LW, layer, W_QN);
+    const bf16_t* kn = lw(LW, layer, W_KN);
+    const int c = lane;  // channels c and c + 64
+    const int row = rot_row(c, pos);
+    const double cl = bf2f(a.cos_t[(size_t)row * HDIM + c]), sl = bf2f(a.sin_t[(size_t)row * HDIM + c]);
+    const double ch = bf2f(a.cos_t[(size_t)row * HDIM + c + 64]), sh = bf2f(a.sin_t[(size_t)row * HDIM + c + 64]);
+    float outl[3], outh[3];
+#pragma unroll
+    for (int h = 0; h < 3; ++h) {
+      const double xl_ = s.stage[128 * h + c], xh = s.stage[128 * h + c + 64];
+      const double ss = group_sum<64>(fma(xl_, xl_, xh * xh));
+      const double r = 1.0 / sqrt(ss / (double)HDIM + EPSD);
+      const bf16_t* gn = h < 2 ? qn : kn;
+      const double nl = (xl_ * r) * (double)bf2f(gn[c]), nh = (xh * r) * (double)bf2f(gn[c + 64]);
+      outl[h] = (float)(nl * cl - nh * sl);
+      outh[h] = (float)(nl * sh + nh * ch);
+    }
+    s.q[0][c] = outl[0]; s.q[0][c + 64] = outh[0];
+    s.q[1][c] = outl[1]; s.q[1][c + 64] = outh[1];
+    float kl = outl[2], kh = outh[2];
+    float vl = s.stage[384 + c], vh = s.stage[384 + c + 64];
+    if constexpr (BB) { kl = rbf(kl); kh = rbf(kh); vl = rbf(vl); vh = rbf(vh); }
+    s.knew[c] = kl; s.knew[c + 64] = kh;
+    s.vnew[c] = vl; s.vnew[c + 64] = vh;
+    if (li == C - 1) {
+      const size_t off = (((size_t)layer * NKVH + xcd) * (size_t)a.max_seq + pos) * HDIM;
+      if constexpr (BB) {
+        bf16_t* kc = reinterpret_cast<bf16_t*>(a.kc) + off;
+        bf16_t* vc = reinterpret_cast<bf16_t*>(a.vc) + off;
+        kc[c] = f2bf(kl); kc[c + 64] = f2bf(kh);
+        vc[c] = f2bf(vl); vc[c + 64] = f2bf(vh);
+      } else {
+        float* kc = reinterpret_cast<float*>(a.kc) + off;
+        float* vc = reinterpret_cast<float*>(a.vc) + off;
+        kc[c] = kl; kc[c + 64] = kh;
+        vc[c] = vl; vc[c + 64] = vh;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    }
+  };
+  // ---- poller: merge the C attention partials -> attn
+  auto prep_o = [&](int lp, int C) {
+    const int par = lp & 1;
+    poll_vec<17>(P, ws->attp[xcd][par], C * APS, tag_of(lp, T_ATT), s.stage);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float M = -INFINITY;
+      for (int c = 0; c < C; ++c) M = fmaxf(M, s.stage[c * APS + 256 + 2 * h]);
+      double Z = 0.0;
+      for (int c = 0; c < C; ++c)
+        Z += (double)s.stage[c * APS + 257 + 2 * h] * exp((double)s.stage[c * APS + 256 + 2 * h] - (double)M);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int d = lane + 64 * j;
+        double acc = 0.0;
+        for (int c = 0; c < C; ++c)
+          acc += (double)s.stage[c * APS + 128 * h + d] * exp((double)s.stage[c * APS + 256 + 2 * h] - (double)M);
+        s.attn[128 * h + d] = (float)(acc / Z);
+      }
+    }
+  };
+  // ---- poller: AR1 (O partials + residual) -> h1 slots; then h1 -> h1res, hn
+  auto prep_gu = [&](int lp, int layer) {
+    const int par = lp & 1;
+    poll_parts(P, ws->opart[par], 32 * li, tag_of(lp, T_OPART), s.stage);
+    if (lane < 32) {
+      // h1 = x + sum of the 8 XCD partials, added in this order in f64
+      double acc = (double)s.xres[32 * li + lane];
+#pragma unroll
+      for (int x = 0; x < NXCD; ++x) acc += (double)s.stage[32 * x + lane];
+      put_local(&ws->h1[xcd][par][32 * li + lane], (float)acc, tag_of(lp, T_H1));
+    }
+    poll_vec<8>(P, ws->h1[xcd][par], HID, tag_of(lp, T_H1), s.h1res);
+    const double rstd = wave_rstd(s.h1res);
+    const bf16_t* g = lw(LW, layer, W_LNPOST);
+    for (int i = lane; i < HID; i += 64) s.hn[i] = norm_f32(s.h1res[i], rstd, g[i]);
+  };
+  auto prep_down = [&](int lp) {
+    poll_vec<3>(P, ws->inter[xcd][lp & 1], XI, tag_of(lp, T_INTER), s.inter);
+  };
+
+  // ---- math: attention over this workgroup's chunk [c0, c1) at KV length L
+  auto attention = [&](int lp, int layer, int L, int c0, int c1) {
+    constexpr int JJ = KVGeo<BB>::JJ, SUB = KVGeo<BB>::SUB;
+    const int Lold = L - 1;
+    const int d0 = 8 * (lane & 15);
+    const double scale = (double)a.scale;
+    const int nsb = (c1 - c0 + SUB - 1) / SUB;
+    // one query head at a time keeps the f64 accumulators of a single head live
+#pragma unroll 1
+    for (int h = 0; h < 2; ++h) {
+      float qv[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qv[i] = s.q[h][d0 + i];
+      // online softmax in f64 over f32-rounded scores; m is always an f32 value
+      double m = -INFINITY, l = 0.0;
+      double acc[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = 0.0;
+      for (int sb = 0; sb < nsb; ++sb) {
+        const int b0 = c0 + sb * SUB;
+        if (sb > 0 || h > 0) {
+          if (nsb > 1) load_kv<BB>(tk, a, layer, xcd, b0, c1 < Lold ? c1 : Lold, mw, lane);
+        }
+        const TileKV& t = tk;
+#pragma unroll
+        for (int jj = 0; jj < JJ; ++jj) {
+          const int pos = b0 + 4 * JJ * mw + 4 * jj + (lane >> 4);
+          const bool valid = pos < c1;
+          float kv[8], vv[8];
+          if (pos == Lold) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) { kv[i] = s.knew[d0 + i]; vv[i] = s.vnew[d0 + i]; }
+          } else {
+            unpack8<BB>(t, true, jj, kv);
+            unpack8<BB>(t, false, jj, vv);
+          }
+          double dd = 0.0;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) dd = fma((double)qv[i], (double)kv[i], dd);
+          dd = group_sum<16>(dd);
+          const double sc = valid ? (double)(float)(dd * scale) : -INFINITY;
+          const double mn = sc > m ? sc : m;
+          if (mn != -INFINITY) {
+            const double alpha = exp(m - mn);
+            const double p = exp(sc - mn);
+            l = l * alpha + p;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i] = fma(p, (double)vv[i], acc[i] * alpha);
+            m = mn;
+          }
+        }
+      }
+      // merge the 4 lane groups (xor 16, 32); the 4 waves are merged through LDS below
+      const double M = group_max<64>(m);
+      const double f = (m == -INFINITY) ? 0.0 : exp(m - M);
+      double lt = l * f;
+      lt += __shfl_xor(lt, 16, 64);
+      lt += __shfl_xor(lt, 32, 64);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        double v = acc[i] * f;
+        v += __shfl_xor(v, 16, 64);
+        v += __shfl_xor(v, 32, 64);
+        acc[i] = v;
+      }
+      if (lane < 16)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s.red[mw][h][d0 + i] = acc[i];
+      if (lane == 0) { s.red[mw][h][HDIM] = M; s.red[mw][h][HDIM + 1] = lt; }
+    }
+    math_barrier(s, mgen, &ws->err);
+    const int t = threadIdx.x;  // 0..255
+    const int h = t >> 7, d = t & 127;
+    double M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NMATH; ++w) M = s.red[w][h][HDIM] > M ? s.red[w][h][HDIM] : M;
+    double A = 0.0, Lsum = 0.0;
+#pragma unroll
+    for (int w = 0; w < NMATH; ++w) {
+      const double mw_ = s.red[w][h][HDIM];
+      const double f = mw_ == -INFINITY ? 0.0 : exp(mw_ - M);
+      A = fma(s.red[w][h][d], f, A);
+      Lsum = fma(s.red[w][h][HDIM + 1], f, Lsum);
+    }
+    const int c = li;
+    uint64_t* dst = &ws->attp[xcd][lp & 1][c * APS];
+    const uint32_t tg = tag_of(lp, T_ATT);
+    put_local(dst + 128 * h + d, (float)A, tg);
+    if (d == 0) { put_local(dst + 256 + 2 * h, (float)M, tg); put_local(dst + 257 + 2 * h, (float)Lsum, tg); }
+    math_barrier(s, mgen, &ws->err);   // s.red is reused by the next attention
+  };
+
+  // ---- math: GEMV stages (f64 accumulation, f32 results)
+  auto load_x16 = [&](const float* x, double* xv) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) { xv[i] = x[8 * lane + i]; xv[8 + i] = x[512 + 8 * lane + i]; }
+  };
+  auto math_qkv = [&](int lp) {
+    double xv[16];
+    load_x16(s.xn, xv);
+    const uint32_t tg = tag_of(lp, T_QKV);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      double v = dot8d(tq.p[2 * r], xv, 0.0);
+      v = group_sum<64>(dot8d(tq.p[2 * r + 1], xv + 8, v));
+      if (lane == r) put_local(&ws->qkv[xcd][lp & 1][16 * li + 4 * mw + r], (float)v, tg);
+    }
+  };
+  auto math_o = [&](int lp) {
+    double xv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xv[i] = s.attn[8 * (lane & 31) + i];
+    const uint32_t tg = tag_of(lp, T_OPART);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const double v = group_sum<32>(dot8d(to.p[j], xv, 0.0));
+      if ((lane & 31) == 0) put_cross(&ws->opart[lp & 1][xcd][32 * li + 8 * mw + 2 * j + (lane >> 5)], (float)v, tg);
+    }
+  };
+  auto math_gu = [&](int lp) {
+    double xv[16];
+    load_x16(s.hn, xv);
+    const uint32_t tg = tag_of(lp, T_INTER);
+#pragma unroll
+    for (int r = 0; r < 3; ++r) {
+      double g = dot8d(tgu.g[2 * r], xv, 0.0);
+      g = group_sum<64>(dot8d(tgu.g[2 * r + 1], xv + 8, g));
+      double u = dot8d(tgu.u[2 * r], xv, 0.0);
+      u = group_sum<64>(dot8d(tgu.u[2 * r + 1], xv + 8, u));
+      const double act = g / (1.0 + exp(-g)) * u;
+      if (lane == r) put_local(&ws->inter[xcd][lp & 1][12 * li + 3 * mw + r], (float)act, tg);
+    }
+  };
+  auto math_down = [&](int lp) {
+    double xv[24];
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xv[8 * j + i] = s.inter[8 * ((lane & 15) + 16 * j) + i];
+    const uint32_t tg = tag_of(lp, T_DPART);
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      double v = 0.0;
+#pragma unroll
+      for (int j = 0; j < 3; ++j) v = dot8d(td.p[3 * g + j], xv + 8 * j, v);
+      v = group_sum<16>(v);
+      if ((lane & 15) == 0) put_cross(&ws->dpart[lp & 1][xcd][32 * li + 8 * mw + 4 * g + (lane >> 4)], (float)v, tg);
+    }
+  };
+  // head rows of this workgroup: backbone codec head 12 rows (3 per wave), CP head 8 (2 per wave)
+  auto head_rows = [&](int& row0, int& nrows) {
+    const int per_wg = (a.cp_frame ? a.cp_vocab : a.vocab) / NWG;
+    nrows = per_wg / NMATH;
+    row0 = wg * per_wg + mw * nrows;
+  };
+  auto math_head = [&](int pi) {
+    int row0, nrows;
+    head_rows(row0, nrows);
+    double xv[16];
+    load_x16(s.hb, xv);
+    const uint32_t tg = a.tag_base + TAG_HEAD + (uint32_t)pi;
+#pragma unroll
+    for (int r = 0; r < 3; ++r) {
+      if (r < nrows) {
+        double v = dot8d(tq.p[2 * r], xv, 0.0);
+        v = group_sum<64>(dot8d(tq.p[2 * r + 1], xv + 8, v));
+        if (lane == r) {
+          put_cross(&ws->logits[pi & 1][row0 + r], (float)v, tg);
+          if (!a.cp_frame && a.out_logits) a.out_logits[row0 + r] = (float)v;
+        }
+      }
+    }
+  };
+  auto head_weights = [&](int pi) -> const bf16_t* {
+    return a.cp_frame ? a.cp_heads[pi - 1] : a.head;
+  };
+  // ---- poller: collect a head's logits and select a token
+  auto select = [&](int pi) -> int {
+    const int n = a.cp_frame ? a.cp_vocab : a.vocab;
+    poll_vec<24>(P, ws->logits[pi & 1], n, a.tag_base + TAG_HEAD + (uint32_t)pi, s.stage);
+    SelParams sp = a.sel;
+    if (a.cp_frame) {
+      sp.group = pi;   // CP head pi-1 selects codebook group pi
+    } else {
+      // suppress ids [V-1024, V) except EOS (generator.py:71-75)
+      if (a.mask_tail)
+        for (int i = lane; i < n; i += 64)
+          if (i >= n - 1024 && i != a.eos_id) s.stage[i] = -INFINITY;
+      // repetition penalty, once per distinct id (generator.py:161-167)
+      if (a.rep_penalty != 1.0f && a.n_history > 0) {
+        for (int i = lane; i < MAXV / 32; i += 64) s.pen_bits[i] = 0u;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        for (int i = lane; i < a.n_history; i += 64) {
+          const int id = a.history[i];
+          if (id >= 0 && id < n) atomicOr(&s.pen_bits[id >> 5], 1u << (id & 31));
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        for (int i = lane; i < n; i += 64) {
+          if (s.pen_bits[i >> 5] & (1u << (i & 31))) {
+            const float v = s.stage[i];
+            s.stage[i] = v > 0.f ? v / a.rep_penalty : v * a.rep_penalty;
+          }
+        }
+      }
+      if (a.suppress_eos && a.eos_id >= 0 && a.eos_id < n && lane == 0) s.stage[a.eos_id] = -INFINITY;
+      sp.group = 0;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    return wave_select(s.stage, n, sp, &s.sel);
+  };
+
+  // =====================================================================================
+  // Step schedule. One walker defines the barrier sequence; the poller wave and the math
+  // waves each run it with their own action, in separate loops (so the math waves' weight
+  // tiles and the poller's poll registers are never live at the same time). Math waves run
+  // the compute of step k on operands the poller prepared during step k-1 and issue the
+  // weight loads needed two steps later.
+  // =====================================================================================
+  enum Step { S_PRO, S_QKV, S_ATT, S_O, S_GU, S_DOWN, S_HEAD };
+  auto walk = [&](auto&& act) {
+    act(S_PRO, 0, 0);
+    step_barrier();
+    for (int pi = 0; pi < a.n_pos; ++pi) {
+      for (int layer = 0; layer < NL; ++layer) {
+        act(S_QKV, pi, layer); step_barrier();
+        act(S_ATT, pi, layer); step_barrier();
+        act(S_O, pi, layer); step_barrier();
+        act(S_GU, pi, layer); step_barrier();
+        act(S_DOWN, pi, layer); step_barrier();
+      }
+      if (has_head(pi)) { act(S_HEAD, pi, NL - 1); step_barrier(); }
+    }
+  };
+  struct PosInfo { int pos, L, C, P, c0, c1; bool last_pos, head; };
+  auto pinfo = [&](int pi) {
+    PosInfo q;
+    q.pos = a.pos0 + pi;
+    q.L = q.pos + 1;
+    chunking<BB>(q.L, q.C, q.P);
+    q.c0 = li * q.P;
+    q.c1 = min(q.L, (li + 1) * q.P);
+    q.last_pos = pi == a.n_pos - 1;
+    q.head = has_head(pi);
+    return q;
+  };
+  // chunk of this workgroup at the next position, restricted to cached (old) positions
+  auto next_kv = [&](int pi, int layer) {
+    const PosInfo n = pinfo(pi + 1);
+    if (li < n.C) load_kv<BB>(tk, a, layer, xcd, n.c0, min(n.c1, n.L - 1), mw, lane);
+    else tk = TileKV{};
+  };
+  // Tiles are (re)defined on every path so that no stale tile value stays live across the
+  // step loop (that would keep all tiles resident at once and spill).
+
+  if (poller) {
+    walk([&](int st, int pi, int layer) {
+      const PosInfo q = pinfo(pi);
+      const int lp = pi * NL + layer;
+      switch (st) {
+        case S_PRO: prep_input0(0); break;
+        case S_QKV: prep_att(lp, layer, q.pos, q.C); break;
+        case S_ATT: prep_o(lp, q.C); break;
+        case S_O: prep_gu(lp, layer); break;
+        case S_GU: prep_down(lp); break;
+        case S_DOWN:
+          if (layer < NL - 1) { ar2(lp); prep_input_next(lp, layer + 1); }
+          else if (q.head || q.last_pos) { ar2(lp); prep_final(lp); }
+          else prep_input0(pi + 1);
+          break;
+        case S_HEAD:
+          if (a.cp_frame || wg == 0) {
+            const int tok = select(pi);
+            if (a.cp_frame) {
+              if (lane == 0) s.tok[pi - 1] = tok;
+              __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+              if (!q.last_pos) prep_input0(pi + 1);
+            } else if (lane == 0 && a.out_token) {
+              *a.out_token = tok;
+            }
+          }
+          break;
+      }
+    });
+  } else {
+    walk([&](int st, int pi, int layer) {
+      const PosInfo q = pinfo(pi);
+      const int lp = pi * NL + layer;
+      const bool last_layer = layer == NL - 1;
+      switch (st) {
+        case S_PRO:
+          load_qkv<BB>(tq, LW, 0, xcd, li, mw, lane);
+          if (li < q.C) load_kv<BB>(tk, a, 0, xcd, q.c0, min(q.c1, q.L - 1), mw, lane);
+          else tk = TileKV{};
+          break;
+        case S_QKV:
+          math_qkv(lp);
+          load_o<BB>(to, LW, layer, xcd, li, mw, lane);
+          break;
+        case S_ATT:
+          if (li < q.C) attention(lp, layer, q.L, q.c0, q.c1);
+          load_gu<BB>(tgu, LW, layer, xcd, li, mw, lane);
+          break;
+        case S_O:
+          math_o(lp);
+          load_d<BB>(td, LW, layer, xcd, li, mw, lane);
+          break;
+        case S_GU:
+          math_gu(lp);
+          if (!last_layer) {
+            load_qkv<BB>(tq, LW, layer + 1, xcd, li, mw, lane);
+          } else if (q.head) {
+            int row0, nrows;
+            head_rows(row0, nrows);
+            load_head<BB>(tq, head_weights(pi), row0, nrows, lane);
+          } else if (!q.last_pos) {
+            load_qkv<BB>(tq, LW, 0, xcd, li, mw, lane);
+          } else {
+            tq = TileQKV{};
+          }
+          break;
+        case S_DOWN:
+          math_down(lp);
+          if (!last_layer) {
+            if (li < q.C) load_kv<BB>(tk, a, layer + 1, xcd, q.c0, min(q.c1, q.L - 1), mw, lane);
+            else tk = TileKV{};
+          } else if (!q.head && !q.last_pos) {
+            next_kv(pi, 0);
+          } else {
+            tk = TileKV{};
+          }
+          break;
+        case S_HEAD:
+          math_head(pi);
+          if (!q.last_pos) {
+            load_qkv<BB>(tq, LW, 0, xcd, li, mw, lane);
+            next_kv(pi, 0);
+          } else {
+            tq = TileQKV{};
+            tk = TileKV{};
+          }
+          break;
+      }
+    });
+  }
+
+  // ---- code-predictor frame epilogue: tokens and the bf16 embedding combine
+  if (a.cp_frame && wg == 0 && poller) {
+    if (lane == 0) {
+      if (a.hist_slot) *a.hist_slot = g0;
+      a.out_tokens[0] = g0;
+      for (int g = 0; g < a.n_groups; ++g) a.out_tokens[1 + g] = s.tok[g];
+    }
+    for (int d = lane; d < HID; d += 64) {
+      float acc = bf2f(a.bb_emb[(size_t)g0 * HID + d]);
+      for (int g = 0; g < a.n_groups; ++g) acc = rbf(acc + bf2f(a.cp_embs[g][(size_t)s.tok[g] * HID + d]));
+      if (a.text_row) acc = rbf(acc + bf2f(a.text_row[d]));
+      a.out_combined[d] = f2bf(acc);
+    }
+  }
+}
+
+template __global__ void qtts_decode_kernel<true>(const KArgs a);
+template __global__ void qtts_decode_kernel<false>(const KArgs a);
+
+}  // namespace qtts
+
+// =========================================================================================
+// Host side
+// =========================================================================================
+namespace {
+
+using qtts::KArgs;
+using qtts::Workspace;
+
+constexpr uint32_t kSpinCap = 1u << 22;   // ~4 s of polling before a wait is declared failed
+
+struct DeviceCheck {
+  bool done = false;
+  hipError_t status = hipSuccess;
+};
+std::mutex g_mu;
+std::unordered_map<int, DeviceCheck> g_dev;
+std::unordered_map<const void*, uint32_t> g_seq;   // launch sequence per workspace
+std::unordered_map<int, void*> g_lib_ws;           // library-owned workspace per device
+
+__global__ void xcc_probe_kernel(int* out) {
+  if (threadIdx.x == 0) out[blockIdx.x] = (int)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15u);
+}
+__global__ void zero_kernel(uint4* p, size_t n16) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x)
+    p[i] = make_uint4(0, 0, 0, 0);
+}
+
+// gfx950 with 256 CUs, cooperative launch, and a cooperative grid of 256 workgroups whose
+// XCC ids are a rotation of blockIdx % 8 with 32 workgroups per XCD.
+hipError_t check_device(int device) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  DeviceCheck& dc = g_dev[device];
+  if (dc.done) return dc.status;
+  dc.done = true;
+  hipDeviceProp_t prop;
+  hipError_t e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess) return dc.status = e;
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0 || prop.multiProcessorCount != qtts::NWG || !prop.cooperativeLaunch)
+    return dc.status = hipErrorInvalidDevice;
+  int occ = 0;
+  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)qtts::qtts_decode_kernel<true>, qtts::NTHR, 0);
+  if (e != hipSuccess || occ < 1) return dc.status = (e != hipSuccess ? e : hipErrorInvalidDevice);
+  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)qtts::qtts_decode_kernel<false>, qtts::NTHR, 0);
+  if (e != hipSuccess || occ < 1) return dc.status = (e != hipSuccess ? e : hipErrorInvalidDevice);
+  int* d = nullptr;
+  if ((e = hipMalloc(&d, qtts::NWG * sizeof(int))) != hipSuccess) return dc.status = e;
+  void* args[] = {&d};
+  e = hipLaunchCooperativeKernel((const void*)xcc_probe_kernel, dim3(qtts::NWG), dim3(64), args, 0, 0);
+  int h[qtts::NWG];
+  if (e == hipSuccess) e = hipMemcpy(h, d, sizeof(h), hipMemcpyDeviceToHost);
+  const hipError_t fe = hipFree(d);
+  if (e == hipSuccess) e = fe;
+  if (e != hipSuccess) return dc.status = e;
+  int count[16] = {0};
+  for (int b = 0; b < qtts::NWG; ++b) {
+    if (h[b] < 0 || h[b] >= qtts::NXCD || ((h[b] - b) & 7) != ((h[0] - 0) & 7)) return dc.status = hipErrorInvalidDevice;
+    ++count[h[b]];
+  }
+  for (int x = 0; x < qtts::NXCD; ++x)
+    if (count[x] != qtts::WPX) return dc.status = hipErrorInvalidDevice;
+  return dc.status = hipSuccess;
+}
+
+uint32_t next_tag_base(void* ws, hipStream_t stream, hipError_t* err) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  uint32_t& seq = g_seq[ws];
+  if (seq == 0 || seq >= (1u << 20) - 1u) {
+    // first use (or tag wrap): clear every exchange slot with a fill kernel
+    const size_t n16 = sizeof(Workspace) / 16;
+    hipLaunchKernelGGL(zero_kernel, dim3(256), dim3(256), 0, stream, reinterpret_cast<uint4*>(ws), n16);
+    *err = hipGetLastError();
+    seq = 1;
+  }
+  return (seq++) << 12;
+}
+
+hipError_t launch(bool bb, KArgs& a, hipStream_t stream) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if ((e = check_device(dev)) != hipSuccess) return e;
+  if (a.num_layers < 1 || a.n_pos < 1 || a.num_layers * a.n_pos > qtts::MAX_LAYER_PASSES) return hipErrorInvalidValue;
+  if (a.pos0 < 0 || a.pos0 + a.n_pos > a.max_seq) return hipErrorInvalidValue;
+  hipError_t ze = hipSuccess;
+  a.tag_base = next_tag_base(a.ws, stream, &ze);
+  if (ze != hipSuccess) return ze;
+  a.spin_cap = kSpinCap;
+  void* args[] = {&a};
+  const void* fn = bb ? (const void*)qtts::qtts_decode_kernel<true> : (const void*)qtts::qtts_decode_kernel<false>;
+  return hipLaunchCooperativeKernel(fn, dim3(qtts::NWG), dim3(qtts::NTHR), args, 0, stream);
+}
+
+void* lib_workspace(hipError_t* err) {
+  int dev = 0;
+  *err = hipGetDevice(&dev);
+  if (*err != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> lk(g_mu);
+  void*& p = g_lib_ws[dev];
+  if (p == nullptr) {
+    *err = hipMalloc(&p, sizeof(Workspace));
+    if (*err != hipSuccess) { p = nullptr; return nullptr; }
+    *err = hipMemset(p, 0, sizeof(Workspace));
+  }
+  return p;
+}
+
+void base_args(KArgs& a, const TTSLayerWeights* layers, int num_layers, const void* final_norm, const void* cos_t,
+               const void* sin_t, void* kc, void* vc, int max_seq) {
+  std::memset(&a, 0, sizeof(a));
+  a.layers = layers;
+  a.num_layers = num_layers;
+  a.final_norm = reinterpret_cast<const qtts::bf16_t*>(final_norm);
+  a.cos_t = reinterpret_cast<const qtts::bf16_t*>(cos_t);
+  a.sin_t = reinterpret_cast<const qtts::bf16_t*>(sin_t);
+  a.kc = kc;
+  a.vc = vc;
+  a.max_seq = max_seq;
+  a.scale = 0.08838834764831845f;
+  a.eos_id = -1;
+  a.n_pos = 1;
+  a.sel.temperature = 1.0f;
+  a.sel.top_p = 1.0f;
+}
+
+hipError_t ref_launch(bool bb, int token, const void* embed, const void* emb, const TTSLayerWeights* layers,
+                      const void* final_norm, const void* cos_t, const void* sin_t, void* kc, void* vc,
+                      void* hidden_buffer, void* g_normalized, int num_layers, int position, int cache_len,
+                      int max_seq_len, float attn_scale, hipStream_t stream) {
+  if (cache_len != position + 1 || position < 0 || position >= max_seq_len) return hipErrorInvalidValue;
+  if (layers == nullptr || final_norm == nullptr || cos_t == nullptr || sin_t == nullptr || kc == nullptr || vc == nullptr ||
+      g_normalized == nullptr || (emb == nullptr && embed == nullptr))
+    return hipErrorInvalidValue;
+  hipError_t e;
+  void* ws = lib_workspace(&e);
+  if (ws == nullptr) return e;
+  KArgs a;
+  base_args(a, layers, num_layers, final_norm, cos_t, sin_t, kc, vc, max_seq_len);
+  a.scale = attn_scale;
+  a.ws = reinterpret_cast<Workspace*>(ws);
+  a.pos0 = position;
+  a.pos3[0] = a.pos3[1] = a.pos3[2] = position;
+  a.in_emb = reinterpret_cast<const qtts::bf16_t*>(emb);
+  a.embed_w = reinterpret_cast<const qtts::bf16_t*>(embed);
+  a.in_tok = token;
+  a.out_hidden = reinterpret_cast<float*>(g_normalized);
+  a.out_residual = hidden_buffer;
+  return launch(bb, a, stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+hipError_t launch_tts_decode(int input_token_id, const void* embed_weight, const TTSLayerWeights* layer_weights,
+                             const void* final_norm_weight, const void* cos_table, const void* sin_table, void* k_cache,
+                             void* v_cache, void* hidden_buffer, void*, void*, void*, void*, void*, void*, void*,
+                             void* g_normalized, int num_layers, int position, int cache_len, int max_seq_len,
+                             float attn_scale, hipStream_t stream) {
+  if (embed_weight == nullptr || input_token_id < 0) return hipErrorInvalidValue;
+  return ref_launch(true, input_token_id, embed_weight, nullptr, layer_weights, final_norm_weight, cos_table, sin_table,
+                    k_cache, v_cache, hidden_buffer, g_normalized, num_layers, position, cache_len, max_seq_len,
+                    attn_scale, stream);
+}
+
+hipError_t launch_tts_decode_with_embedding(const void* input_embedding, const TTSLayerWeights* layer_weights,
+                                            const void* final_norm_weight, const void* cos_table, const void* sin_table,
+                                            void* k_cache, void* v_cache, void* hidden_buffer, void*, void*, void*,
+                                            void*, void*, void*, void*, void* g_normalized, int num_layers,
+                                            int position, int cache_len, int max_seq_len, float attn_scale,
+                                            hipStream_t stream) {
+  if (input_embedding == nullptr) return hipErrorInvalidValue;
+  return ref_launch(true, 0, nullptr, input_embedding, layer_weights, final_norm_weight, cos_table, sin_table, k_cache,
+                    v_cache, hidden_buffer, g_normalized, num_layers, position, cache_len, max_seq_len, attn_scale,
+                    stream);
+}
+
+hipError_t launch_cp_decode_with_embedding(const void* input_embedding, const CPLayerWeights* layer_weights,
+                                           const void* final_norm_weight, const void* cos_table, const void* sin_table,
+                                           void* k_cache, void* v_cache, void* hidden_buffer, void*, void*, void*,
+                                           void*, void*, void*, void*, void* g_normalized, int num_layers,
+                                           int position, int cache_len, int max_seq_len, float attn_scale,
+                                           hipStream_t stream) {
+  if (input_embedding == nullptr) return hipErrorInvalidValue;
+  return ref_launch(false, 0, nullptr, input_embedding, layer_weights, final_norm_weight, cos_table, sin_table, k_cache,
+                    v_cache, hidden_buffer, g_normalized, num_layers, position, cache_len, max_seq_len, attn_scale,
+                    stream);
+}
+
+size_t qtts_workspace_bytes(void) { return sizeof(Workspace); }
+
+hipError_t qtts_workspace_init(void* workspace, int device) {
+  if (workspace == nullptr || (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return hipErrorInvalidValue;
+  return check_device(device);
+}
+
+hipError_t qtts_workspace_check(void* workspace, unsigned int* error_code, hipStream_t stream) {
+  if (workspace == nullptr || error_code == nullptr) return hipErrorInvalidValue;
+  Workspace* ws = reinterpret_cast<Workspace*>(workspace);
+  hipError_t e = hipMemcpyAsync(error_code, &ws->err, sizeof(unsigned int), hipMemcpyDeviceToHost, stream);
+  if (e != hipSuccess) return e;
+  if ((e = hipStreamSynchronize(stream)) != hipSuccess) return e;
+  if (*error_code != 0u) {
+    unsigned int zero = 0u;
+    e = hipMemcpy(&ws->err, &zero, sizeof(zero), hipMemcpyHostToDevice);
+  }
+  return e;
+}
+
+hipError_t qtts_backbone_step(void* workspace, const TTSLayerWeights* layer_weights, int num_layers,
+                              const void* final_norm_weight, const void* cos_table, const void* sin_table,
+                              void* k_cache, void* v_cache, int max_seq_len, int position, const int pos3[3],
+                              const void* input_embedding, const void* embed_weight, int input_token_id,
+                              float* out_hidden, void* out_residual, const void* codec_head, int vocab,
+                              float* out_logits, int* out_token, int mask_tail, const int* history,
+                              int n_history, float repetition_penalty, int eos_id, int suppress_eos,
+                              const QttsSampling* sampling, int frame_step, const int* skip_if,
+                              hipStream_t stream) {
+  if (workspace == nullptr || (input_embedding == nullptr && embed_weight == nullptr)) return hipErrorInvalidValue;
+  if (codec_head != nullptr && (vocab <= 0 || vocab > qtts::MAXV || vocab % (qtts::NWG * qtts::NMATH) != 0))
+    return hipErrorInvalidValue;
+  if (n_history < 0 || (n_history > 0 && history == nullptr)) return hipErrorInvalidValue;
+  KArgs a;
+  base_args(a, layer_weights, num_layers, final_norm_weight, cos_table, sin_table, k_cache, v_cache, max_seq_len);
+  a.ws = reinterpret_cast<Workspace*>(workspace);
+  a.pos0 = position;
+  for (int i = 0; i < 3; ++i) a.pos3[i] = pos3 ? pos3[i] : position;
+  for (int i = 0; i < 3; ++i)
+    if (a.pos3[i] < 0 || a.pos3[i] >= max_seq_len) return hipErrorInvalidValue;
+  a.in_emb = reinterpret_cast<const qtts::bf16_t*>(input_embedding);
+  a.embed_w = reinterpret_cast<const qtts::bf16_t*>(embed_weight);
+  a.in_tok = input_token_id;
+  a.out_hidden = out_hidden;
+  a.out_residual = out_residual;
+  a.head = reinterpret_cast<const qtts::bf16_t*>(codec_head);
+  a.vocab = vocab;
+  a.out_logits = out_logits;
+  a.out_token = out_token;
+  a.mask_tail = mask_tail;
+  a.skip = skip_if;
+  a.history = history;
+  a.n_history = n_history;
+  a.rep_penalty = repetition_penalty;
+  a.eos_id = eos_id;
+  a.suppress_eos = suppress_eos;
+  if (sampling) {
+    a.sel.do_sample = sampling->do_sample;
+    a.sel.temperature = sampling->temperature;
+    a.sel.top_k = sampling->top_k;
+    a.sel.top_p = sampling->top_p;
+    a.sel.seed = sampling->seed;
+  }
+  a.sel.frame_step = frame_step;
+  return launch(true, a, stream);
+}
+
+hipError_t qtts_cp_step(void* workspace, const CPLayerWeights* layer_weights, int num_layers,
+                        const void* final_norm_weight, const void* cos_table, const void* sin_table, void* k_cache,
+                        void* v_cache, int max_seq_len, int position, const void* input_embedding, float* out_hidden,
+                        float* out_residual, hipStream_t stream) {
+  if (workspace == nullptr || input_embedding == nullptr) return hipErrorInvalidValue;
+  KArgs a;
+  base_args(a, layer_weights, num_layers, final_norm_weight, cos_table, sin_table, k_cache, v_cache, max_seq_len);
+  a.ws = reinterpret_cast<Workspace*>(workspace);
+  a.pos0 = position;
+  a.in_emb = reinterpret_cast<const qtts::bf16_t*>(input_embedding);
+  a.out_hidden = out_hidden;
+  a.out_residual = out_residual;
+  return launch(false, a, stream);
+}
+
+hipError_t qtts_cp_frame(void* workspace, const CPLayerWeights* layer_weights, int num_layers,
+                         const void* final_norm_weight, const void* cos_table, const void* sin_table, void* k_cache,
+                         void* v_cache, int max_seq_len, const float* bb_hidden, const int* g0,
+                         const void* bb_embedding, const void* const* lm_heads, const void* const* cp_embeddings,
+                         int n_groups, int cp_vocab, const void* text_row, int* out_tokens, void* out_combined,
+                         int* g0_history_slot, int eos_id, int* done, const QttsSampling* sampling, int frame_step,
+                         hipStream_t stream) {
+  if (workspace == nullptr || bb_hidden == nullptr || g0 == nullptr || bb_embedding == nullptr || lm_heads == nullptr ||
+      cp_embeddings == nullptr || out_tokens == nullptr || out_combined == nullptr || done == nullptr)
+    return hipErrorInvalidValue;
+  if (n_groups < 1 || n_groups + 1 > 31 || n_groups + 1 > max_seq_len) return hipErrorInvalidValue;
+  if (cp_vocab <= 0 || cp_vocab > qtts::MAXV || cp_vocab % (qtts::NWG * qtts::NMATH) != 0) return hipErrorInvalidValue;
+  KArgs a;
+  base_args(a, layer_weights, num_layers, final_norm_weight, cos_table, sin_table, k_cache, v_cache, max_seq_len);
+  a.ws = reinterpret_cast<Workspace*>(workspace);
+  a.pos0 = 0;
+  a.n_pos = n_groups + 1;
+  a.cp_frame = 1;
+  a.bb_hidden = bb_hidden;
+  a.g0 = g0;
+  a.bb_emb = reinterpret_cast<const qtts::bf16_t*>(bb_embedding);
+  a.cp_heads = reinterpret_cast<const qtts::bf16_t* const*>(lm_heads);
+  a.cp_embs = reinterpret_cast<const qtts::bf16_t* const*>(cp_embeddings);
+  a.n_groups = n_groups;
+  a.cp_vocab = cp_vocab;
+  a.text_row = reinterpret_cast<const qtts::bf16_t*>(text_row);
+  a.out_tokens = out_tokens;
+  a.hist_slot = g0_history_slot;
+  a.out_combined = reinterpret_cast<qtts::bf16_t*>(out_combined);
+  a.eos_id = eos_id;
+  a.done = done;
+  if (sampling) {
+    a.sel.do_sample = sampling->do_sample;
+    a.sel.temperature = sampling->temperature;
+    a.sel.top_k = sampling->top_k;
+    a.sel.top_p = sampling->top_p;
+    a.sel.seed = sampling->seed;
+  }
+  a.sel.frame_step = frame_step;
+  return launch(false, a, stream);
+}
+
+}  // extern "C"

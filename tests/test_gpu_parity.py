@@ -1,0 +1,220 @@
+"""GPU parity: the HIP decode kernels against the CPU oracle on the same seeded inputs.
+
+Both sides accumulate in f64 and round to f32 / bf16 at the same storage points, so
+per-step hidden states must agree within rel-L2 <= 1e-5 (the north-star bar against the
+reference's PyTorch path is 1e-2, checked in test_gpu_hf_policy.py), greedy tokens exactly.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle.qtts_oracle import (DecoderOracle, TalkerOracle, TalkerWeights, head_logits, rel_l2, sample_token,
+                                suppress_mask, apply_repetition_penalty)
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+def _print(*a):
+    print(*a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def full(pkg):
+    sd = pkg.synthetic_state_dict(seed=1234)
+    dsd = {k: v.to("cuda") for k, v in sd.items()}
+    return sd, dsd, TalkerWeights.from_state_dict(sd, 28, 5)
+
+
+def _rand_kv(n_layers, L, seed, dtype):
+    g = torch.Generator().manual_seed(seed)
+    k = torch.randn(n_layers, 8, L, 128, generator=g).to(dtype)
+    v = torch.randn(n_layers, 8, L, 128, generator=g).to(dtype)
+    return k, v
+
+
+def test_backbone_two_layers_prefill_steps(pkg):
+    cfg = pkg.SyntheticConfig(n_bb_layers=2, n_cp_layers=1, n_groups=1)
+    sd = pkg.synthetic_state_dict(seed=11, cfg=cfg)
+    bb = pkg.TTSMegakernelGenerator(model={k: v.cuda() for k, v in sd.items()}, max_seq_len=256)
+    tw = TalkerWeights.from_state_dict(sd, 2, 1)
+    orc = DecoderOracle(tw.bb_layers, tw.bb_norm, 256, "backbone", "kernel")
+    g = torch.Generator().manual_seed(5)
+    xs = torch.randn(70, 1024, generator=g).to(torch.bfloat16)
+    worst = 0.0
+    for i in range(70):
+        h = bb.decode_step_with_embedding(xs[i].cuda())
+        hr, _ = orc.step(xs[i], pos=i)
+        worst = max(worst, rel_l2(h.cpu(), hr))
+    bb.check_error()
+    _print(f"2-layer backbone, 70 steps: worst rel_l2 {worst:.2e}")
+    assert worst < TOL
+    # KV written by the kernel equals the oracle's within bf16 rounding
+    k = bb.get_k_cache()[:, :, :70].float().cpu()
+    assert rel_l2(k, orc.k[:, :, :70].float()) < TOL
+
+
+def test_backbone_28_layers_L129(full, pkg):
+    sd, dsd, tw = full
+    bb = pkg.TTSMegakernelGenerator(model=dsd, max_seq_len=512)
+    orc = DecoderOracle(tw.bb_layers, tw.bb_norm, 512, "backbone", "kernel")
+    k, v = _rand_kv(28, 128, 21, torch.bfloat16)
+    bb.set_kv_cache(k.cuda(), v.cuda())
+    bb.set_position(128)
+    orc.set_kv(k, v)
+    x = torch.randn(1024, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16)
+    h = bb.decode_step_with_embedding(x.cuda())
+    hr, layers = orc.step(x, pos=128)
+    e = rel_l2(h.cpu(), hr)
+    res = bb.decoder.residual_buffer().float().cpu()
+    e_res = rel_l2(res, layers[-1])
+    lg = head_logits(tw.codec_head, h.cpu())
+    lr = head_logits(tw.codec_head, hr)
+    _print(f"28-layer backbone L=129: hidden rel_l2 {e:.2e}, residual {e_res:.2e}, logits {rel_l2(lg, lr):.2e}")
+    bb.check_error()
+    assert e < TOL and e_res < TOL
+
+
+def test_backbone_long_context_2048(full, pkg):
+    sd, dsd, tw = full
+    n = 4
+    orc = DecoderOracle(tw.bb_layers[:n], tw.bb_norm, 2048, "backbone", "kernel")
+    # 4-layer model so the oracle stays fast; exercises 8 chunks x 4 sub-blocks of attention
+    sd4 = {k: v for k, v in dsd.items() if not k.startswith("talker.model.layers.") or int(k.split(".")[3]) < n}
+    bbn = pkg.TTSMegakernelGenerator(model=sd4, max_seq_len=2048)
+    k, v = _rand_kv(n, 2047, 31, torch.bfloat16)
+    bbn.set_kv_cache(k.cuda(), v.cuda())
+    bbn.set_position(2047)
+    orc.set_kv(k, v)
+    x = torch.randn(1024, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
+    h = bbn.decode_step_with_embedding(x.cuda())
+    hr, _ = orc.step(x, pos=2047)
+    e = rel_l2(h.cpu(), hr)
+    _print(f"4-layer backbone L=2048: hidden rel_l2 {e:.2e}")
+    bbn.check_error()
+    assert e < TOL
+
+
+def test_backbone_mrope_distinct_positions(full, pkg):
+    sd, dsd, tw = full
+    n = 2
+    sd2 = {k: v for k, v in dsd.items() if not k.startswith("talker.model.layers.") or int(k.split(".")[3]) < n}
+    bb = pkg.TTSMegakernelGenerator(model=sd2, max_seq_len=600)
+    orc = DecoderOracle(tw.bb_layers[:n], tw.bb_norm, 600, "backbone", "kernel")
+    k, v = _rand_kv(n, 300, 41, torch.bfloat16)
+    bb.set_kv_cache(k.cuda(), v.cuda())
+    bb.set_position(300)
+    orc.set_kv(k, v)
+    x = torch.randn(1024, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16)
+    pos3 = (300, 157, 111)
+    h = bb.decode_step_with_embedding(x.cuda(), pos3=pos3)
+    hr, _ = orc.step(x, pos=300, pos3=pos3)
+    h1d, _ = DecoderOracle(tw.bb_layers[:n], tw.bb_norm, 600, "backbone", "kernel").step(x, pos=300)
+    e = rel_l2(h.cpu(), hr)
+    _print(f"mRoPE (300,157,111): rel_l2 {e:.2e} (vs 1D-RoPE oracle {rel_l2(h.cpu(), h1d):.2e})")
+    assert e < TOL
+
+
+def test_cp_reference_steps(full, pkg):
+    sd, dsd, tw = full
+    cp = pkg.CodePredictorMegakernelGenerator(model=dsd, max_seq_len=256)
+    orc = DecoderOracle(tw.cp_layers, tw.cp_norm, 256, "cp", "kernel")
+    g = torch.Generator().manual_seed(6)
+    worst = 0.0
+    for i in range(6):
+        x = torch.randn(1024, generator=g).to(torch.bfloat16)
+        h = cp.decode_step_with_embedding(x.cuda())
+        hr, _ = orc.step(x, pos=i)
+        worst = max(worst, rel_l2(h.cpu(), hr))
+    cp.check_error()
+    _print(f"CP 6 steps: worst rel_l2 {worst:.2e}")
+    assert worst < TOL
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_cp_frame_greedy_tokens(full, pkg, seed):
+    sd, dsd, tw = full
+    cp = pkg.CodePredictorMegakernelGenerator(model=dsd, max_seq_len=32)
+    talker = TalkerOracle(tw, max_seq=64)
+    g = torch.Generator().manual_seed(100 + seed)
+    hid = torch.randn(1024, generator=g)
+    g0 = int(torch.randint(0, 3072, (1,), generator=g))
+    trace = {}
+    ref = talker.cp_frame(hid, g0, trace=trace)
+    i32 = dict(dtype=torch.int32, device="cuda")
+    out = torch.full((16,), -1, **i32)
+    comb = torch.empty(1024, dtype=torch.bfloat16, device="cuda")
+    text = torch.randn(1024, generator=g).to(torch.bfloat16)
+    cp.decoder.frame(hid.cuda(), torch.tensor([g0], **i32), text.cuda(), out, comb, -1, torch.zeros(1, **i32),
+                     False, 1.0, 0, 1.0, 0, 0)
+    torch.cuda.synchronize()
+    cp.check_error()
+    toks = out.cpu().tolist()
+    margins = [float(torch.topk(l, 2)[0][0] - torch.topk(l, 2)[0][1]) for l in trace["cp_logits"]]
+    _print(f"CP frame seed {seed}: gpu {toks[1:]} oracle {ref} min top-2 margin {min(margins):.3g}")
+    assert toks[0] == g0
+    assert toks[1:] == ref
+    comb_ref = talker.combine([g0] + ref, text)
+    assert torch.equal(comb.cpu(), comb_ref)
+
+
+def test_backbone_head_select_greedy_and_penalty(full, pkg):
+    sd, dsd, tw = full
+    n = 2
+    sd2 = {k: v for k, v in dsd.items() if not k.startswith("talker.model.layers.") or int(k.split(".")[3]) < n}
+    bb = pkg.TTSMegakernelGenerator(model=sd2, max_seq_len=64)
+    x = torch.randn(1024, generator=torch.Generator().manual_seed(8)).to(torch.bfloat16)
+    i32 = dict(dtype=torch.int32, device="cuda")
+    tok = torch.zeros(1, **i32)
+    hist = torch.tensor([5, 7, 5, 3000, 12], **i32)
+    eos = 2150
+    for pen, sup in ((1.0, False), (1.3, True)):
+        bb.reset()
+        bb.decoder.decode_step_select(x.cuda(), tok, hist, 5, pen, eos, sup, False, 1.0, 50, 1.0, 0, 1)
+        torch.cuda.synchronize()
+        logits = bb.decoder.logits_buffer().cpu()
+        lg = logits.clone()
+        lg[suppress_mask(3072, eos)] = float("-inf")
+        lg = apply_repetition_penalty(lg, hist.cpu().tolist(), pen)
+        ref = sample_token(lg, False, 1.0, 50, 1.0, eos if sup else None)
+        _print(f"head select pen={pen} sup={sup}: gpu {int(tok.item())} oracle {ref}")
+        assert int(tok.item()) == ref
+    bb.check_error()
+
+
+@pytest.mark.parametrize("top_k,top_p", [(50, 1.0), (0, 0.8), (20, 0.5)])
+def test_backbone_sampling_matches_oracle(full, pkg, top_k, top_p):
+    sd, dsd, tw = full
+    n = 1
+    sd1 = {k: v for k, v in dsd.items() if not k.startswith("talker.model.layers.") or int(k.split(".")[3]) < n}
+    bb = pkg.TTSMegakernelGenerator(model=sd1, max_seq_len=64)
+    i32 = dict(dtype=torch.int32, device="cuda")
+    tok = torch.zeros(1, **i32)
+    hist = torch.zeros(1, **i32)
+    eos = 2150
+    agree = 0
+    for trial in range(6):
+        x = torch.randn(1024, generator=torch.Generator().manual_seed(50 + trial)).to(torch.bfloat16)
+        bb.reset()
+        bb.decoder.decode_step_select(x.cuda(), tok, hist, 0, 1.0, eos, False, True, 0.9, top_k, top_p, 77, trial)
+        torch.cuda.synchronize()
+        lg = bb.decoder.logits_buffer().cpu().clone()
+        lg[suppress_mask(3072, eos)] = float("-inf")
+        ref = sample_token(lg, True, 0.9, top_k, top_p, None, seed=77, frame_step=trial, group=0)
+        agree += int(int(tok.item()) == ref)
+    _print(f"sampling top_k={top_k} top_p={top_p}: {agree}/6 identical draws")
+    bb.check_error()
+    assert agree == 6
+
+
+def test_reference_kv_roundtrip(full, pkg):
+    sd, dsd, tw = full
+    sd1 = {k: v for k, v in dsd.items() if not k.startswith("talker.model.layers.") or int(k.split(".")[3]) < 1}
+    bb = pkg.TTSMegakernelGenerator(model=sd1, max_seq_len=64)
+    k, v = _rand_kv(1, 17, 3, torch.bfloat16)
+    bb.set_kv_cache(k.cuda(), v.cuda())
+    assert torch.equal(bb.get_k_cache()[:, :, :17].cpu(), k)
+    assert torch.equal(bb.get_v_cache()[:, :, :17].cpu(), v)
+    assert int(bb.get_k_cache()[:, :, 17:].abs().sum()) == 0
