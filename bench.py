@@ -1,0 +1,201 @@
+"""Benchmark: codec frames/s at batch 1 and 512 context on one MI355X.
+
+One step = one codec frame = one code-predictor frame launch (2-token prefill + 14 decode
+steps, 15 lm-heads with greedy selection, embedding combine; 5 layers) + one backbone decode
+launch (28 layers at KV length 512, codec head, suppression, greedy group-0 selection), with
+random-init bf16 weights of the Qwen3-TTS 0.6B talker shapes and a KV cache filled with random
+bf16 values up to position 511 (each frame writes slot 511, so every frame attends to 512).
+
+Prints one JSON line (see the repository's bench contract) with:
+  value         frames/s over the timed K frames (inputs resident in HBM, no host sync inside)
+  roofline      algorithmic bytes / kernel time for the dominant kernel, timed with HIP events
+                on the launch stream, against MI355X's 8 TB/s
+  cpu_baseline  the same frame through the CPU oracle's HF-bf16 path (eager PyTorch, bf16
+                weights) on this host, timed on a bounded sample of frames
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+# Algorithmic bytes (weights + KV traffic), per the unit definitions of the decode path:
+LAYER_BYTES = 15_728_640 * 2 + 4_608          # bf16 matrices + norm gains of one layer
+W_BB = 28 * LAYER_BYTES + 2_048 + 3072 * 1024 * 2               # + final norm + codec head
+W_CP = 5 * LAYER_BYTES + 2_048 + 2048 * 1024 * 2 + 1024 * 2     # + final norm + 1 lm-head + 1 emb row
+KV_BB = 28 * 8 * 128 * 2 * 2                  # bf16 K+V bytes per attended token
+KV_CP = 5 * 8 * 128 * 4 * 2                   # f32 K+V bytes per attended token
+HBM_PEAK_GBS = 8000.0
+
+
+def backbone_bytes(L: int) -> int:
+    return W_BB + KV_BB * L + KV_BB
+
+
+def cp_frame_bytes() -> int:
+    # 15 code-predictor steps attending to L = 2..16 (the reference's unit of work)
+    return sum(W_CP + KV_CP * L + KV_CP for L in range(2, 17))
+
+
+def frame_bytes(L: int = 512) -> int:
+    return backbone_bytes(L) + cp_frame_bytes()
+
+
+def cpu_baseline(sample_seconds: float = 15.0) -> dict:
+    """The frame through the oracle's HF-bf16 path on the host CPU, over a bounded sample."""
+    import torch
+    import __graft_entry__ as ge
+    from oracle.qtts_oracle import DecoderOracle, TalkerWeights, head_logits, sample_token, rb
+    pkg = ge.import_package()
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    sd = pkg.synthetic_state_dict(seed=1234)
+    tw = TalkerWeights.from_state_dict(sd, 28, 5)
+    bb = DecoderOracle(tw.bb_layers, tw.bb_norm, 520, "backbone", "hf_bf16")
+    cp = DecoderOracle(tw.cp_layers, tw.cp_norm, 17, "cp", "hf_bf16")
+    heads = [h.to(torch.bfloat16) for h in tw.cp_heads]
+    embs = [e.to(torch.bfloat16) for e in tw.cp_embeddings]
+    codec_head = tw.codec_head.to(torch.bfloat16)
+    g = torch.Generator().manual_seed(9)
+    bb.k[:, :, :511] = torch.randn(28, 8, 511, 128, generator=g).to(torch.bfloat16)
+    bb.v[:, :, :511] = torch.randn(28, 8, 511, 128, generator=g).to(torch.bfloat16)
+    hidden = torch.randn(1024, generator=g)
+    x = torch.randn(1024, generator=g).to(torch.bfloat16)
+
+    def frame(hidden, x):
+        cp.reset()
+        cp.step(rb(hidden).to(torch.bfloat16), pos=0)
+        h, _ = cp.step(tw.codec_embedding[5].to(torch.bfloat16), pos=1)
+        toks = []
+        for gi in range(15):
+            if gi:
+                h, _ = cp.step(embs[gi - 1][toks[-1]], pos=gi + 1)
+            toks.append(int(torch.argmax(torch.mv(heads[gi], h.to(torch.bfloat16)).float())))
+        hb, _ = bb.step(x, pos=511)
+        lg = torch.mv(codec_head, hb.to(torch.bfloat16)).float()
+        return hb, int(torch.argmax(lg))
+
+    frame(hidden, x)  # warm-up
+    n, t0 = 0, time.perf_counter()
+    while True:
+        frame(hidden, x)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= sample_seconds or n >= 50:
+            break
+    return {"value": n / el, "unit": "frames/s", "cores": threads, "kind": "port",
+            "sample": f"{n} frames (1 backbone step at 512 context + 16 code-predictor steps, HF-bf16 eager "
+                      f"PyTorch oracle) in {el:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X "
+              "(batch-1 decode runs on a single GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import __graft_entry__ as ge
+    pkg = ge.import_package()
+    assert torch.cuda.is_available(), "bench.py needs an MI355X"
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    sd = pkg.synthetic_state_dict(seed=1234, device="cuda")
+    bbg = pkg.TTSMegakernelGenerator(model=sd, max_seq_len=4096)
+    cpg = pkg.CodePredictorMegakernelGenerator(model=sd, max_seq_len=32)
+    bb, cp = bbg.decoder, cpg.decoder
+    g = torch.Generator(device="cuda").manual_seed(5)
+    k = torch.randn(28, 8, 511, 128, generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn(28, 8, 511, 128, generator=g, device="cuda").to(torch.bfloat16)
+    bb.set_kv_cache(k, v)
+    del k, v
+    i32 = dict(dtype=torch.int32, device="cuda")
+    g0 = torch.tensor([17], **i32)
+    done = torch.zeros(1, **i32)
+    hist = torch.zeros(1, **i32)
+    toks = torch.zeros(16, **i32)
+    comb = torch.empty(1024, dtype=torch.bfloat16, device="cuda")
+    text = torch.randn(1024, generator=g, device="cuda").to(torch.bfloat16)
+    bb.set_position(511)
+    bb.decode_step_select(text, g0, hist, 0, 1.0, -1, False, False, 1.0, 0, 1.0, 0, 0)
+    hidden = bb.hidden_state_buffer()
+
+    def one_frame(step):
+        cp.frame(hidden, g0, text, toks, comb, -1, done, False, 1.0, 0, 1.0, 0, step)
+        bb.set_position(511)
+        bb.decode_step_select(comb, g0, hist, 0, 1.0, -1, False, False, 1.0, 0, 1.0, 0, step + 1)
+
+    for i in range(args.warmup):
+        one_frame(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        one_frame(args.warmup + i)
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    bb.check_error()
+    cp.check_error()
+
+    # per-kernel durations with HIP events on the launch stream (torch's current stream)
+    n_ev = 30
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n_ev)]
+    for i in range(n_ev):
+        ev[i][0].record()
+        cp.frame(hidden, g0, text, toks, comb, -1, done, False, 1.0, 0, 1.0, 0, i)
+        ev[i][1].record()
+        bb.set_position(511)
+        bb.decode_step_select(comb, g0, hist, 0, 1.0, -1, False, False, 1.0, 0, 1.0, 0, i + 1)
+        ev[i][2].record()
+    torch.cuda.synchronize()
+    t_cp = sum(e[0].elapsed_time(e[1]) for e in ev) / n_ev * 1e-3
+    t_bb = sum(e[1].elapsed_time(e[2]) for e in ev) / n_ev * 1e-3
+    cp_gbs = cp_frame_bytes() / t_cp / 1e9
+    bb_gbs = backbone_bytes(512) / t_bb / 1e9
+    dominant = ("qtts_decode_kernel<false> (code-predictor frame)", cp_gbs, cp_frame_bytes()) if t_cp >= t_bb else \
+        ("qtts_decode_kernel<true> (backbone step, L=512)", bb_gbs, backbone_bytes(512))
+
+    fps = args.steps / el
+    out = {
+        "metric": "codec frames/s (1 backbone+15 CP steps), bs=1; % HBM roofline",
+        "value": round(fps, 2),
+        "unit": "frames/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1000 * el / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 weights, f64 accumulation",
+        "data": "synthetic (seeded random-init weights, random bf16 KV cache)",
+        "config": {"workload": "codec frame at 512 context: backbone 28 layers (L=512) + code predictor "
+                               "5 layers x 16 positions, 15 lm-heads; batch 1 (BASELINE configs[2] frame)",
+                   "global_batch": 1, "seq_len": 512, "parallelism": "none (1 GPU)"},
+        "frame_roofline_frac": round(fps * frame_bytes(512) / (HBM_PEAK_GBS * 1e9), 4),
+        "kernels_us": {"cp_frame": round(t_cp * 1e6, 2), "backbone_step": round(t_bb * 1e6, 2)},
+        "kernel_gbs": {"cp_frame": round(cp_gbs, 1), "backbone_step": round(bb_gbs, 1)},
+        "roofline": {"bound": "hbm", "kernel": dominant[0], "achieved": round(dominant[1], 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(dominant[1] / HBM_PEAK_GBS, 4),
+                     "algorithmic_bytes": dominant[2], "traffic": None},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -112,6 +112,12 @@ hipError_t qtts_workspace_init(void* workspace, int device);
  * *error_code = 0 when every wait completed; bit 0 = a wait timed out. */
 hipError_t qtts_workspace_check(void* workspace, unsigned int* error_code, hipStream_t stream);
 
+/* Diagnostics: when device_buffer is non-NULL (>= 256 * 1024 * 2 * 8 bytes), every later launch
+ * records, per workgroup and step, the s_memrealtime stamp (100 MHz) at which its poller wave
+ * (slot 1) and math waves (slot 0) finished the step: buffer[(wg * 1024 + step) * 2 + slot].
+ * NULL switches recording off. Not thread-safe against concurrent launches. */
+hipError_t qtts_debug_trace(void* device_buffer, size_t bytes);
+
 /* Token selection for one head (backbone g0 or a code-predictor group).
  * Mirrors generator.py:178-207: optional EOS suppression, greedy argmax (lowest index on
  * ties) or temperature -> top-k (ties with the k-th value kept) -> top-p (a value is kept

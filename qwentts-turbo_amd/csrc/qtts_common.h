@@ -73,16 +73,57 @@ __device__ __forceinline__ u32x4 ldw_nt(const bf16_t* p) {
 // ---------------------------------------------------------------------------------------
 // wave64 reductions
 // ---------------------------------------------------------------------------------------
+// Cross-lane exchange partners used by the group reductions (all VALU, no LDS traffic):
+//   step 0: quad_perm [1,0,3,2]   (lane ^ 1)
+//   step 1: quad_perm [2,3,0,1]   (lane ^ 2)
+//   step 2: row_half_mirror       (lane i <-> 7 - i within 8 lanes)
+//   step 3: row_mirror            (lane i <-> 15 - i within 16 lanes)
+//   step 4: v_permlane16_swap     (lane i <-> i + 16 within 32 lanes)
+//   step 5: v_permlane32_swap     (lane i <-> i + 32)
+// After step k every lane of its 2^(k+1)-lane group holds the same combined value.
+template <int STEP>
+__device__ __forceinline__ uint32_t xlane(uint32_t v) {
+  if constexpr (STEP == 0) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);
+  else if constexpr (STEP == 1) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);
+  else if constexpr (STEP == 2) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, false);
+  else if constexpr (STEP == 3) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, false);
+  else if constexpr (STEP == 4) { auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false); return r[0] ^ r[1] ^ v; }
+  else { auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false); return r[0] ^ r[1] ^ v; }
+}
+template <int STEP>
+__device__ __forceinline__ float xlane_f(float v) { return __uint_as_float(xlane<STEP>(__float_as_uint(v))); }
+template <int STEP>
+__device__ __forceinline__ double xlane_d(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint64_t r = (uint64_t)xlane<STEP>((uint32_t)u) | ((uint64_t)xlane<STEP>((uint32_t)(u >> 32)) << 32);
+  return __builtin_bit_cast(double, r);
+}
+template <int STEP, typename T>
+__device__ __forceinline__ T xlane_t(T v) {
+  if constexpr (sizeof(T) == 8) return xlane_d<STEP>(v); else return xlane_f<STEP>(v);
+}
+
+// Sum / max over aligned groups of WIDTH lanes (WIDTH in {16, 32, 64}); every lane of a group
+// receives the group's result.
 template <int WIDTH, typename T>
 __device__ __forceinline__ T group_sum(T v) {
-#pragma unroll
-  for (int o = 1; o < WIDTH; o <<= 1) v += __shfl_xor(v, o, 64);
+  v += xlane_t<0>(v);
+  v += xlane_t<1>(v);
+  v += xlane_t<2>(v);
+  v += xlane_t<3>(v);
+  if constexpr (WIDTH >= 32) v += xlane_t<4>(v);
+  if constexpr (WIDTH >= 64) v += xlane_t<5>(v);
   return v;
 }
 template <int WIDTH, typename T>
 __device__ __forceinline__ T group_max(T v) {
-#pragma unroll
-  for (int o = 1; o < WIDTH; o <<= 1) { const T u = __shfl_xor(v, o, 64); v = u > v ? u : v; }
+  T u;
+  u = xlane_t<0>(v); v = u > v ? u : v;
+  u = xlane_t<1>(v); v = u > v ? u : v;
+  u = xlane_t<2>(v); v = u > v ? u : v;
+  u = xlane_t<3>(v); v = u > v ? u : v;
+  if constexpr (WIDTH >= 32) { u = xlane_t<4>(v); v = u > v ? u : v; }
+  if constexpr (WIDTH >= 64) { u = xlane_t<5>(v); v = u > v ? u : v; }
   return v;
 }
 __device__ __forceinline__ double wave_sum_d(double v) { return group_sum<64>(v); }

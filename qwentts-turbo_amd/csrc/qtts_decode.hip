@@ -102,7 +102,9 @@ struct KArgs {
   bf16_t* out_combined;
   int* done;
   SelParams sel;
+  uint64_t* trace;         // optional step timeline: [wg][step][role] s_memrealtime stamps
 };
+constexpr int TRACE_STEPS = 1024;
 
 // LDS of one workgroup.
 struct Lds {
@@ -407,6 +409,45 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     }
   };
 
+  // ---- poller registers: small per-layer vectors, loaded a step (or a layer) before use so
+  // that no dependent global load sits on the critical path of a step.
+  //   g_in / g_post: RMSNorm gains of elements [16 lane, 16 lane + 16) (8 packed bf16 pairs)
+  //   qn/kn: q/k-norm gains of channels lane, lane + 64; rope: cos/sin of those channels
+  uint32_t g_in[8], g_post[8], g_fin[8];
+  float qn_l, qn_h, kn_l, kn_h, cl_, sl_, ch_, sh_;
+  auto load_gain16 = [&](uint32_t (&g)[8], const bf16_t* src) {
+    const u32x4 a0 = ldw(src + 16 * lane), a1 = ldw(src + 16 * lane + 8);
+    g[0] = a0.x; g[1] = a0.y; g[2] = a0.z; g[3] = a0.w; g[4] = a1.x; g[5] = a1.y; g[6] = a1.z; g[7] = a1.w;
+  };
+  auto load_qk_gains = [&](int layer) {
+    const bf16_t* qn = lw(LW, layer, W_QN);
+    const bf16_t* kn = lw(LW, layer, W_KN);
+    qn_l = bf2f(qn[lane]); qn_h = bf2f(qn[lane + 64]);
+    kn_l = bf2f(kn[lane]); kn_h = bf2f(kn[lane + 64]);
+  };
+  auto load_rope = [&](int pos) {
+    const int row = rot_row(lane, pos);
+    cl_ = bf2f(a.cos_t[(size_t)row * HDIM + lane]);
+    sl_ = bf2f(a.sin_t[(size_t)row * HDIM + lane]);
+    ch_ = bf2f(a.cos_t[(size_t)row * HDIM + lane + 64]);
+    sh_ = bf2f(a.sin_t[(size_t)row * HDIM + lane + 64]);
+  };
+  // RMSNorm of x (LDS, 1024 f32) with gains g: out[i] = f32((x_i * rstd) * g_i), f64 math
+  auto norm16 = [&](const float* x, float* out, const uint32_t (&g)[8], bool round_bf16) {
+    float xv[16];
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) { xv[j] = x[16 * lane + j]; ss = fma((double)xv[j], (double)xv[j], ss); }
+    ss = group_sum<64>(ss);
+    const double rstd = 1.0 / sqrt(ss / (double)HID + EPSD);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const double gj = (j & 1) ? (double)bfhi(g[j >> 1]) : (double)bflo(g[j >> 1]);
+      const float v = (float)(((double)xv[j] * rstd) * gj);
+      out[16 * lane + j] = round_bf16 ? rbf(v) : v;
+    }
+  };
+
   // ---- poller: input of layer 0 of position pi (embedding source) -> xres, xn
   auto prep_input0 = [&](int pi) {
     const bf16_t* src = nullptr;
@@ -421,11 +462,14 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     } else {
       src = a.in_emb != nullptr ? a.in_emb : a.embed_w + (size_t)a.in_tok * HID;
     }
-    if (src != nullptr)
-      for (int i = lane; i < HID; i += 64) s.xres[i] = bf2f(src[i]);
-    const double rstd = wave_rstd(s.xres);
-    const bf16_t* g = lw(LW, 0, W_LNIN);
-    for (int i = lane; i < HID; i += 64) s.xn[i] = norm_f32(s.xres[i], rstd, g[i]);
+    if (src != nullptr) {
+      const u32x4 a0 = ldw(src + 16 * lane), a1 = ldw(src + 16 * lane + 8);
+      const uint32_t w[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) { s.xres[16 * lane + 2 * j] = bflo(w[j]); s.xres[16 * lane + 2 * j + 1] = bfhi(w[j]); }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    norm16(s.xres, s.xn, g_in, false);
   };
 
   // ---- poller: AR2 of layer pass lp (down partials + residual) -> xl slots
@@ -443,46 +487,40 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     }
   };
   // ---- poller: next layer input (after ar2 of lp) -> xres, xn
-  auto prep_input_next = [&](int lp, int next_layer) {
+  auto prep_input_next = [&](int lp) {
     poll_vec<8>(P, ws->xl[xcd][lp & 1], HID, tag_of(lp, T_XL), s.xres);
-    const double rstd = wave_rstd(s.xres);
-    const bf16_t* g = lw(LW, next_layer, W_LNIN);
-    for (int i = lane; i < HID; i += 64) s.xn[i] = norm_f32(s.xres[i], rstd, g[i]);
+    norm16(s.xres, s.xn, g_in, false);
   };
   // ---- poller: final norm (after ar2 of lp) -> hb (bf16-rounded), outputs
   auto prep_final = [&](int lp) {
     poll_vec<8>(P, ws->xl[xcd][lp & 1], HID, tag_of(lp, T_XL), s.xres);
-    const double rstd = wave_rstd(s.xres);
-    for (int i = lane; i < HID; i += 64) {
-      const float h = norm_f32(s.xres[i], rstd, a.final_norm[i]);
-      s.hb[i] = rbf(h);
-      if (wg == 0) {
-        if (a.out_hidden) a.out_hidden[i] = h;
+    norm16(s.xres, s.hb, g_fin, false);
+    if (wg == 0) {
+      for (int i = lane; i < HID; i += 64) {
+        if (a.out_hidden) a.out_hidden[i] = s.hb[i];
         if (a.out_residual) {
           if constexpr (BB) reinterpret_cast<bf16_t*>(a.out_residual)[i] = f2bf(s.xres[i]);
           else reinterpret_cast<float*>(a.out_residual)[i] = s.xres[i];
         }
       }
     }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) s.hb[16 * lane + j] = rbf(s.hb[16 * lane + j]);
   };
   // ---- poller: q/k norm, RoPE, KV write for layer `layer` at position pos
   auto prep_att = [&](int lp, int layer, int pos, int C) {
     const int par = lp & 1;
     poll_vec<4>(P, ws->qkv[xcd][par], LROWS, tag_of(lp, T_QKV), s.stage);
-    const bf16_t* qn = lw(LW, layer, W_QN);
-    const bf16_t* kn = lw(LW, layer, W_KN);
     const int c = lane;  // channels c and c + 64
-    const int row = rot_row(c, pos);
-    const double cl = bf2f(a.cos_t[(size_t)row * HDIM + c]), sl = bf2f(a.sin_t[(size_t)row * HDIM + c]);
-    const double ch = bf2f(a.cos_t[(size_t)row * HDIM + c + 64]), sh = bf2f(a.sin_t[(size_t)row * HDIM + c + 64]);
+    const double cl = cl_, sl = sl_, ch = ch_, sh = sh_;
     float outl[3], outh[3];
 #pragma unroll
     for (int h = 0; h < 3; ++h) {
       const double xl_ = s.stage[128 * h + c], xh = s.stage[128 * h + c + 64];
       const double ss = group_sum<64>(fma(xl_, xl_, xh * xh));
       const double r = 1.0 / sqrt(ss / (double)HDIM + EPSD);
-      const bf16_t* gn = h < 2 ? qn : kn;
-      const double nl = (xl_ * r) * (double)bf2f(gn[c]), nh = (xh * r) * (double)bf2f(gn[c + 64]);
+      const double gl = h < 2 ? qn_l : kn_l, gh = h < 2 ? qn_h : kn_h;
+      const double nl = (xl_ * r) * gl, nh = (xh * r) * gh;
       outl[h] = (float)(nl * cl - nh * sl);
       outh[h] = (float)(nl * sh + nh * ch);
     }
@@ -517,15 +555,20 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     for (int h = 0; h < 2; ++h) {
       float M = -INFINITY;
       for (int c = 0; c < C; ++c) M = fmaxf(M, s.stage[c * APS + 256 + 2 * h]);
+      double wc[MAXC];
       double Z = 0.0;
-      for (int c = 0; c < C; ++c)
-        Z += (double)s.stage[c * APS + 257 + 2 * h] * exp((double)s.stage[c * APS + 256 + 2 * h] - (double)M);
+#pragma unroll
+      for (int c = 0; c < MAXC; ++c) {
+        wc[c] = c < C ? exp((double)s.stage[c * APS + 256 + 2 * h] - (double)M) : 0.0;
+        if (c < C) Z += (double)s.stage[c * APS + 257 + 2 * h] * wc[c];
+      }
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int d = lane + 64 * j;
         double acc = 0.0;
-        for (int c = 0; c < C; ++c)
-          acc += (double)s.stage[c * APS + 128 * h + d] * exp((double)s.stage[c * APS + 256 + 2 * h] - (double)M);
+#pragma unroll
+        for (int c = 0; c < MAXC; ++c)
+          if (c < C) acc += (double)s.stage[c * APS + 128 * h + d] * wc[c];
         s.attn[128 * h + d] = (float)(acc / Z);
       }
     }
@@ -542,9 +585,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       put_local(&ws->h1[xcd][par][32 * li + lane], (float)acc, tag_of(lp, T_H1));
     }
     poll_vec<8>(P, ws->h1[xcd][par], HID, tag_of(lp, T_H1), s.h1res);
-    const double rstd = wave_rstd(s.h1res);
-    const bf16_t* g = lw(LW, layer, W_LNPOST);
-    for (int i = lane; i < HID; i += 64) s.hn[i] = norm_f32(s.h1res[i], rstd, g[i]);
+    norm16(s.h1res, s.hn, g_post, false);
   };
   auto prep_down = [&](int lp) {
     poll_vec<3>(P, ws->inter[xcd][lp & 1], XI, tag_of(lp, T_INTER), s.inter);
@@ -574,45 +615,61 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           if (nsb > 1) load_kv<BB>(tk, a, layer, xcd, b0, c1 < Lold ? c1 : Lold, mw, lane);
         }
         const TileKV& t = tk;
+        // scores of this lane group's JJ positions (f32-rounded), then one rescale
+        double sc[JJ];
+        double mloc = -INFINITY;
 #pragma unroll
         for (int jj = 0; jj < JJ; ++jj) {
           const int pos = b0 + 4 * JJ * mw + 4 * jj + (lane >> 4);
-          const bool valid = pos < c1;
-          float kv[8], vv[8];
+          float kv[8];
           if (pos == Lold) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) { kv[i] = s.knew[d0 + i]; vv[i] = s.vnew[d0 + i]; }
+            for (int i = 0; i < 8; ++i) kv[i] = s.knew[d0 + i];
           } else {
             unpack8<BB>(t, true, jj, kv);
-            unpack8<BB>(t, false, jj, vv);
           }
           double dd = 0.0;
 #pragma unroll
           for (int i = 0; i < 8; ++i) dd = fma((double)qv[i], (double)kv[i], dd);
           dd = group_sum<16>(dd);
-          const double sc = valid ? (double)(float)(dd * scale) : -INFINITY;
-          const double mn = sc > m ? sc : m;
-          if (mn != -INFINITY) {
-            const double alpha = exp(m - mn);
-            const double p = exp(sc - mn);
-            l = l * alpha + p;
+          sc[jj] = pos < c1 ? (double)(float)(dd * scale) : -INFINITY;
+          mloc = sc[jj] > mloc ? sc[jj] : mloc;
+        }
+        const double mn = mloc > m ? mloc : m;
+        if (mn != -INFINITY) {
+          const double alpha = m == -INFINITY ? 0.0 : exp(m - mn);
+          l *= alpha;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) acc[i] = fma(p, (double)vv[i], acc[i] * alpha);
-            m = mn;
+          for (int i = 0; i < 8; ++i) acc[i] *= alpha;
+#pragma unroll
+          for (int jj = 0; jj < JJ; ++jj) {
+            const int pos = b0 + 4 * JJ * mw + 4 * jj + (lane >> 4);
+            const double p = sc[jj] == -INFINITY ? 0.0 : exp(sc[jj] - mn);
+            float vv[8];
+            if (pos == Lold) {
+#pragma unroll
+              for (int i = 0; i < 8; ++i) vv[i] = s.vnew[d0 + i];
+            } else {
+              unpack8<BB>(t, false, jj, vv);
+            }
+            l += p;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i] = fma(p, (double)vv[i], acc[i]);
           }
+          m = mn;
         }
       }
       // merge the 4 lane groups (xor 16, 32); the 4 waves are merged through LDS below
       const double M = group_max<64>(m);
       const double f = (m == -INFINITY) ? 0.0 : exp(m - M);
       double lt = l * f;
-      lt += __shfl_xor(lt, 16, 64);
-      lt += __shfl_xor(lt, 32, 64);
+      lt += xlane_d<4>(lt);
+      lt += xlane_d<5>(lt);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         double v = acc[i] * f;
-        v += __shfl_xor(v, 16, 64);
-        v += __shfl_xor(v, 32, 64);
+        v += xlane_d<4>(v);
+        v += xlane_d<5>(v);
         acc[i] = v;
       }
       if (lane < 16)
@@ -769,18 +826,24 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   // weight loads needed two steps later.
   // =====================================================================================
   enum Step { S_PRO, S_QKV, S_ATT, S_O, S_GU, S_DOWN, S_HEAD };
+  int nstep = 0;
+  auto stamp = [&]() {
+    if (a.trace != nullptr && lane == 0 && (poller || mw == 0) && nstep < TRACE_STEPS)
+      a.trace[((size_t)wg * TRACE_STEPS + nstep) * 2 + (poller ? 1 : 0)] = __builtin_amdgcn_s_memrealtime();
+    ++nstep;
+  };
   auto walk = [&](auto&& act) {
-    act(S_PRO, 0, 0);
+    act(S_PRO, 0, 0); stamp();
     step_barrier();
     for (int pi = 0; pi < a.n_pos; ++pi) {
       for (int layer = 0; layer < NL; ++layer) {
-        act(S_QKV, pi, layer); step_barrier();
-        act(S_ATT, pi, layer); step_barrier();
-        act(S_O, pi, layer); step_barrier();
-        act(S_GU, pi, layer); step_barrier();
-        act(S_DOWN, pi, layer); step_barrier();
+        act(S_QKV, pi, layer); stamp(); step_barrier();
+        act(S_ATT, pi, layer); stamp(); step_barrier();
+        act(S_O, pi, layer); stamp(); step_barrier();
+        act(S_GU, pi, layer); stamp(); step_barrier();
+        act(S_DOWN, pi, layer); stamp(); step_barrier();
       }
-      if (has_head(pi)) { act(S_HEAD, pi, NL - 1); step_barrier(); }
+      if (has_head(pi)) { act(S_HEAD, pi, NL - 1); stamp(); step_barrier(); }
     }
   };
   struct PosInfo { int pos, L, C, P, c0, c1; bool last_pos, head; };
@@ -808,16 +871,34 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     walk([&](int st, int pi, int layer) {
       const PosInfo q = pinfo(pi);
       const int lp = pi * NL + layer;
+      const int nl = layer + 1 < NL ? layer + 1 : 0;   // next layer pass (wraps to the next position)
       switch (st) {
-        case S_PRO: prep_input0(0); break;
-        case S_QKV: prep_att(lp, layer, q.pos, q.C); break;
+        case S_PRO:
+          load_gain16(g_in, lw(LW, 0, W_LNIN));
+          load_gain16(g_post, lw(LW, 0, W_LNPOST));
+          load_gain16(g_fin, a.final_norm);
+          load_qk_gains(0);
+          load_rope(q.pos);
+          prep_input0(0);
+          load_gain16(g_in, lw(LW, NL > 1 ? 1 : 0, W_LNIN));
+          break;
+        case S_QKV:
+          prep_att(lp, layer, q.pos, q.C);
+          load_qk_gains(nl);
+          if (layer == NL - 1 && !q.last_pos) load_rope(q.pos + 1);
+          break;
         case S_ATT: prep_o(lp, q.C); break;
-        case S_O: prep_gu(lp, layer); break;
+        case S_O:
+          prep_gu(lp, layer);
+          load_gain16(g_post, lw(LW, nl, W_LNPOST));
+          break;
         case S_GU: prep_down(lp); break;
         case S_DOWN:
-          if (layer < NL - 1) { ar2(lp); prep_input_next(lp, layer + 1); }
+          if (layer < NL - 1) { ar2(lp); prep_input_next(lp); }
           else if (q.head || q.last_pos) { ar2(lp); prep_final(lp); }
           else prep_input0(pi + 1);
+          // g_in now serves the layer after next
+          if (layer < NL - 1 || !(q.head || q.last_pos)) load_gain16(g_in, lw(LW, (nl + 1) % NL, W_LNIN));
           break;
         case S_HEAD:
           if (a.cp_frame || wg == 0) {
@@ -825,7 +906,10 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
             if (a.cp_frame) {
               if (lane == 0) s.tok[pi - 1] = tok;
               __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-              if (!q.last_pos) prep_input0(pi + 1);
+              if (!q.last_pos) {
+                prep_input0(pi + 1);
+                load_gain16(g_in, lw(LW, NL > 1 ? 1 : 0, W_LNIN));
+              }
             } else if (lane == 0 && a.out_token) {
               *a.out_token = tok;
             }
@@ -934,6 +1018,7 @@ std::mutex g_mu;
 std::unordered_map<int, DeviceCheck> g_dev;
 std::unordered_map<const void*, uint32_t> g_seq;   // launch sequence per workspace
 std::unordered_map<int, void*> g_lib_ws;           // library-owned workspace per device
+uint64_t* g_trace = nullptr;                       // optional step timeline buffer
 
 __global__ void xcc_probe_kernel(int* out) {
   if (threadIdx.x == 0) out[blockIdx.x] = (int)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15u);
@@ -1003,6 +1088,7 @@ hipError_t launch(bool bb, KArgs& a, hipStream_t stream) {
   a.tag_base = next_tag_base(a.ws, stream, &ze);
   if (ze != hipSuccess) return ze;
   a.spin_cap = kSpinCap;
+  a.trace = g_trace;
   void* args[] = {&a};
   const void* fn = bb ? (const void*)qtts::qtts_decode_kernel<true> : (const void*)qtts::qtts_decode_kernel<false>;
   return hipLaunchCooperativeKernel(fn, dim3(qtts::NWG), dim3(qtts::NTHR), args, 0, stream);
@@ -1105,6 +1191,14 @@ hipError_t launch_cp_decode_with_embedding(const void* input_embedding, const CP
 }
 
 size_t qtts_workspace_bytes(void) { return sizeof(Workspace); }
+
+hipError_t qtts_debug_trace(void* device_buffer, size_t bytes) {
+  if (device_buffer != nullptr && bytes < (size_t)qtts::NWG * qtts::TRACE_STEPS * 2 * sizeof(uint64_t))
+    return hipErrorInvalidValue;
+  std::lock_guard<std::mutex> lk(g_mu);
+  g_trace = reinterpret_cast<uint64_t*>(device_buffer);
+  return hipSuccess;
+}
 
 hipError_t qtts_workspace_init(void* workspace, int device) {
   if (workspace == nullptr || (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return hipErrorInvalidValue;
