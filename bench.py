@@ -33,6 +33,11 @@ KV_BB = 28 * 8 * 128 * 2 * 2                  # bf16 K+V bytes per attended toke
 KV_CP = 5 * 8 * 128 * 4 * 2                   # f32 K+V bytes per attended token
 HBM_PEAK_GBS = 8000.0
 
+# HBM bytes per launch measured with rocprofv3 PMC counters on the same workload
+# (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000 KiB, both factors from a plain 512 MiB device copy);
+# the summary with the commands is profiles/qtts_decode_kernel_frame512_pmc_traffic.md.
+PMC_TRAFFIC = {"cp_frame": 2_816_874_680, "backbone_step": 1_008_896_563}
+
 
 def backbone_bytes(L: int) -> int:
     return W_BB + KV_BB * L + KV_BB
@@ -87,7 +92,7 @@ def cpu_baseline(sample_seconds: float = 15.0) -> dict:
         frame(hidden, x)
         n += 1
         el = time.perf_counter() - t0
-        if el >= sample_seconds or n >= 50:
+        if el >= sample_seconds or n >= 500:
             break
     return {"value": n / el, "unit": "frames/s", "cores": threads, "kind": "port",
             "sample": f"{n} frames (1 backbone step at 512 context + 16 code-predictor steps, HF-bf16 eager "
@@ -101,10 +106,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run 5 plain device-to-device copies of MIB MiB (the reference kernel for "
+                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X "
-              "(batch-1 decode runs on a single GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
+              "(batch-1 decode of one stream runs on a single GPU; streams shard one per GPU)", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -113,6 +121,15 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs an MI355X"
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src = torch.ones(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "copies": 5}), flush=True)
+        return
 
     sd = pkg.synthetic_state_dict(seed=1234, device="cuda")
     bbg = pkg.TTSMegakernelGenerator(model=sd, max_seq_len=4096)
@@ -165,8 +182,9 @@ def main():
     t_bb = sum(e[1].elapsed_time(e[2]) for e in ev) / n_ev * 1e-3
     cp_gbs = cp_frame_bytes() / t_cp / 1e9
     bb_gbs = backbone_bytes(512) / t_bb / 1e9
-    dominant = ("qtts_decode_kernel<false> (code-predictor frame)", cp_gbs, cp_frame_bytes()) if t_cp >= t_bb else \
-        ("qtts_decode_kernel<true> (backbone step, L=512)", bb_gbs, backbone_bytes(512))
+    dominant = ("qtts_decode_kernel<false> (code-predictor frame)", cp_gbs, cp_frame_bytes(), PMC_TRAFFIC["cp_frame"]) \
+        if t_cp >= t_bb else \
+        ("qtts_decode_kernel<true> (backbone step, L=512)", bb_gbs, backbone_bytes(512), PMC_TRAFFIC["backbone_step"])
 
     fps = args.steps / el
     out = {
@@ -187,10 +205,14 @@ def main():
                    "global_batch": 1, "seq_len": 512, "parallelism": "none (1 GPU)"},
         "frame_roofline_frac": round(fps * frame_bytes(512) / (HBM_PEAK_GBS * 1e9), 4),
         "kernels_us": {"cp_frame": round(t_cp * 1e6, 2), "backbone_step": round(t_bb * 1e6, 2)},
+        "backbone_steps_per_s": round(1.0 / t_bb, 1),
+        "backbone_roofline_frac": round(bb_gbs / HBM_PEAK_GBS, 4),
+        "cp_steps_per_s": round(15.0 / t_cp, 1),
+        "cp_roofline_frac": round(cp_gbs / HBM_PEAK_GBS, 4),
         "kernel_gbs": {"cp_frame": round(cp_gbs, 1), "backbone_step": round(bb_gbs, 1)},
         "roofline": {"bound": "hbm", "kernel": dominant[0], "achieved": round(dominant[1], 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(dominant[1] / HBM_PEAK_GBS, 4),
-                     "algorithmic_bytes": dominant[2], "traffic": None},
+                     "algorithmic_bytes": dominant[2], "traffic": dominant[3]},
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

@@ -44,8 +44,11 @@ def philox4x64_10(ctr, key):
 
 
 def uniform_from_word(w):
-    """Map a 64-bit word to a double in the open interval (0, 1): ((w >> 11) + 0.5) * 2**-53."""
-    return ((int(w) >> 11) + 0.5) * (1.0 / 9007199254740992.0)
+    """Map a 64-bit word to a double in the open interval (0, 1): ((w >> 12) + 0.5) * 2**-52.
+
+    The top 52 bits plus one half fit a double's 53-bit significand exactly, so no word maps
+    to 0 or 1 (with 53 bits, (2**53 - 1) + 0.5 would round up to 2**53 and give u = 1)."""
+    return ((int(w) >> 12) + 0.5) * (1.0 / 4503599627370496.0)
 
 
 # Sampler stream layout shared with the device code: one Philox block per 4 vocabulary ids.

@@ -161,6 +161,33 @@ def r32(x: torch.Tensor) -> torch.Tensor:
     return x.to(torch.float32).to(torch.float64)
 
 
+def split_attention(q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, scale: float, sub: int,
+                    R=lambda t: t) -> torch.Tensor:
+    """Decode attention split over sequence chunks and merged (split-K softmax).
+
+    q [h, d], K/V [h, L, d] (f64). The sequence is cut as ``chunking(L, sub)``; chunk c keeps
+    its max m_c, its sum l_c = sum exp(s - m_c) and its unnormalised output acc_c; the merge
+    rescales by exp(m_c - M) with M the global max (the LDS split-K combine of
+    fused_decode_tts.cu:282-385, here over up to 8 chunks). ``R`` is applied where the kernels
+    store f32: the scores, l_c, acc_c and the merged output.
+    """
+    L = K.shape[1]
+    scores = R(torch.einsum("hd,hpd->hp", q, K) * scale)
+    C, P = chunking(L, sub)
+    ms, ls, accs = [], [], []
+    for c in range(C):
+        sl = slice(c * P, min((c + 1) * P, L))
+        m_c = scores[:, sl].max(dim=-1).values
+        p = torch.exp(scores[:, sl] - m_c[:, None])
+        ms.append(m_c)
+        ls.append(R(p.sum(-1)))
+        accs.append(R(torch.einsum("hp,hpd->hd", p, V[:, sl])))
+    M = torch.stack(ms).max(dim=0).values
+    wts = [torch.exp(m - M) for m in ms]
+    Z = sum(wc * lc for wc, lc in zip(wts, ls))
+    return R(sum(wc[:, None] * ac for wc, ac in zip(wts, accs)) / Z[:, None])
+
+
 def r16(x: torch.Tensor) -> torch.Tensor:
     """Round an f64 tensor to f32, then to bf16 (the kernels' double rounding), back to f64."""
     return x.to(torch.float32).to(torch.bfloat16).to(torch.float64)
@@ -279,20 +306,8 @@ class DecoderOracle:
             attn = torch.einsum("hp,hpd->hd", torch.softmax(scores, dim=-1), V[kv_of_q]).reshape(-1)
             h1 = r + w.o @ attn
         else:
-            scores = r32(torch.einsum("hd,hpd->hp", q, K[kv_of_q]) * SCALE_F32)
-            C, P = chunking(L, SUB_BB if self.kind == "backbone" else SUB_CP)
-            ms, ls, accs = [], [], []
-            for c in range(C):
-                sl = slice(c * P, min((c + 1) * P, L))
-                m_c = scores[:, sl].max(dim=-1).values                       # f32 values
-                p = torch.exp(scores[:, sl] - m_c[:, None])
-                ms.append(m_c)
-                ls.append(r32(p.sum(-1)))
-                accs.append(r32(torch.einsum("hp,hpd->hd", p, V[kv_of_q][:, sl])))
-            M = torch.stack(ms).max(dim=0).values
-            wts = [torch.exp(m - M) for m in ms]
-            Z = sum(wc * lc for wc, lc in zip(wts, ls))
-            attn = R(sum(wc[:, None] * ac for wc, ac in zip(wts, accs)) / Z[:, None]).reshape(-1)
+            attn = split_attention(q, K[kv_of_q], V[kv_of_q], SCALE_F32,
+                                   SUB_BB if self.kind == "backbone" else SUB_CP, r32).reshape(-1)
             # O projection as 8 per-XCD partials (XCD x: heads 2x, 2x+1 = columns [256x, 256x+256))
             cols = attn.numel() // 8
             h1 = r.clone()
@@ -427,19 +442,39 @@ def apply_repetition_penalty(logits: torch.Tensor, history: Sequence[int], penal
 
 
 def filter_logits(logits: torch.Tensor, temperature: float, top_k: int, top_p: float) -> torch.Tensor:
-    """Temperature, top-k (keeps ties with the k-th value) and top-p, as generator.py:189-204."""
+    """Temperature, top-k and top-p filtering (generator.py:189-204); dropped ids become -inf.
+
+    * temperature: f32 division, as ``logits / temperature`` on f32 logits.
+    * top-k keeps every value >= the k-th largest, ties included (generator.py:192-194).
+    * top-p keeps x when the softmax mass of the strictly larger kept values is <= top_p,
+      with probabilities exp(s - max) summed in f64. On distinct values this is the
+      reference's sort / cumsum / shift-by-one rule (generator.py:197-204: position i of the
+      descending order survives iff cumprobs[i-1] <= top_p); on exact ties it keeps every
+      tied value, which makes the kept set independent of sort order.
+    """
     scaled = logits.to(torch.float32) / temperature
-    if top_k > 0:
-        kth = torch.topk(scaled, min(top_k, scaled.numel()))[0][-1]
+    if top_k > 0 and top_k < scaled.numel():
+        kth = torch.topk(scaled, top_k)[0][-1]
         scaled = torch.where(scaled < kth, torch.full_like(scaled, float("-inf")), scaled)
     if top_p < 1.0:
-        vals, idx = torch.sort(scaled, descending=True, stable=True)
-        cum = torch.cumsum(torch.softmax(vals.double(), dim=-1), dim=-1)
-        remove = cum > top_p
-        remove[1:] = remove[:-1].clone()
-        remove[0] = False
-        vals = torch.where(remove, torch.full_like(vals, float("-inf")), vals)
-        scaled = torch.empty_like(scaled).scatter_(0, idx, vals)
+        s = scaled.double()
+        fin = torch.isfinite(s)
+        m = s[fin].max()
+        p = torch.where(fin, torch.exp(s - m), torch.zeros_like(s))
+        z = float(p.sum())
+        order = torch.argsort(s, descending=True, stable=True)
+        sv, pv = s[order], p[order]
+        keep = torch.zeros_like(fin)
+        acc, i, n = 0.0, 0, s.numel()
+        while i < n and torch.isfinite(sv[i]):
+            j = i
+            while j < n and sv[j] == sv[i]:
+                j += 1
+            if acc <= float(torch.tensor(top_p, dtype=torch.float32).double()) * z:
+                keep[order[i:j]] = True
+            acc += float(pv[i:j].sum())
+            i = j
+        scaled = torch.where(keep, scaled, torch.full_like(scaled, float("-inf")))
     return scaled
 
 

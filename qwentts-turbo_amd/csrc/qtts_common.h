@@ -191,7 +191,8 @@ __device__ bool poll_slots(const uint64_t* buf, int n, uint32_t tag, float* dst,
 // ---------------------------------------------------------------------------------------
 // Philox-4x64-10 (Salmon et al., SC'11) and the sampler's uniform draw.
 // Stream layout: key = (seed, "QTTSAFMP"), counter = (vocab_id / 4, frame_step, group, 0),
-// word = vocab_id % 4, u = ((word >> 11) + 0.5) * 2^-53.
+// word = vocab_id % 4, u = ((word >> 12) + 0.5) * 2^-52: the sum is exact (53 bits), so
+// u lies strictly inside (0, 1) for every word.
 // ---------------------------------------------------------------------------------------
 __device__ __forceinline__ void philox4x64_10(uint64_t c[4], uint64_t k0, uint64_t k1) {
   const uint64_t M0 = 0xD2E7470EE14C6C93ull, M1 = 0xCA5A826395121157ull;
@@ -208,7 +209,7 @@ __device__ __forceinline__ void philox4x64_10(uint64_t c[4], uint64_t k0, uint64
 __device__ __forceinline__ double sampler_uniform(uint64_t seed, int frame_step, int group, int vid) {
   uint64_t c[4] = {(uint64_t)(vid >> 2), (uint64_t)(uint32_t)frame_step, (uint64_t)(uint32_t)group, 0ull};
   philox4x64_10(c, seed, 0x5154545341464D50ull);
-  return ((double)(c[vid & 3] >> 11) + 0.5) * (1.0 / 9007199254740992.0);
+  return ((double)(c[vid & 3] >> 12) + 0.5) * (1.0 / 4503599627370496.0);
 }
 
 // Order-preserving map float -> uint32 (larger float, larger key).

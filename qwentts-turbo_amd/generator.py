@@ -10,7 +10,7 @@ Mirrors /root/reference/qwentts_turbo/generator.py:21-362 and keeps ``generate()
 The host enqueues frames without waiting and checks the EOS flag every ``sync_every`` frames
 (the reference synchronises 16 times per frame through ``.item()``).
 
-Differences (by design, see DESIGN.md of the repository):
+Differences (by design):
   * sampling draws with Gumbel-max over Philox-4x64-10 noise instead of torch.multinomial
     (same distribution; reproducible on device). Greedy decoding is unchanged.
   * the prefill runs the backbone decode kernel token by token (kernel precision), not the

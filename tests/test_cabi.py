@@ -1,0 +1,56 @@
+"""The C-ABI library and the torch extension load, and export every entry point the public
+header declares (CPU only: nothing is launched)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "qwentts_amd.h"
+LIB = ROOT / "qwentts-turbo_amd" / "lib" / "libqwentts_amd.so"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    body = text[text.index('extern "C" {'):]
+    return re.findall(r"^(?:hipError_t|size_t|void|int)\s+(\w+)\s*\(", body, flags=re.M)
+
+
+def test_header_declares_reference_launchers():
+    names = declared_functions()
+    for ref in ("launch_tts_decode", "launch_tts_decode_with_embedding", "launch_cp_decode_with_embedding"):
+        assert ref in names
+    assert len(names) == len(set(names)) >= 9
+
+
+def test_library_exports_every_declared_symbol():
+    if not LIB.exists():
+        pytest.skip("libqwentts_amd.so is not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(str(LIB))
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_workspace_bytes_is_callable_without_a_gpu():
+    """qtts_workspace_bytes is a pure size query (no HIP call)."""
+    if not LIB.exists():
+        pytest.skip("libqwentts_amd.so is not built")
+    lib = ctypes.CDLL(str(LIB))
+    lib.qtts_workspace_bytes.restype = ctypes.c_size_t
+    n = lib.qtts_workspace_bytes()
+    assert 0 < n < 8 << 20 and n % 256 == 0
+
+
+def test_torch_extension_exposes_reference_classes(pkg):
+    ext = pkg._ext.load()
+    for cls, methods in {
+        "MegakernelTTSDecoder": ("decode_step", "decode_step_with_argmax", "decode_step_with_embedding", "reset",
+                                 "position", "set_position", "get_hidden_states", "get_k_cache", "get_v_cache",
+                                 "set_kv_cache"),
+        "MegakernelCodePredictorDecoder": ("decode_step_with_embedding", "reset", "position", "set_position",
+                                           "get_hidden_states", "set_kv_cache"),
+    }.items():
+        c = getattr(ext, cls)
+        for m in methods:
+            assert hasattr(c, m), (cls, m)
