@@ -140,7 +140,7 @@ def rope_apply(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.T
 EPS_F32 = float(torch.tensor(1e-6, dtype=torch.float32))   # the reference's 1e-6f
 SCALE_F32 = float(torch.tensor(1.0 / math.sqrt(128.0), dtype=torch.float32))  # attn_scale (f32)
 MAX_CHUNKS = 8      # attention chunks per KV head in the kernels
-SUB_BB, SUB_CP = 64, 32
+SUB_BB, SUB_CP = 64, 2   # chunking granularity (positions per chunk before the 8-chunk cap)
 
 
 def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
@@ -168,8 +168,9 @@ def split_attention(q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, scale: fl
     q [h, d], K/V [h, L, d] (f64). The sequence is cut as ``chunking(L, sub)``; chunk c keeps
     its max m_c, its sum l_c = sum exp(s - m_c) and its unnormalised output acc_c; the merge
     rescales by exp(m_c - M) with M the global max (the LDS split-K combine of
-    fused_decode_tts.cu:282-385, here over up to 8 chunks). ``R`` is applied where the kernels
-    store f32: the scores, l_c, acc_c and the merged output.
+    fused_decode_tts.cu:282-385, here over up to 8 chunks): out = (sum_c acc_c w_c) * (1 / Z),
+    Z = sum_c l_c w_c. ``R`` is applied where the kernels store f32: the scores, l_c, acc_c and
+    the merged output.
     """
     L = K.shape[1]
     scores = R(torch.einsum("hd,hpd->hp", q, K) * scale)
@@ -184,8 +185,8 @@ def split_attention(q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, scale: fl
         accs.append(R(torch.einsum("hp,hpd->hd", p, V[:, sl])))
     M = torch.stack(ms).max(dim=0).values
     wts = [torch.exp(m - M) for m in ms]
-    Z = sum(wc * lc for wc, lc in zip(wts, ls))
-    return R(sum(wc[:, None] * ac for wc, ac in zip(wts, accs)) / Z[:, None])
+    Z = sum(lc * wc for wc, lc in zip(wts, ls))
+    return R(sum(ac * wc[:, None] for wc, ac in zip(wts, accs)) * (1.0 / Z)[:, None])
 
 
 def r16(x: torch.Tensor) -> torch.Tensor:

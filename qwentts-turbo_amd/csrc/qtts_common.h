@@ -65,9 +65,17 @@ __device__ __forceinline__ double dot8d(const u32x4 w, const double* x, double a
   return acc;
 }
 
-__device__ __forceinline__ u32x4 ldw(const bf16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+// Global-address-space view of a device pointer. Loads through it compile to global_load
+// (counted by vmcnt only); loads through a generic pointer compile to flat_load, which also
+// counts against lgkmcnt, so every LDS wait would also wait for the weight prefetches.
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* gmem(const T* p) {
+  return (const __attribute__((address_space(1))) T*)p;
+}
+__device__ __forceinline__ u32x4 ldw(const bf16_t* p) { return *gmem(reinterpret_cast<const u32x4*>(p)); }
+__device__ __forceinline__ float ldbf(const bf16_t* p) { return bf2f(*gmem(p)); }
 __device__ __forceinline__ u32x4 ldw_nt(const bf16_t* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return __builtin_nontemporal_load(gmem(reinterpret_cast<const u32x4*>(p)));
 }
 
 // ---------------------------------------------------------------------------------------
@@ -98,9 +106,14 @@ __device__ __forceinline__ double xlane_d(double v) {
   const uint64_t r = (uint64_t)xlane<STEP>((uint32_t)u) | ((uint64_t)xlane<STEP>((uint32_t)(u >> 32)) << 32);
   return __builtin_bit_cast(double, r);
 }
+// a pair of doubles reduced together (e.g. a gate and an up projection of one row)
+struct d2 { double a, b; };
+__device__ __forceinline__ d2 operator+(d2 x, d2 y) { return d2{x.a + y.a, x.b + y.b}; }
 template <int STEP, typename T>
 __device__ __forceinline__ T xlane_t(T v) {
-  if constexpr (sizeof(T) == 8) return xlane_d<STEP>(v); else return xlane_f<STEP>(v);
+  if constexpr (sizeof(T) == 16) return T{xlane_d<STEP>(v.a), xlane_d<STEP>(v.b)};
+  else if constexpr (sizeof(T) == 8) return xlane_d<STEP>(v);
+  else return xlane_f<STEP>(v);
 }
 
 // Sum / max over aligned groups of WIDTH lanes (WIDTH in {16, 32, 64}); every lane of a group
@@ -127,6 +140,60 @@ __device__ __forceinline__ T group_max(T v) {
   return v;
 }
 __device__ __forceinline__ double wave_sum_d(double v) { return group_sum<64>(v); }
+// Reduce-scatter sum of N values (N a power of two) over aligned groups of 2^(STEP+1) lanes.
+// At each of the first log2(N) steps the lane keeps half of its values (the lower half when
+// its STEP bit is 0) and adds the partner's copy of that half, received in one exchange per
+// kept value; the remaining steps sum the single value left. On return every lane holds the
+// group total of value k = sum over the split steps s of bit_s(lane) * (count at s) / 2,
+// e.g. N = 4 over 64 lanes: k = 2 * bit5 + bit4. The exchange partners are those of xlane.
+template <int STEP, int N, typename T>
+__device__ __forceinline__ T rs_sum(const T (&c)[N], int lane) {
+  if constexpr (STEP < 0) {
+    return c[0];
+  } else if constexpr (N == 1) {
+    T v = c[0];
+    v = v + xlane_t<STEP>(v);
+    if constexpr (STEP > 0) {
+      const T o[1] = {v};
+      return rs_sum<STEP - 1, 1>(o, lane);
+    } else {
+      return v;
+    }
+  } else {
+    constexpr int H = N / 2;
+    const bool hi = (lane >> STEP) & 1;
+    T o[H];
+#pragma unroll
+    for (int j = 0; j < H; ++j) {
+      const T send = hi ? c[j] : c[H + j];
+      const T keep = hi ? c[H + j] : c[j];
+      o[j] = keep + xlane_t<STEP>(send);
+    }
+    return rs_sum<STEP - 1, H>(o, lane);
+  }
+}
+
+// group_sum / group_max of N independent values, step by step across all of them, so the
+// cross-lane moves of one value fill the DPP wait states of the others (same results).
+template <int WIDTH, int N, typename T>
+__device__ __forceinline__ void group_sum_n(T (&v)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += xlane_t<0>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += xlane_t<1>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += xlane_t<2>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += xlane_t<3>(v[i]);
+  if constexpr (WIDTH >= 32) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += xlane_t<4>(v[i]);
+  }
+  if constexpr (WIDTH >= 64) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += xlane_t<5>(v[i]);
+  }
+}
 
 // ---------------------------------------------------------------------------------------
 // exchange slots

@@ -107,23 +107,31 @@ struct KArgs {
 constexpr int TRACE_STEPS = 1024;
 
 // LDS of one workgroup.
+// Arrays the math waves read sit in the first 64 KB, so their LDS accesses use one base
+// register plus an immediate offset (the ds_* offset field is 16 bits); poller-only buffers
+// and the selection scratch follow.
 struct Lds {
-  float xres[HID];
-  float xn[HID];
-  float h1res[HID];
-  float hn[HID];
+  double red[NMATH][2][8][64];     // attention partials [wave][head][dim % 8][lane group * 16 + dim / 8]
+  double redl[NMATH][4][2];         // their softmax sums
+  double redm[NMATH][2];            // per (wave, head) running max
+  double wts[2][MAXC + 1];          // per head: chunk weights exp(m_c - M), then 1 / Z
+  uint32_t mbar;                    // math-wave barrier counter
+  uint32_t pad0[3];
   float q[2][HDIM];
   float knew[HDIM];
   float vnew[HDIM];
-  float attn[2 * HDIM];
+  float attp[MAXC * APS];  // raw attention partials of the XCD's chunks (poller -> math)
+  float xn[HID];
+  float hn[HID];
   float inter[XI];
   float hb[HID];
+  // poller-only from here
+  float xres[HID];
+  float h1res[HID];
   float stage[MAXC * APS > MAXV ? MAXC * APS : MAXV];
-  double red[NMATH][2][HDIM + 4];
-  SelScratch sel;
   uint32_t pen_bits[MAXV / 32];
   int tok[32];
-  uint32_t mbar;          // math-wave barrier counter
+  SelScratch sel;
 };
 
 // ---------------------------------------------------------------------------------------
@@ -144,15 +152,17 @@ __device__ __forceinline__ const bf16_t* lw(const TTSLayerWeights* layers, int l
 // KV geometry. bf16 cache (backbone): a position is 16 pieces of 8 dims; per wave 16
 // positions = 4 steps (jj) of 4 positions (one per 16-lane group). f32 cache (code predictor):
 // a position is 32 pieces of 4 dims; per wave 8 positions = 2 steps of 4 positions, each
-// lane holding 2 pieces (8 dims) per position.
+// lane holding 2 pieces (8 dims) per position. SUB = positions one pass of the 4 math waves
+// covers; CSUB = the chunking granularity (a chunk per CSUB positions, at most MAXC chunks), so
+// the short code-predictor contexts (L <= 16) still spread over up to 8 workgroups.
 template <bool BB> struct KVGeo;
-template <> struct KVGeo<true> { static constexpr int JJ = 4, PPP = 1, SUB = 64; };
-template <> struct KVGeo<false> { static constexpr int JJ = 2, PPP = 2, SUB = 32; };
+template <> struct KVGeo<true> { static constexpr int JJ = 4, PPP = 1, SUB = 64, CSUB = 64; };
+template <> struct KVGeo<false> { static constexpr int JJ = 2, PPP = 2, SUB = 32, CSUB = 2; };
 
 template <bool BB>
 __device__ __forceinline__ void chunking(int L, int& C, int& P) {
-  constexpr int SUB = KVGeo<BB>::SUB;
-  int c0 = (L + SUB - 1) / SUB;
+  constexpr int CSUB = KVGeo<BB>::CSUB;
+  int c0 = (L + CSUB - 1) / CSUB;
   if (c0 > MAXC) c0 = MAXC;
   if (c0 < 1) c0 = 1;
   P = (L + c0 - 1) / c0;
@@ -379,6 +389,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     }
   }
   if (threadIdx.x == 0) s.mbar = 0;
+  for (int i = threadIdx.x; i < MAXC * APS; i += NTHR) s.attp[i] = 0.0f;   // weights of unused chunks are 0
   uint32_t mgen = 0;
   __syncthreads();
 
@@ -387,6 +398,17 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   P.base = ws;
   P.ec.err = &ws->err;
   P.ec.spin_cap = a.spin_cap;
+  // Slot publishes go through the workspace buffer descriptor (SGPRs) with a 32-bit offset:
+  // XCD-local slots as plain stores (they land in the XCD's L2), cross-XCD slots with sc1
+  // (written through to memory). One 8-byte store carries value and tag together.
+  auto pub_local = [&](const uint64_t* p, float v, uint32_t tag) {
+    const u32x2 d = {__float_as_uint(v), tag};
+    __builtin_amdgcn_raw_buffer_store_b64(d, P.rs, (int)ws_off(P, p), 0, 0);
+  };
+  auto pub_cross = [&](const uint64_t* p, float v, uint32_t tag) {
+    const u32x2 d = {__float_as_uint(v), tag};
+    __builtin_amdgcn_raw_buffer_store_b64(d, P.rs, (int)ws_off(P, p), 0, 16);
+  };
   const TTSLayerWeights* LW = a.layers;
   const int NL = a.num_layers;
 
@@ -422,15 +444,15 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   auto load_qk_gains = [&](int layer) {
     const bf16_t* qn = lw(LW, layer, W_QN);
     const bf16_t* kn = lw(LW, layer, W_KN);
-    qn_l = bf2f(qn[lane]); qn_h = bf2f(qn[lane + 64]);
-    kn_l = bf2f(kn[lane]); kn_h = bf2f(kn[lane + 64]);
+    qn_l = ldbf(qn + lane); qn_h = ldbf(qn + lane + 64);
+    kn_l = ldbf(kn + lane); kn_h = ldbf(kn + lane + 64);
   };
   auto load_rope = [&](int pos) {
     const int row = rot_row(lane, pos);
-    cl_ = bf2f(a.cos_t[(size_t)row * HDIM + lane]);
-    sl_ = bf2f(a.sin_t[(size_t)row * HDIM + lane]);
-    ch_ = bf2f(a.cos_t[(size_t)row * HDIM + lane + 64]);
-    sh_ = bf2f(a.sin_t[(size_t)row * HDIM + lane + 64]);
+    cl_ = ldbf(a.cos_t + (size_t)row * HDIM + lane);
+    sl_ = ldbf(a.sin_t + (size_t)row * HDIM + lane);
+    ch_ = ldbf(a.cos_t + (size_t)row * HDIM + lane + 64);
+    sh_ = ldbf(a.sin_t + (size_t)row * HDIM + lane + 64);
   };
   // RMSNorm of x (LDS, 1024 f32) with gains g: out[i] = f32((x_i * rstd) * g_i), f64 math
   auto norm16 = [&](const float* x, float* out, const uint32_t (&g)[8], bool round_bf16) {
@@ -453,11 +475,11 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     const bf16_t* src = nullptr;
     if (a.cp_frame) {
       if (pi == 0) {
-        for (int i = lane; i < HID; i += 64) s.xres[i] = rbf(a.bb_hidden[i]);
+        for (int i = lane; i < HID; i += 64) s.xres[i] = rbf(*gmem(a.bb_hidden + i));
       } else if (pi == 1) {
         src = a.bb_emb + (size_t)g0 * HID;
       } else {
-        src = a.cp_embs[pi - 2] + (size_t)s.tok[pi - 2] * HID;
+        src = *gmem(a.cp_embs + (pi - 2)) + (size_t)s.tok[pi - 2] * HID;
       }
     } else {
       src = a.in_emb != nullptr ? a.in_emb : a.embed_w + (size_t)a.in_tok * HID;
@@ -483,7 +505,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       for (int x = 0; x < NXCD; ++x) acc += (double)s.stage[32 * x + lane];
       float xo = (float)acc;
       if constexpr (BB) xo = rbf(xo);
-      put_local(&ws->xl[xcd][par][32 * li + lane], xo, tag_of(lp, T_XL));
+      pub_local(&ws->xl[xcd][par][32 * li + lane], xo, tag_of(lp, T_XL));
     }
   };
   // ---- poller: next layer input (after ar2 of lp) -> xres, xn
@@ -547,30 +569,22 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     }
   };
-  // ---- poller: merge the C attention partials -> attn
+  // ---- poller: collect the C attention partials; per head the chunk weights
+  // w_c = exp(m_c - M) (M = max_c m_c, one chunk per lane) and 1 / Z, Z = sum_c l_c w_c.
+  // The weighted sum itself runs in the math waves (math_o), one output column per lane.
   auto prep_o = [&](int lp, int C) {
     const int par = lp & 1;
-    poll_vec<17>(P, ws->attp[xcd][par], C * APS, tag_of(lp, T_ATT), s.stage);
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      float M = -INFINITY;
-      for (int c = 0; c < C; ++c) M = fmaxf(M, s.stage[c * APS + 256 + 2 * h]);
-      double wc[MAXC];
+    poll_vec<17>(P, ws->attp[xcd][par], C * APS, tag_of(lp, T_ATT), s.attp);
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    const int h = lane >> 5, c = lane & 31;
+    float M = -INFINITY;
+    for (int j = 0; j < C; ++j) M = fmaxf(M, s.attp[j * APS + 256 + 2 * h]);
+    if (c < MAXC) s.wts[h][c] = c < C ? exp((double)s.attp[c * APS + 256 + 2 * h] - (double)M) : 0.0;
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    if (c == 0) {
       double Z = 0.0;
-#pragma unroll
-      for (int c = 0; c < MAXC; ++c) {
-        wc[c] = c < C ? exp((double)s.stage[c * APS + 256 + 2 * h] - (double)M) : 0.0;
-        if (c < C) Z += (double)s.stage[c * APS + 257 + 2 * h] * wc[c];
-      }
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int d = lane + 64 * j;
-        double acc = 0.0;
-#pragma unroll
-        for (int c = 0; c < MAXC; ++c)
-          if (c < C) acc += (double)s.stage[c * APS + 128 * h + d] * wc[c];
-        s.attn[128 * h + d] = (float)(acc / Z);
-      }
+      for (int j = 0; j < C; ++j) Z += (double)s.attp[j * APS + 257 + 2 * h] * s.wts[h][j];
+      s.wts[h][MAXC] = 1.0 / Z;
     }
   };
   // ---- poller: AR1 (O partials + residual) -> h1 slots; then h1 -> h1res, hn
@@ -582,7 +596,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       double acc = (double)s.xres[32 * li + lane];
 #pragma unroll
       for (int x = 0; x < NXCD; ++x) acc += (double)s.stage[32 * x + lane];
-      put_local(&ws->h1[xcd][par][32 * li + lane], (float)acc, tag_of(lp, T_H1));
+      pub_local(&ws->h1[xcd][par][32 * li + lane], (float)acc, tag_of(lp, T_H1));
     }
     poll_vec<8>(P, ws->h1[xcd][par], HID, tag_of(lp, T_H1), s.h1res);
     norm16(s.h1res, s.hn, g_post, false);
@@ -592,110 +606,136 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   };
 
   // ---- math: attention over this workgroup's chunk [c0, c1) at KV length L
+  // Both query heads of the XCD share the KV head, so one pass over the K/V tile serves both.
+  // Lane group g (16 lanes x 8 dims) scores positions b0 + 4 JJ mw + 4 jj + g (jj < JJ); each
+  // wave keeps one running max per head (shared by its 4 lane groups), so lane-group partials
+  // are plain sums: they go to LDS unscaled, and the final merge weighs the 4 waves by
+  // exp(m_w - M). Every exp is branch-free (a masked argument becomes -1000, whose exp is 0).
   auto attention = [&](int lp, int layer, int L, int c0, int c1) {
     constexpr int JJ = KVGeo<BB>::JJ, SUB = KVGeo<BB>::SUB;
+    constexpr double NEG = -1000.0;
     const int Lold = L - 1;
-    const int d0 = 8 * (lane & 15);
+    const int d0 = 8 * (lane & 15), g = lane >> 4;
     const double scale = (double)a.scale;
     const int nsb = (c1 - c0 + SUB - 1) / SUB;
-    // one query head at a time keeps the f64 accumulators of a single head live
-#pragma unroll 1
-    for (int h = 0; h < 2; ++h) {
-      float qv[8];
+    double qv[2][8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) qv[i] = s.q[h][d0 + i];
-      // online softmax in f64 over f32-rounded scores; m is always an f32 value
-      double m = -INFINITY, l = 0.0;
-      double acc[8];
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] = 0.0;
-      for (int sb = 0; sb < nsb; ++sb) {
-        const int b0 = c0 + sb * SUB;
-        if (sb > 0 || h > 0) {
-          if (nsb > 1) load_kv<BB>(tk, a, layer, xcd, b0, c1 < Lold ? c1 : Lold, mw, lane);
+      for (int i = 0; i < 8; ++i) qv[h][i] = s.q[h][d0 + i];
+    double m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0, 0.0};
+    double acc[2][8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[h][i] = 0.0;
+    for (int sb = 0; sb < nsb; ++sb) {
+      const int b0 = c0 + sb * SUB;
+      if (sb > 0) load_kv<BB>(tk, a, layer, xcd, b0, c1 < Lold ? c1 : Lold, mw, lane);
+      double sc[2 * JJ];
+#pragma unroll
+      for (int jj = 0; jj < JJ; ++jj) {
+        const int pos = b0 + 4 * JJ * mw + 4 * jj + g;
+        float kv[8];
+        if (pos == Lold) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) kv[i] = s.knew[d0 + i];
+        } else {
+          unpack8<BB>(tk, true, jj, kv);
         }
-        const TileKV& t = tk;
-        // scores of this lane group's JJ positions (f32-rounded), then one rescale
-        double sc[JJ];
+        double d_0 = 0.0, d_1 = 0.0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) { d_0 = fma(qv[0][i], (double)kv[i], d_0); d_1 = fma(qv[1][i], (double)kv[i], d_1); }
+        sc[jj] = d_0;
+        sc[JJ + jj] = d_1;
+      }
+      group_sum_n<16>(sc);
+      // f32-rounded scores; masked positions -inf; wave-wide max per head
+      double mx[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
         double mloc = -INFINITY;
 #pragma unroll
         for (int jj = 0; jj < JJ; ++jj) {
-          const int pos = b0 + 4 * JJ * mw + 4 * jj + (lane >> 4);
-          float kv[8];
-          if (pos == Lold) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) kv[i] = s.knew[d0 + i];
-          } else {
-            unpack8<BB>(t, true, jj, kv);
-          }
-          double dd = 0.0;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) dd = fma((double)qv[i], (double)kv[i], dd);
-          dd = group_sum<16>(dd);
-          sc[jj] = pos < c1 ? (double)(float)(dd * scale) : -INFINITY;
-          mloc = sc[jj] > mloc ? sc[jj] : mloc;
+          const int pos = b0 + 4 * JJ * mw + 4 * jj + g;
+          const double v = pos < c1 ? (double)(float)(sc[h * JJ + jj] * scale) : -INFINITY;
+          sc[h * JJ + jj] = v;
+          mloc = v > mloc ? v : mloc;
         }
-        const double mn = mloc > m ? mloc : m;
-        if (mn != -INFINITY) {
-          const double alpha = m == -INFINITY ? 0.0 : exp(m - mn);
-          l *= alpha;
+        mx[h] = mloc;
+      }
 #pragma unroll
-          for (int i = 0; i < 8; ++i) acc[i] *= alpha;
+      for (int h = 0; h < 2; ++h) {
+        double u = xlane_d<4>(mx[h]);
+        mx[h] = u > mx[h] ? u : mx[h];
+        u = xlane_d<5>(mx[h]);
+        mx[h] = u > mx[h] ? u : mx[h];
+      }
+      double mn[2], alpha[2];
 #pragma unroll
-          for (int jj = 0; jj < JJ; ++jj) {
-            const int pos = b0 + 4 * JJ * mw + 4 * jj + (lane >> 4);
-            const double p = sc[jj] == -INFINITY ? 0.0 : exp(sc[jj] - mn);
-            float vv[8];
-            if (pos == Lold) {
+      for (int h = 0; h < 2; ++h) {
+        mn[h] = mx[h] > m[h] ? mx[h] : m[h];
+        alpha[h] = exp(m[h] == -INFINITY ? NEG : m[h] - mn[h]);
+      }
+      double pr[2 * JJ];
 #pragma unroll
-              for (int i = 0; i < 8; ++i) vv[i] = s.vnew[d0 + i];
-            } else {
-              unpack8<BB>(t, false, jj, vv);
-            }
-            l += p;
+      for (int k = 0; k < 2 * JJ; ++k) pr[k] = exp(sc[k] == -INFINITY ? NEG : sc[k] - mn[k / JJ]);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) acc[i] = fma(p, (double)vv[i], acc[i]);
-          }
-          m = mn;
+      for (int h = 0; h < 2; ++h) {
+        l[h] *= alpha[h];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[h][i] *= alpha[h];
+      }
+#pragma unroll
+      for (int jj = 0; jj < JJ; ++jj) {
+        const int pos = b0 + 4 * JJ * mw + 4 * jj + g;
+        float vv[8];
+        if (pos == Lold) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) vv[i] = s.vnew[d0 + i];
+        } else {
+          unpack8<BB>(tk, false, jj, vv);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          l[h] += pr[h * JJ + jj];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[h][i] = fma(pr[h * JJ + jj], (double)vv[i], acc[h][i]);
         }
       }
-      // merge the 4 lane groups (xor 16, 32); the 4 waves are merged through LDS below
-      const double M = group_max<64>(m);
-      const double f = (m == -INFINITY) ? 0.0 : exp(m - M);
-      double lt = l * f;
-      lt += xlane_d<4>(lt);
-      lt += xlane_d<5>(lt);
+      m[0] = mn[0];
+      m[1] = mn[1];
+    }
+    // lane-major layout: each store of the wave writes 64 consecutive doubles (no bank conflicts)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        double v = acc[i] * f;
-        v += xlane_d<4>(v);
-        v += xlane_d<5>(v);
-        acc[i] = v;
-      }
-      if (lane < 16)
+    for (int h = 0; h < 2; ++h) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) s.red[mw][h][d0 + i] = acc[i];
-      if (lane == 0) { s.red[mw][h][HDIM] = M; s.red[mw][h][HDIM + 1] = lt; }
+      for (int i = 0; i < 8; ++i) s.red[mw][h][i][lane] = acc[h][i];
+      if ((lane & 15) == 0) s.redl[mw][g][h] = l[h];
+      if (lane == 0) s.redm[mw][h] = m[h];
     }
     math_barrier(s, mgen, &ws->err);
+    // thread t merges dim d = 8 j + i of head h, reading row i at columns 16 g + j (contiguous in j)
     const int t = threadIdx.x;  // 0..255
-    const int h = t >> 7, d = t & 127;
-    double M = -INFINITY;
+    const int h = t >> 7, ii = (t >> 4) & 7, jj0 = t & 15, d = 8 * jj0 + ii;
+    double Mw = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < NMATH; ++w) M = s.red[w][h][HDIM] > M ? s.red[w][h][HDIM] : M;
+    for (int w = 0; w < NMATH; ++w) Mw = s.redm[w][h] > Mw ? s.redm[w][h] : Mw;
     double A = 0.0, Lsum = 0.0;
 #pragma unroll
     for (int w = 0; w < NMATH; ++w) {
-      const double mw_ = s.red[w][h][HDIM];
-      const double f = mw_ == -INFINITY ? 0.0 : exp(mw_ - M);
-      A = fma(s.red[w][h][d], f, A);
-      Lsum = fma(s.red[w][h][HDIM + 1], f, Lsum);
+      const double mw_ = s.redm[w][h];
+      const double fw = exp(mw_ == -INFINITY ? NEG : mw_ - Mw);
+      const double aw = (s.red[w][h][ii][jj0] + s.red[w][h][ii][16 + jj0]) + (s.red[w][h][ii][32 + jj0] + s.red[w][h][ii][48 + jj0]);
+      const double lw_ = (s.redl[w][0][h] + s.redl[w][1][h]) + (s.redl[w][2][h] + s.redl[w][3][h]);
+      A = fma(aw, fw, A);
+      Lsum = fma(lw_, fw, Lsum);
     }
     const int c = li;
     uint64_t* dst = &ws->attp[xcd][lp & 1][c * APS];
     const uint32_t tg = tag_of(lp, T_ATT);
-    put_local(dst + 128 * h + d, (float)A, tg);
-    if (d == 0) { put_local(dst + 256 + 2 * h, (float)M, tg); put_local(dst + 257 + 2 * h, (float)Lsum, tg); }
+    pub_local(dst + 128 * h + d, (float)A, tg);
+    if (d == 0) { pub_local(dst + 256 + 2 * h, (float)Mw, tg); pub_local(dst + 257 + 2 * h, (float)Lsum, tg); }
     math_barrier(s, mgen, &ws->err);   // s.red is reused by the next attention
   };
 
@@ -708,36 +748,52 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     double xv[16];
     load_x16(s.xn, xv);
     const uint32_t tg = tag_of(lp, T_QKV);
+    double v[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      double v = dot8d(tq.p[2 * r], xv, 0.0);
-      v = group_sum<64>(dot8d(tq.p[2 * r + 1], xv + 8, v));
-      if (lane == r) put_local(&ws->qkv[xcd][lp & 1][16 * li + 4 * mw + r], (float)v, tg);
-    }
+    for (int r = 0; r < 4; ++r) v[r] = dot8d(tq.p[2 * r + 1], xv + 8, dot8d(tq.p[2 * r], xv, 0.0));
+    const double t = rs_sum<5, 4>(v, lane);   // row lane >> 4 in lanes 0, 16, 32, 48
+    if ((lane & 15) == 0) pub_local(&ws->qkv[xcd][lp & 1][16 * li + 4 * mw + (lane >> 4)], (float)t, tg);
   };
   auto math_o = [&](int lp) {
+    // merged attention of this lane's 8 columns: f32((sum_c acc_c w_c) * (1 / Z))
+    const int hh = (lane & 31) >> 4, col = 128 * hh + 8 * (lane & 15);
     double xv[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) xv[i] = s.attn[8 * (lane & 31) + i];
-    const uint32_t tg = tag_of(lp, T_OPART);
+    for (int i = 0; i < 8; ++i) xv[i] = 0.0;
+    // chunks c >= C carry weight 0 (their partials are finite: zero-initialised or older)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const double v = group_sum<32>(dot8d(to.p[j], xv, 0.0));
-      if ((lane & 31) == 0) put_cross(&ws->opart[lp & 1][xcd][32 * li + 8 * mw + 2 * j + (lane >> 5)], (float)v, tg);
+    for (int c = 0; c < MAXC; ++c) {
+      const double w = s.wts[hh][c];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xv[i] = fma((double)s.attp[c * APS + col + i], w, xv[i]);
     }
+    const double iz = s.wts[hh][MAXC];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xv[i] = (double)(float)(xv[i] * iz);
+    const uint32_t tg = tag_of(lp, T_OPART);
+    double v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = dot8d(to.p[j], xv, 0.0);
+    // per half-wave: row pair j = (lane >> 3) & 3 ends in lanes 0, 8, 16, 24 (+32)
+    const double t = rs_sum<4, 4>(v, lane);
+    if ((lane & 7) == 0)
+      pub_cross(&ws->opart[lp & 1][xcd][32 * li + 8 * mw + 2 * ((lane >> 3) & 3) + (lane >> 5)], (float)t, tg);
   };
   auto math_gu = [&](int lp) {
     double xv[16];
     load_x16(s.hn, xv);
     const uint32_t tg = tag_of(lp, T_INTER);
+    d2 c[4];
 #pragma unroll
-    for (int r = 0; r < 3; ++r) {
-      double g = dot8d(tgu.g[2 * r], xv, 0.0);
-      g = group_sum<64>(dot8d(tgu.g[2 * r + 1], xv + 8, g));
-      double u = dot8d(tgu.u[2 * r], xv, 0.0);
-      u = group_sum<64>(dot8d(tgu.u[2 * r + 1], xv + 8, u));
-      const double act = g / (1.0 + exp(-g)) * u;
-      if (lane == r) put_local(&ws->inter[xcd][lp & 1][12 * li + 3 * mw + r], (float)act, tg);
+    for (int r = 0; r < 3; ++r)
+      c[r] = d2{dot8d(tgu.g[2 * r + 1], xv + 8, dot8d(tgu.g[2 * r], xv, 0.0)),
+                dot8d(tgu.u[2 * r + 1], xv + 8, dot8d(tgu.u[2 * r], xv, 0.0))};
+    c[3] = d2{0.0, 0.0};
+    const d2 t = rs_sum<5, 4>(c, lane);   // (gate, up) of row lane >> 4 in lanes 0, 16, 32
+    const int r = lane >> 4;
+    if ((lane & 15) == 0 && r < 3) {
+      const double act = t.a / (1.0 + exp(-t.a)) * t.b;
+      pub_local(&ws->inter[xcd][lp & 1][12 * li + 3 * mw + r], (float)act, tg);
     }
   };
   auto math_down = [&](int lp) {
@@ -747,14 +803,17 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) xv[8 * j + i] = s.inter[8 * ((lane & 15) + 16 * j) + i];
     const uint32_t tg = tag_of(lp, T_DPART);
+    double v[2];
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
-      double v = 0.0;
+      v[g] = 0.0;
 #pragma unroll
-      for (int j = 0; j < 3; ++j) v = dot8d(td.p[3 * g + j], xv + 8 * j, v);
-      v = group_sum<16>(v);
-      if ((lane & 15) == 0) put_cross(&ws->dpart[lp & 1][xcd][32 * li + 8 * mw + 4 * g + (lane >> 4)], (float)v, tg);
+      for (int j = 0; j < 3; ++j) v[g] = dot8d(td.p[3 * g + j], xv + 8 * j, v[g]);
     }
+    // per 16-lane group: row set g = (lane >> 3) & 1 ends in lanes 0 and 8
+    const double t = rs_sum<3, 2>(v, lane);
+    if ((lane & 7) == 0)
+      pub_cross(&ws->dpart[lp & 1][xcd][32 * li + 8 * mw + 4 * ((lane >> 3) & 1) + (lane >> 4)], (float)t, tg);
   };
   // head rows of this workgroup: backbone codec head 12 rows (3 per wave), CP head 8 (2 per wave)
   auto head_rows = [&](int& row0, int& nrows) {
@@ -768,20 +827,19 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     double xv[16];
     load_x16(s.hb, xv);
     const uint32_t tg = a.tag_base + TAG_HEAD + (uint32_t)pi;
+    double v[4];
 #pragma unroll
-    for (int r = 0; r < 3; ++r) {
-      if (r < nrows) {
-        double v = dot8d(tq.p[2 * r], xv, 0.0);
-        v = group_sum<64>(dot8d(tq.p[2 * r + 1], xv + 8, v));
-        if (lane == r) {
-          put_cross(&ws->logits[pi & 1][row0 + r], (float)v, tg);
-          if (!a.cp_frame && a.out_logits) a.out_logits[row0 + r] = (float)v;
-        }
-      }
+    for (int r = 0; r < 4; ++r)
+      v[r] = r < 3 && r < nrows ? dot8d(tq.p[2 * r + 1], xv + 8, dot8d(tq.p[2 * r], xv, 0.0)) : 0.0;
+    const double t = rs_sum<5, 4>(v, lane);   // row lane >> 4 in lanes 0, 16, 32, 48
+    const int r = lane >> 4;
+    if ((lane & 15) == 0 && r < nrows) {
+      pub_cross(&ws->logits[pi & 1][row0 + r], (float)t, tg);
+      if (!a.cp_frame && a.out_logits) a.out_logits[row0 + r] = (float)t;
     }
   };
   auto head_weights = [&](int pi) -> const bf16_t* {
-    return a.cp_frame ? a.cp_heads[pi - 1] : a.head;
+    return a.cp_frame ? *gmem(a.cp_heads + (pi - 1)) : a.head;
   };
   // ---- poller: collect a head's logits and select a token
   auto select = [&](int pi) -> int {
@@ -987,9 +1045,9 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       for (int g = 0; g < a.n_groups; ++g) a.out_tokens[1 + g] = s.tok[g];
     }
     for (int d = lane; d < HID; d += 64) {
-      float acc = bf2f(a.bb_emb[(size_t)g0 * HID + d]);
-      for (int g = 0; g < a.n_groups; ++g) acc = rbf(acc + bf2f(a.cp_embs[g][(size_t)s.tok[g] * HID + d]));
-      if (a.text_row) acc = rbf(acc + bf2f(a.text_row[d]));
+      float acc = ldbf(a.bb_emb + (size_t)g0 * HID + d);
+      for (int g = 0; g < a.n_groups; ++g) acc = rbf(acc + ldbf(a.cp_embs[g] + (size_t)s.tok[g] * HID + d));
+      if (a.text_row) acc = rbf(acc + ldbf(a.text_row + d));
       a.out_combined[d] = f2bf(acc);
     }
   }
