@@ -72,6 +72,14 @@ template <class T>
 __device__ __forceinline__ const __attribute__((address_space(1))) T* gmem(const T* p) {
   return (const __attribute__((address_space(1))) T*)p;
 }
+// Constant-address-space view of a table that no wave writes during the launch (the layer
+// pointer table, the head / embedding pointer arrays): loads at a wave-uniform address become
+// scalar loads, which are counted by lgkmcnt and so never wait behind the vector-memory queue
+// of in-flight weight prefetches.
+template <class T>
+__device__ __forceinline__ T ld_const(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)p;
+}
 __device__ __forceinline__ u32x4 ldw(const bf16_t* p) { return *gmem(reinterpret_cast<const u32x4*>(p)); }
 __device__ __forceinline__ float ldbf(const bf16_t* p) { return bf2f(*gmem(p)); }
 __device__ __forceinline__ u32x4 ldw_nt(const bf16_t* p) {

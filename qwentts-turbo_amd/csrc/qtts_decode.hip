@@ -121,6 +121,7 @@ struct Lds {
   float knew[HDIM];
   float vnew[HDIM];
   float attp[MAXC * APS];  // raw attention partials of the XCD's chunks (poller -> math)
+  float attn[2 * HDIM];    // merged attention output of the XCD's two heads
   float xn[HID];
   float hn[HID];
   float inter[XI];
@@ -146,7 +147,7 @@ struct TileKV { u32x4 k[4]; u32x4 v[4]; };
 enum { W_LNIN = 0, W_Q, W_K, W_V, W_QN, W_KN, W_O, W_LNPOST, W_GATE, W_UP, W_DOWN };
 __device__ __forceinline__ const bf16_t* lw(const TTSLayerWeights* layers, int layer, int i) {
   const void* const* p = reinterpret_cast<const void* const*>(layers + layer);
-  return reinterpret_cast<const bf16_t*>(p[i]);
+  return reinterpret_cast<const bf16_t*>(ld_const(p + i));
 }
 
 // KV geometry. bf16 cache (backbone): a position is 16 pieces of 8 dims; per wave 16
@@ -479,7 +480,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       } else if (pi == 1) {
         src = a.bb_emb + (size_t)g0 * HID;
       } else {
-        src = *gmem(a.cp_embs + (pi - 2)) + (size_t)s.tok[pi - 2] * HID;
+        src = ld_const(a.cp_embs + (pi - 2)) + (size_t)s.tok[pi - 2] * HID;
       }
     } else {
       src = a.in_emb != nullptr ? a.in_emb : a.embed_w + (size_t)a.in_tok * HID;
@@ -755,21 +756,23 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     if ((lane & 15) == 0) pub_local(&ws->qkv[xcd][lp & 1][16 * li + 4 * mw + (lane >> 4)], (float)t, tg);
   };
   auto math_o = [&](int lp) {
-    // merged attention of this lane's 8 columns: f32((sum_c acc_c w_c) * (1 / Z))
-    const int hh = (lane & 31) >> 4, col = 128 * hh + 8 * (lane & 15);
+    // merged attention, one column per thread: f32((sum_c acc_c w_c) * (1 / Z)); chunks
+    // c >= C carry weight 0 (their partials are finite: zero-initialised or older)
+    {
+      const int t = threadIdx.x, hh = t >> 7;
+      float pv[MAXC];
+#pragma unroll
+      for (int c = 0; c < MAXC; ++c) pv[c] = s.attp[c * APS + t];
+      double acc = 0.0;
+#pragma unroll
+      for (int c = 0; c < MAXC; ++c) acc = fma((double)pv[c], s.wts[hh][c], acc);
+      s.attn[t] = (float)(acc * s.wts[hh][MAXC]);
+    }
+    math_barrier(s, mgen, &ws->err);
+    const int col = 8 * (lane & 31);
     double xv[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) xv[i] = 0.0;
-    // chunks c >= C carry weight 0 (their partials are finite: zero-initialised or older)
-#pragma unroll
-    for (int c = 0; c < MAXC; ++c) {
-      const double w = s.wts[hh][c];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) xv[i] = fma((double)s.attp[c * APS + col + i], w, xv[i]);
-    }
-    const double iz = s.wts[hh][MAXC];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) xv[i] = (double)(float)(xv[i] * iz);
+    for (int i = 0; i < 8; ++i) xv[i] = s.attn[col + i];
     const uint32_t tg = tag_of(lp, T_OPART);
     double v[4];
 #pragma unroll
@@ -839,7 +842,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     }
   };
   auto head_weights = [&](int pi) -> const bf16_t* {
-    return a.cp_frame ? *gmem(a.cp_heads + (pi - 1)) : a.head;
+    return a.cp_frame ? ld_const(a.cp_heads + (pi - 1)) : a.head;
   };
   // ---- poller: collect a head's logits and select a token
   auto select = [&](int pi) -> int {
@@ -1046,7 +1049,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     }
     for (int d = lane; d < HID; d += 64) {
       float acc = ldbf(a.bb_emb + (size_t)g0 * HID + d);
-      for (int g = 0; g < a.n_groups; ++g) acc = rbf(acc + ldbf(a.cp_embs[g] + (size_t)s.tok[g] * HID + d));
+      for (int g = 0; g < a.n_groups; ++g) acc = rbf(acc + ldbf(ld_const(a.cp_embs + g) + (size_t)s.tok[g] * HID + d));
       if (a.text_row) acc = rbf(acc + ldbf(a.text_row + d));
       a.out_combined[d] = f2bf(acc);
     }
