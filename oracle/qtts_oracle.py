@@ -141,6 +141,7 @@ EPS_F32 = float(torch.tensor(1e-6, dtype=torch.float32))   # the reference's 1e-
 SCALE_F32 = float(torch.tensor(1.0 / math.sqrt(128.0), dtype=torch.float32))  # attn_scale (f32)
 MAX_CHUNKS = 8      # attention chunks per KV head in the kernels
 SUB_BB, SUB_CP = 64, 2   # chunking granularity (positions per chunk before the 8-chunk cap)
+PASS_BB, PASS_CP = 64, 32  # contexts up to this length are attended whole by every workgroup
 
 
 def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
@@ -159,6 +160,16 @@ def chunking(L: int, sub: int) -> Tuple[int, int]:
 def r32(x: torch.Tensor) -> torch.Tensor:
     """Round an f64 tensor to f32 and back."""
     return x.to(torch.float32).to(torch.float64)
+
+
+def local_attention(q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, scale: float, R=lambda t: t) -> torch.Tensor:
+    """Decode attention over the whole context in one workgroup (contexts up to one pass of the
+    kernels' math waves): f32 scores, out = (sum_p exp(s_p - M) v_p) * (1 / sum_p exp(s_p - M))
+    in f64, rounded once (R) at the output -- no per-chunk rounding."""
+    scores = R(torch.einsum("hd,hpd->hp", q, K) * scale)
+    M = scores.max(dim=-1).values
+    p = torch.exp(scores - M[:, None])
+    return R(torch.einsum("hp,hpd->hd", p, V) * (1.0 / p.sum(-1))[:, None])
 
 
 def split_attention(q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, scale: float, sub: int,
@@ -307,8 +318,11 @@ class DecoderOracle:
             attn = torch.einsum("hp,hpd->hd", torch.softmax(scores, dim=-1), V[kv_of_q]).reshape(-1)
             h1 = r + w.o @ attn
         else:
-            attn = split_attention(q, K[kv_of_q], V[kv_of_q], SCALE_F32,
-                                   SUB_BB if self.kind == "backbone" else SUB_CP, r32).reshape(-1)
+            if L <= (PASS_BB if self.kind == "backbone" else PASS_CP):
+                attn = local_attention(q, K[kv_of_q], V[kv_of_q], SCALE_F32, r32).reshape(-1)
+            else:
+                attn = split_attention(q, K[kv_of_q], V[kv_of_q], SCALE_F32,
+                                       SUB_BB if self.kind == "backbone" else SUB_CP, r32).reshape(-1)
             # O projection as 8 per-XCD partials (XCD x: heads 2x, 2x+1 = columns [256x, 256x+256))
             cols = attn.numel() // 8
             h1 = r.clone()

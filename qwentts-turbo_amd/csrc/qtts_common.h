@@ -65,6 +65,13 @@ __device__ __forceinline__ double dot8d(const u32x4 w, const double* x, double a
   return acc;
 }
 
+// Value the optimizer must treat as unknown (an empty asm that claims to modify it): derived
+// quantities cannot be hoisted or CSE'd across the point where it is produced.
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 // Global-address-space view of a device pointer. Loads through it compile to global_load
 // (counted by vmcnt only); loads through a generic pointer compile to flat_load, which also
 // counts against lgkmcnt, so every LDS wait would also wait for the weight prefetches.

@@ -246,9 +246,15 @@ __device__ __forceinline__ void load_kv(TileKV& t, const KArgs& a, int layer, in
         t.k[jj] = ok ? ldw(reinterpret_cast<const bf16_t*>(a.kc) + off) : u32x4{0, 0, 0, 0};
         t.v[jj] = ok ? ldw(reinterpret_cast<const bf16_t*>(a.vc) + off) : u32x4{0, 0, 0, 0};
       } else {
-        const size_t off = (head_base + (size_t)pos) * HDIM + 8 * (lane & 15) + 4 * pp;
-        t.k[PPP * jj + pp] = ok ? *reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(a.kc) + off) : u32x4{0, 0, 0, 0};
-        t.v[PPP * jj + pp] = ok ? *reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(a.vc) + off) : u32x4{0, 0, 0, 0};
+        // The code-predictor cache is rewritten inside one frame launch and read by other
+        // CUs, so its loads are L2-coherent (sc1: no L1 line of an older write is used).
+        // Lanes without a position read past the buffer end, which returns zeros.
+        const uint32_t bytes = (uint32_t)((size_t)a.num_layers * NKVH * (size_t)a.max_seq * HDIM * 4);
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(a.kc, (short)0, (int)bytes, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(a.vc, (short)0, (int)bytes, 0x00020000);
+        const uint32_t off = ok ? (uint32_t)(((head_base + (size_t)pos0_) * HDIM + 8 * (lane & 15) + 4 * pp) * 4) : 0xFFFFFFF0u;
+        t.k[PPP * jj + pp] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 16);
+        t.v[PPP * jj + pp] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 16);
       }
     }
   }
@@ -371,7 +377,10 @@ __device__ __forceinline__ void step_barrier() {
 template <bool BB>
 __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   __shared__ Lds s;
-  const int lane = threadIdx.x & 63;
+  // lane index, re-derived opaquely at every step (see walk) so that lane-dependent slot
+  // offsets are recomputed where used instead of being hoisted out of the step loop and
+  // kept live (and spilled) across all steps
+  int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const bool poller = wave == NMATH;
   const int mw = __builtin_amdgcn_readfirstlane(wave);   // wave-uniform: row bases stay in SGPRs
@@ -612,7 +621,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   // wave keeps one running max per head (shared by its 4 lane groups), so lane-group partials
   // are plain sums: they go to LDS unscaled, and the final merge weighs the 4 waves by
   // exp(m_w - M). Every exp is branch-free (a masked argument becomes -1000, whose exp is 0).
-  auto attention = [&](int lp, int layer, int L, int c0, int c1) {
+  auto attention = [&](int lp, int layer, int L, int c0, int c1, bool local) {
     constexpr int JJ = KVGeo<BB>::JJ, SUB = KVGeo<BB>::SUB;
     constexpr double NEG = -1000.0;
     const int Lold = L - 1;
@@ -732,12 +741,17 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       A = fma(aw, fw, A);
       Lsum = fma(lw_, fw, Lsum);
     }
-    const int c = li;
-    uint64_t* dst = &ws->attp[xcd][lp & 1][c * APS];
-    const uint32_t tg = tag_of(lp, T_ATT);
-    pub_local(dst + 128 * h + d, (float)A, tg);
-    if (d == 0) { pub_local(dst + 256 + 2 * h, (float)Mw, tg); pub_local(dst + 257 + 2 * h, (float)Lsum, tg); }
-    math_barrier(s, mgen, &ws->err);   // s.red is reused by the next attention
+    if (local) {
+      // the whole context in this workgroup: f32(A * (1 / l)), no partial exchange
+      s.attn[128 * h + d] = (float)(A * (1.0 / Lsum));
+    } else {
+      const int c = li;
+      uint64_t* dst = &ws->attp[xcd][lp & 1][c * APS];
+      const uint32_t tg = tag_of(lp, T_ATT);
+      pub_local(dst + 128 * h + d, (float)A, tg);
+      if (d == 0) { pub_local(dst + 256 + 2 * h, (float)Mw, tg); pub_local(dst + 257 + 2 * h, (float)Lsum, tg); }
+    }
+    math_barrier(s, mgen, &ws->err);   // s.red is reused by the next attention; s.attn complete
   };
 
   // ---- math: GEMV stages (f64 accumulation, f32 results)
@@ -755,10 +769,10 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     const double t = rs_sum<5, 4>(v, lane);   // row lane >> 4 in lanes 0, 16, 32, 48
     if ((lane & 15) == 0) pub_local(&ws->qkv[xcd][lp & 1][16 * li + 4 * mw + (lane >> 4)], (float)t, tg);
   };
-  auto math_o = [&](int lp) {
-    // merged attention, one column per thread: f32((sum_c acc_c w_c) * (1 / Z)); chunks
+  auto math_o = [&](int lp, bool merged) {
+    // chunked attention: merge, one column per thread: f32((sum_c acc_c w_c) * (1 / Z)); chunks
     // c >= C carry weight 0 (their partials are finite: zero-initialised or older)
-    {
+    if (!merged) {
       const int t = threadIdx.x, hh = t >> 7;
       float pv[MAXC];
 #pragma unroll
@@ -767,8 +781,8 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
 #pragma unroll
       for (int c = 0; c < MAXC; ++c) acc = fma((double)pv[c], s.wts[hh][c], acc);
       s.attn[t] = (float)(acc * s.wts[hh][MAXC]);
+      math_barrier(s, mgen, &ws->err);
     }
-    math_barrier(s, mgen, &ws->err);
     const int col = 8 * (lane & 31);
     double xv[8];
 #pragma unroll
@@ -893,6 +907,9 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       a.trace[((size_t)wg * TRACE_STEPS + nstep) * 2 + (poller ? 1 : 0)] = __builtin_amdgcn_s_memrealtime();
     ++nstep;
   };
+  // attention over the whole context in every workgroup when it fits one pass of the math
+  // waves (attention and O projection then share a step); split into chunks otherwise
+  auto att_local = [&](int pi) { return a.pos0 + pi + 1 <= KVGeo<BB>::SUB; };
   auto walk = [&](auto&& act) {
     act(S_PRO, 0, 0); stamp();
     step_barrier();
@@ -900,36 +917,33 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       for (int layer = 0; layer < NL; ++layer) {
         act(S_QKV, pi, layer); stamp(); step_barrier();
         act(S_ATT, pi, layer); stamp(); step_barrier();
-        act(S_O, pi, layer); stamp(); step_barrier();
+        if (!att_local(pi)) { act(S_O, pi, layer); stamp(); step_barrier(); }
         act(S_GU, pi, layer); stamp(); step_barrier();
         act(S_DOWN, pi, layer); stamp(); step_barrier();
       }
       if (has_head(pi)) { act(S_HEAD, pi, NL - 1); stamp(); step_barrier(); }
     }
   };
-  struct PosInfo { int pos, L, C, P, c0, c1; bool last_pos, head; };
+  struct PosInfo { int pos, L, C, P, c0, c1; bool local, has_chunk, last_pos, head; };
   auto pinfo = [&](int pi) {
     PosInfo q;
     q.pos = a.pos0 + pi;
     q.L = q.pos + 1;
     chunking<BB>(q.L, q.C, q.P);
-    q.c0 = li * q.P;
-    q.c1 = min(q.L, (li + 1) * q.P);
+    q.local = att_local(pi);
+    q.has_chunk = q.local || li < q.C;
+    q.c0 = q.local ? 0 : li * q.P;
+    q.c1 = q.local ? q.L : min(q.L, (li + 1) * q.P);
     q.last_pos = pi == a.n_pos - 1;
     q.head = has_head(pi);
     return q;
-  };
-  // chunk of this workgroup at the next position, restricted to cached (old) positions
-  auto next_kv = [&](int pi, int layer) {
-    const PosInfo n = pinfo(pi + 1);
-    if (li < n.C) load_kv<BB>(tk, a, layer, xcd, n.c0, min(n.c1, n.L - 1), mw, lane);
-    else tk = TileKV{};
   };
   // Tiles are (re)defined on every path so that no stale tile value stays live across the
   // step loop (that would keep all tiles resident at once and spill).
 
   if (poller) {
     walk([&](int st, int pi, int layer) {
+      lane = opaque(lane);
       const PosInfo q = pinfo(pi);
       const int lp = pi * NL + layer;
       const int nl = layer + 1 < NL ? layer + 1 : 0;   // next layer pass (wraps to the next position)
@@ -948,7 +962,14 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           load_qk_gains(nl);
           if (layer == NL - 1 && !q.last_pos) load_rope(q.pos + 1);
           break;
-        case S_ATT: prep_o(lp, q.C); break;
+        case S_ATT:
+          if (q.local) {
+            prep_gu(lp, layer);
+            load_gain16(g_post, lw(LW, nl, W_LNPOST));
+          } else {
+            prep_o(lp, q.C);
+          }
+          break;
         case S_O:
           prep_gu(lp, layer);
           load_gain16(g_post, lw(LW, nl, W_LNPOST));
@@ -980,29 +1001,41 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     });
   } else {
     walk([&](int st, int pi, int layer) {
+      lane = opaque(lane);
       const PosInfo q = pinfo(pi);
       const int lp = pi * NL + layer;
       const bool last_layer = layer == NL - 1;
+      // Each tile is loaded one step ahead of its use, right after the step's own compute,
+      // so at most the tile in use and the next one are live.
       switch (st) {
         case S_PRO:
           load_qkv<BB>(tq, LW, 0, xcd, li, mw, lane);
-          if (li < q.C) load_kv<BB>(tk, a, 0, xcd, q.c0, min(q.c1, q.L - 1), mw, lane);
-          else tk = TileKV{};
           break;
         case S_QKV:
           math_qkv(lp);
-          load_o<BB>(to, LW, layer, xcd, li, mw, lane);
+          if (q.has_chunk) load_kv<BB>(tk, a, layer, xcd, q.c0, min(q.c1, q.L - 1), mw, lane);
+          else tk = TileKV{};
+          if (q.local) load_o<BB>(to, LW, layer, xcd, li, mw, lane);
           break;
         case S_ATT:
-          if (li < q.C) attention(lp, layer, q.L, q.c0, q.c1);
-          load_gu<BB>(tgu, LW, layer, xcd, li, mw, lane);
+          if (q.has_chunk) attention(lp, layer, q.L, q.c0, q.c1, q.local);
+          if (q.local) {
+            math_o(lp, true);
+            load_gu<BB>(tgu, LW, layer, xcd, li, mw, lane);
+          } else {
+            load_o<BB>(to, LW, layer, xcd, li, mw, lane);
+          }
           break;
         case S_O:
-          math_o(lp);
-          load_d<BB>(td, LW, layer, xcd, li, mw, lane);
+          math_o(lp, false);
+          load_gu<BB>(tgu, LW, layer, xcd, li, mw, lane);
           break;
         case S_GU:
           math_gu(lp);
+          load_d<BB>(td, LW, layer, xcd, li, mw, lane);
+          break;
+        case S_DOWN:
+          math_down(lp);
           if (!last_layer) {
             load_qkv<BB>(tq, LW, layer + 1, xcd, li, mw, lane);
           } else if (q.head) {
@@ -1015,26 +1048,10 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
             tq = TileQKV{};
           }
           break;
-        case S_DOWN:
-          math_down(lp);
-          if (!last_layer) {
-            if (li < q.C) load_kv<BB>(tk, a, layer + 1, xcd, q.c0, min(q.c1, q.L - 1), mw, lane);
-            else tk = TileKV{};
-          } else if (!q.head && !q.last_pos) {
-            next_kv(pi, 0);
-          } else {
-            tk = TileKV{};
-          }
-          break;
         case S_HEAD:
           math_head(pi);
-          if (!q.last_pos) {
-            load_qkv<BB>(tq, LW, 0, xcd, li, mw, lane);
-            next_kv(pi, 0);
-          } else {
-            tq = TileQKV{};
-            tk = TileKV{};
-          }
+          if (!q.last_pos) load_qkv<BB>(tq, LW, 0, xcd, li, mw, lane);
+          else tq = TileQKV{};
           break;
       }
     });

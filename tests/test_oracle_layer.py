@@ -20,7 +20,7 @@ import pytest
 import torch
 
 from oracle.qtts_oracle import (DecoderOracle, TalkerWeights, head_logits, rel_l2, split_attention, chunking,
-                                SUB_BB, SUB_CP)
+                                local_attention, SUB_BB, SUB_CP)
 
 transformers = pytest.importorskip("transformers")
 from transformers import Qwen3Config  # noqa: E402
@@ -165,6 +165,7 @@ def test_split_attention_equals_single_pass_softmax(L, sub):
     C, P = chunking(L, sub)
     assert 1 <= C <= 8 and (C - 1) * P < L <= C * P
     assert rel_l2(split_attention(q, K, V, scale, sub), ref) < 1e-13
+    assert rel_l2(local_attention(q, K, V, scale), ref) < 1e-13
 
 
 def test_gqa_head_map_uses_kv_head_h_div_2(small):
