@@ -113,10 +113,8 @@ constexpr int TRACE_STEPS = 1024;
 struct Lds {
   double red[NMATH][2][8][64];     // attention partials [wave][head][dim % 8][lane group * 16 + dim / 8]
   double redl[NMATH][4][2];         // their softmax sums
-  double redm[NMATH][2];            // per (wave, head) running max
+  double redm[2][NMATH][2];         // per (pass parity, wave, head) score max
   double wts[2][MAXC + 1];          // per head: chunk weights exp(m_c - M), then 1 / Z
-  uint32_t mbar;                    // math-wave barrier counter
-  uint32_t pad0[3];
   float q[2][HDIM];
   float knew[HDIM];
   float vnew[HDIM];
@@ -273,23 +271,6 @@ __device__ __forceinline__ void unpack8(const TileKV& t, bool key, int jj, float
   }
 }
 
-// Barrier among the 4 math waves only (the poller wave keeps running). Bounded: after ~2^24
-// sleeps the wait is abandoned and the error word latched.
-__device__ __forceinline__ void math_barrier(Lds& s, uint32_t& gen, uint32_t* err) {
-  gen += NMATH;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  if ((threadIdx.x & 63) == 0) atomicAdd(&s.mbar, 1u);
-  uint32_t n = 0;
-  while (__hip_atomic_load(&s.mbar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < gen) {
-    __builtin_amdgcn_s_sleep(1);
-    if (++n > (1u << 24)) {
-      if ((threadIdx.x & 63) == 0) atomicOr(err, 2u);
-      break;
-    }
-  }
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-}
-
 // ---------------------------------------------------------------------------------------
 // Poller helpers
 // ---------------------------------------------------------------------------------------
@@ -363,8 +344,9 @@ __device__ __forceinline__ float norm_f32(float x, double rstd, bf16_t g) {
   return (float)(((double)x * rstd) * (double)bf2f(g));
 }
 
-// Workgroup barrier at a step boundary: makes the LDS operands one role wrote visible to the
-// other role. Both roles reach it the same number of times (see the step walker).
+// Workgroup barrier: makes LDS data one wave wrote visible to the others. Used at every step
+// boundary and inside the attention steps; both roles reach it the same number of times (the
+// poller wave joins the math waves' internal barriers of a step before its own step work).
 __device__ __forceinline__ void step_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __builtin_amdgcn_s_barrier();
@@ -398,9 +380,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       return;
     }
   }
-  if (threadIdx.x == 0) s.mbar = 0;
   for (int i = threadIdx.x; i < MAXC * APS; i += NTHR) s.attp[i] = 0.0f;   // weights of unused chunks are 0
-  uint32_t mgen = 0;
   __syncthreads();
 
   Poll P;
@@ -681,10 +661,17 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
         u = xlane_d<5>(mx[h]);
         mx[h] = u > mx[h] ? u : mx[h];
       }
+      // workgroup-wide maximum of this pass (slots double-buffered by pass parity): every
+      // wave and lane group then shares one running max, so their partial sums add plainly
+      if (lane == 0) { s.redm[sb & 1][mw][0] = mx[0]; s.redm[sb & 1][mw][1] = mx[1]; }
+      step_barrier();
       double mn[2], alpha[2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        mn[h] = mx[h] > m[h] ? mx[h] : m[h];
+        double M = m[h];
+#pragma unroll
+        for (int w = 0; w < NMATH; ++w) M = s.redm[sb & 1][w][h] > M ? s.redm[sb & 1][w][h] : M;
+        mn[h] = M;
         alpha[h] = exp(m[h] == -INFINITY ? NEG : m[h] - mn[h]);
       }
       double pr[2 * JJ];
@@ -722,25 +709,18 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) s.red[mw][h][i][lane] = acc[h][i];
       if ((lane & 15) == 0) s.redl[mw][g][h] = l[h];
-      if (lane == 0) s.redm[mw][h] = m[h];
     }
-    math_barrier(s, mgen, &ws->err);
+    step_barrier();
     // thread t merges dim d = 8 j + i of head h, reading row i at columns 16 g + j (contiguous in j)
     const int t = threadIdx.x;  // 0..255
     const int h = t >> 7, ii = (t >> 4) & 7, jj0 = t & 15, d = 8 * jj0 + ii;
-    double Mw = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < NMATH; ++w) Mw = s.redm[w][h] > Mw ? s.redm[w][h] : Mw;
     double A = 0.0, Lsum = 0.0;
 #pragma unroll
     for (int w = 0; w < NMATH; ++w) {
-      const double mw_ = s.redm[w][h];
-      const double fw = exp(mw_ == -INFINITY ? NEG : mw_ - Mw);
-      const double aw = (s.red[w][h][ii][jj0] + s.red[w][h][ii][16 + jj0]) + (s.red[w][h][ii][32 + jj0] + s.red[w][h][ii][48 + jj0]);
-      const double lw_ = (s.redl[w][0][h] + s.redl[w][1][h]) + (s.redl[w][2][h] + s.redl[w][3][h]);
-      A = fma(aw, fw, A);
-      Lsum = fma(lw_, fw, Lsum);
+      A += (s.red[w][h][ii][jj0] + s.red[w][h][ii][16 + jj0]) + (s.red[w][h][ii][32 + jj0] + s.red[w][h][ii][48 + jj0]);
+      Lsum += (s.redl[w][0][h] + s.redl[w][1][h]) + (s.redl[w][2][h] + s.redl[w][3][h]);
     }
+    const double Mw = h ? m[1] : m[0];
     if (local) {
       // the whole context in this workgroup: f32(A * (1 / l)), no partial exchange
       s.attn[128 * h + d] = (float)(A * (1.0 / Lsum));
@@ -751,7 +731,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       pub_local(dst + 128 * h + d, (float)A, tg);
       if (d == 0) { pub_local(dst + 256 + 2 * h, (float)Mw, tg); pub_local(dst + 257 + 2 * h, (float)Lsum, tg); }
     }
-    math_barrier(s, mgen, &ws->err);   // s.red is reused by the next attention; s.attn complete
+    step_barrier();   // s.red is reused by the next attention; s.attn complete
   };
 
   // ---- math: GEMV stages (f64 accumulation, f32 results)
@@ -781,7 +761,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
 #pragma unroll
       for (int c = 0; c < MAXC; ++c) acc = fma((double)pv[c], s.wts[hh][c], acc);
       s.attn[t] = (float)(acc * s.wts[hh][MAXC]);
-      math_barrier(s, mgen, &ws->err);
+      step_barrier();
     }
     const int col = 8 * (lane & 31);
     double xv[8];
@@ -963,6 +943,12 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           if (layer == NL - 1 && !q.last_pos) load_rope(q.pos + 1);
           break;
         case S_ATT:
+          // the math waves' attention synchronises the whole workgroup (passes + 2 times);
+          // this wave's inputs for the step are produced after those points anyway
+          if (q.has_chunk) {
+            const int nb = (q.c1 - q.c0 + KVGeo<BB>::SUB - 1) / KVGeo<BB>::SUB + 2;
+            for (int b = 0; b < nb; ++b) step_barrier();
+          }
           if (q.local) {
             prep_gu(lp, layer);
             load_gain16(g_post, lw(LW, nl, W_LNPOST));
@@ -971,6 +957,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           }
           break;
         case S_O:
+          step_barrier();   // joins the barrier after the math waves' attention merge
           prep_gu(lp, layer);
           load_gain16(g_post, lw(LW, nl, W_LNPOST));
           break;
