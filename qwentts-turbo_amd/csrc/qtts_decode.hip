@@ -45,6 +45,7 @@ struct Workspace {
   uint64_t opart[2][NXCD][HID];
   uint64_t dpart[2][NXCD][HID];
   uint64_t logits[2][MAXV];
+  uint64_t hbest[2][2 * NWG];   // greedy code-predictor heads: per workgroup {value, tag}, {index, tag}
   uint32_t err;
   uint32_t pad[63];
 };
@@ -120,6 +121,8 @@ struct Lds {
   float vnew[HDIM];
   float attp[MAXC * APS];  // raw attention partials of the XCD's chunks (poller -> math)
   float attn[2 * HDIM];    // merged attention output of the XCD's two heads
+  float hbv[NMATH];        // greedy head: best logit of each math wave ...
+  int hbi[NMATH];          // ... and its vocabulary id
   float xn[HID];
   float hn[HID];
   float inter[XI];
@@ -409,6 +412,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   TileKV tk;
 
   auto tag_of = [&](int lp, int slot) -> uint32_t { return a.tag_base + (uint32_t)(lp * T_NSLOT + slot); };
+  const bool cp_greedy = a.cp_frame && !a.sel.do_sample;
   auto has_head = [&](int pi) -> bool { return a.cp_frame ? pi >= 1 : (a.head != nullptr && pi == a.n_pos - 1); };
 
   // rotary row of channel c (c < 64) at position pos
@@ -830,7 +834,24 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       v[r] = r < 3 && r < nrows ? dot8d(tq.p[2 * r + 1], xv + 8, dot8d(tq.p[2 * r], xv, 0.0)) : 0.0;
     const double t = rs_sum<5, 4>(v, lane);   // row lane >> 4 in lanes 0, 16, 32, 48
     const int r = lane >> 4;
-    if ((lane & 15) == 0 && r < nrows) {
+    if (cp_greedy) {
+      // greedy code-predictor head: only the workgroup's best (value, lowest id on ties) is
+      // published; the selecting waves reduce 256 candidates instead of the whole vocabulary
+      float bv = ((lane & 15) == 0 && r < nrows) ? (float)t : -INFINITY;
+      int bi = row0 + r;
+      best_merge(bv, bi, xlane_f<4>(bv), (int)xlane<4>((uint32_t)bi));
+      best_merge(bv, bi, xlane_f<5>(bv), (int)xlane<5>((uint32_t)bi));
+      if (lane == 0) { s.hbv[mw] = bv; s.hbi[mw] = bi; }
+      step_barrier();
+      if (mw == 0 && lane == 0) {
+        float wv = s.hbv[0];
+        int wi = s.hbi[0];
+#pragma unroll
+        for (int w = 1; w < NMATH; ++w) best_merge(wv, wi, s.hbv[w], s.hbi[w]);
+        pub_cross(&ws->hbest[pi & 1][2 * wg], wv, tg);
+        pub_cross(&ws->hbest[pi & 1][2 * wg + 1], __uint_as_float((uint32_t)wi), tg);
+      }
+    } else if ((lane & 15) == 0 && r < nrows) {
       pub_cross(&ws->logits[pi & 1][row0 + r], (float)t, tg);
       if (!a.cp_frame && a.out_logits) a.out_logits[row0 + r] = (float)t;
     }
@@ -840,6 +861,48 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   };
   // ---- poller: collect a head's logits and select a token
   auto select = [&](int pi) -> int {
+    if (cp_greedy) {
+      // 256 workgroup candidates, 4 per lane, reduced in registers as they arrive
+      const uint32_t tg = a.tag_base + TAG_HEAD + (uint32_t)pi;
+      const uint32_t o = ws_off(P, &ws->hbest[pi & 1][0]);
+      float bv = -INFINITY;
+      int bi = 0x7fffffff;
+      uint32_t pending = 0xFu, spins = 0;
+      for (;;) {
+        u32x4 v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (pending & (1u << k)) v[k] = __builtin_amdgcn_raw_buffer_load_b128(P.rs, o + 16u * (uint32_t)(lane + 64 * k), 0, 16);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          if ((pending & (1u << k)) && v[k].y == tg && v[k].w == tg) {
+            best_merge(bv, bi, __uint_as_float(v[k].x), (int)v[k].z);
+            pending &= ~(1u << k);
+          }
+        }
+        if (__ballot(pending != 0u) == 0ull) break;
+        ++spins;
+        if ((spins & 63u) == 0u && (spins > P.ec.spin_cap || err_set(P.ec))) {
+          if (lane == 0) atomicOr(P.ec.err, 1u);
+          break;
+        }
+      }
+#pragma unroll
+      for (int st = 0; st < 6; ++st) {
+        float ov;
+        int oi;
+        switch (st) {
+          case 0: ov = xlane_f<0>(bv); oi = (int)xlane<0>((uint32_t)bi); break;
+          case 1: ov = xlane_f<1>(bv); oi = (int)xlane<1>((uint32_t)bi); break;
+          case 2: ov = xlane_f<2>(bv); oi = (int)xlane<2>((uint32_t)bi); break;
+          case 3: ov = xlane_f<3>(bv); oi = (int)xlane<3>((uint32_t)bi); break;
+          case 4: ov = xlane_f<4>(bv); oi = (int)xlane<4>((uint32_t)bi); break;
+          default: ov = xlane_f<5>(bv); oi = (int)xlane<5>((uint32_t)bi); break;
+        }
+        best_merge(bv, bi, ov, oi);
+      }
+      return bi == 0x7fffffff ? 0 : bi;
+    }
     const int n = a.cp_frame ? a.cp_vocab : a.vocab;
     poll_vec<24>(P, ws->logits[pi & 1], n, a.tag_base + TAG_HEAD + (uint32_t)pi, s.stage);
     SelParams sp = a.sel;
@@ -970,6 +1033,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           if (layer < NL - 1 || !(q.head || q.last_pos)) load_gain16(g_in, lw(LW, (nl + 1) % NL, W_LNIN));
           break;
         case S_HEAD:
+          if (cp_greedy) step_barrier();   // joins the math waves' head barrier
           if (a.cp_frame || wg == 0) {
             const int tok = select(pi);
             if (a.cp_frame) {

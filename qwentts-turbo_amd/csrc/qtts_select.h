@@ -15,6 +15,11 @@ struct SelParams {
   int group;
 };
 
+// Keep the better of two (value, index) candidates: larger value, lower index on ties.
+__device__ __forceinline__ void best_merge(float& bv, int& bi, float ov, int oi) {
+  if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+}
+
 // Greedy argmax over lg[0..n) (lowest index on ties; all -inf -> index 0), run by one wave.
 __device__ inline int wave_argmax(const float* lg, int n) {
   const int lane = threadIdx.x & 63;
