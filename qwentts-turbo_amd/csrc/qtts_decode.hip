@@ -291,16 +291,13 @@ __device__ __forceinline__ uint32_t ws_off(const Poll& P, const void* p) {
 template <int MAXP, typename OffF>
 __device__ bool poll_pairs(const Poll& P, int npair, uint32_t tag, float* dst, OffF off) {
   const int lane = threadIdx.x & 63;
-  uint32_t pending = 0;
+  uint32_t valid = 0;
 #pragma unroll
   for (int k = 0; k < MAXP; ++k)
-    if (lane + 64 * k < npair) pending |= 1u << k;
+    if (lane + 64 * k < npair) valid |= 1u << k;
+  uint32_t pending = valid;
   uint32_t spins = 0;
-  for (;;) {
-    u32x4 v[MAXP];
-#pragma unroll
-    for (int k = 0; k < MAXP; ++k)
-      if (pending & (1u << k)) v[k] = __builtin_amdgcn_raw_buffer_load_b128(P.rs, off(lane + 64 * k), 0, 16);
+  auto check = [&](const u32x4 (&v)[MAXP]) {
 #pragma unroll
     for (int k = 0; k < MAXP; ++k) {
       if ((pending & (1u << k)) && v[k].y == tag && v[k].w == tag) {
@@ -310,11 +307,43 @@ __device__ bool poll_pairs(const Poll& P, int npair, uint32_t tag, float* dst, O
         pending &= ~(1u << k);
       }
     }
-    if (__ballot(pending != 0u) == 0ull) return true;
+    return __ballot(pending != 0u) == 0ull;
+  };
+  auto timed_out = [&]() {
     ++spins;
     if ((spins & 63u) == 0u && (spins > P.ec.spin_cap || err_set(P.ec))) {
       if (lane == 0) atomicOr(P.ec.err, 1u);
-      return false;
+      return true;
+    }
+    return false;
+  };
+  if constexpr (MAXP <= 8) {
+    // Two batches in flight: the next batch is issued before the previous one is checked, so a
+    // slot is seen about half a load latency after it lands instead of a whole one. Every
+    // batch has the same loads (lanes without a slot re-read slot 0), so the wait for the
+    // older batch is an exact vmcnt.
+    u32x4 va[MAXP], vb[MAXP];
+    auto issue = [&](u32x4 (&v)[MAXP]) {
+#pragma unroll
+      for (int k = 0; k < MAXP; ++k)
+        v[k] = __builtin_amdgcn_raw_buffer_load_b128(P.rs, off((valid >> k) & 1u ? lane + 64 * k : 0), 0, 16);
+    };
+    issue(va);
+    for (;;) {
+      issue(vb);
+      if (check(va)) return true;
+      issue(va);
+      if (check(vb)) return true;
+      if (timed_out()) return false;
+    }
+  } else {
+    for (;;) {
+      u32x4 v[MAXP];
+#pragma unroll
+      for (int k = 0; k < MAXP; ++k)
+        if (pending & (1u << k)) v[k] = __builtin_amdgcn_raw_buffer_load_b128(P.rs, off(lane + 64 * k), 0, 16);
+      if (check(v)) return true;
+      if (timed_out()) return false;
     }
   }
 }
