@@ -141,7 +141,7 @@ EPS_F32 = float(torch.tensor(1e-6, dtype=torch.float32))   # the reference's 1e-
 SCALE_F32 = float(torch.tensor(1.0 / math.sqrt(128.0), dtype=torch.float32))  # attn_scale (f32)
 MAX_CHUNKS = 8      # attention chunks per KV head in the kernels
 SUB_BB, SUB_CP = 64, 2   # chunking granularity (positions per chunk before the 8-chunk cap)
-PASS_BB, PASS_CP = 64, 32  # contexts up to this length are attended whole by every workgroup
+PASS_BB, PASS_CP = 64, 16  # contexts up to this length are attended whole by every workgroup
 
 
 def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:

@@ -143,7 +143,6 @@ struct TileQKV { u32x4 p[8]; };
 struct TileO { u32x4 p[4]; };
 struct TileGU { u32x4 g[6]; u32x4 u[6]; };
 struct TileD { u32x4 p[6]; };
-struct TileKV { u32x4 k[4]; u32x4 v[4]; };
 
 enum { W_LNIN = 0, W_Q, W_K, W_V, W_QN, W_KN, W_O, W_LNPOST, W_GATE, W_UP, W_DOWN };
 __device__ __forceinline__ const bf16_t* lw(const TTSLayerWeights* layers, int layer, int i) {
@@ -153,13 +152,17 @@ __device__ __forceinline__ const bf16_t* lw(const TTSLayerWeights* layers, int l
 
 // KV geometry. bf16 cache (backbone): a position is 16 pieces of 8 dims; per wave 16
 // positions = 4 steps (jj) of 4 positions (one per 16-lane group). f32 cache (code predictor):
-// a position is 32 pieces of 4 dims; per wave 8 positions = 2 steps of 4 positions, each
-// lane holding 2 pieces (8 dims) per position. SUB = positions one pass of the 4 math waves
-// covers; CSUB = the chunking granularity (a chunk per CSUB positions, at most MAXC chunks), so
-// the short code-predictor contexts (L <= 16) still spread over up to 8 workgroups.
+// a position is 32 pieces of 4 dims; per wave 4 positions (one per 16-lane group), each lane
+// holding 2 pieces (8 dims). SUB = positions one pass of the 4 math waves covers (a whole
+// code-predictor frame context, L <= 16, in one pass); CSUB = the chunking granularity for
+// longer contexts (a chunk per CSUB positions, at most MAXC chunks).
 template <bool BB> struct KVGeo;
 template <> struct KVGeo<true> { static constexpr int JJ = 4, PPP = 1, SUB = 64, CSUB = 64; };
-template <> struct KVGeo<false> { static constexpr int JJ = 2, PPP = 2, SUB = 32, CSUB = 2; };
+template <> struct KVGeo<false> { static constexpr int JJ = 1, PPP = 2, SUB = 16, CSUB = 2; };
+template <bool BB> struct TileKV {
+  u32x4 k[KVGeo<BB>::JJ * KVGeo<BB>::PPP];
+  u32x4 v[KVGeo<BB>::JJ * KVGeo<BB>::PPP];
+};
 
 template <bool BB>
 __device__ __forceinline__ void chunking(int L, int& C, int& P) {
@@ -232,7 +235,7 @@ __device__ __forceinline__ void load_head(TileQKV& t, const bf16_t* W, int row0,
 
 // KV sub-block [b0, b0 + SUB) of the chunk, restricted to old positions (< min(bend, Lold)).
 template <bool BB>
-__device__ __forceinline__ void load_kv(TileKV& t, const KArgs& a, int layer, int kvh, int b0, int lim, int mw, int lane) {
+__device__ __forceinline__ void load_kv(TileKV<BB>& t, const KArgs& a, int layer, int kvh, int b0, int lim, int mw, int lane) {
   constexpr int JJ = KVGeo<BB>::JJ, PPP = KVGeo<BB>::PPP;
   const size_t head_base = ((size_t)layer * NKVH + kvh) * (size_t)a.max_seq;
 #pragma unroll
@@ -261,7 +264,7 @@ __device__ __forceinline__ void load_kv(TileKV& t, const KArgs& a, int layer, in
   }
 }
 template <bool BB>
-__device__ __forceinline__ void unpack8(const TileKV& t, bool key, int jj, float* o) {
+__device__ __forceinline__ void unpack8(const TileKV<BB>& t, bool key, int jj, float* o) {
   if constexpr (BB) {
     const u32x4 w = key ? t.k[jj] : t.v[jj];
     o[0] = bflo(w.x); o[1] = bfhi(w.x); o[2] = bflo(w.y); o[3] = bfhi(w.y);
@@ -438,7 +441,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   TileO to;
   TileGU tgu;
   TileD td;
-  TileKV tk;
+  TileKV<BB> tk;
 
   auto tag_of = [&](int lp, int slot) -> uint32_t { return a.tag_base + (uint32_t)(lp * T_NSLOT + slot); };
   const bool cp_greedy = a.cp_frame && !a.sel.do_sample;
@@ -705,7 +708,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
 #pragma unroll
         for (int w = 0; w < NMATH; ++w) M = s.redm[sb & 1][w][h] > M ? s.redm[sb & 1][w][h] : M;
         mn[h] = M;
-        alpha[h] = exp(m[h] == -INFINITY ? NEG : m[h] - mn[h]);
+        alpha[h] = sb == 0 ? 0.0 : exp(m[h] == -INFINITY ? NEG : m[h] - mn[h]);
       }
       double pr[2 * JJ];
 #pragma unroll
@@ -737,11 +740,17 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       m[1] = mn[1];
     }
     // lane-major layout: each store of the wave writes 64 consecutive doubles (no bank conflicts)
+    // the wave's softmax sums (its 4 lane groups), one value per head
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      l[h] += xlane_d<4>(l[h]);
+      l[h] += xlane_d<5>(l[h]);
+    }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) s.red[mw][h][i][lane] = acc[h][i];
-      if ((lane & 15) == 0) s.redl[mw][g][h] = l[h];
+      if (lane == 0) s.redl[mw][0][h] = l[h];
     }
     step_barrier();
     // thread t merges dim d = 8 j + i of head h, reading row i at columns 16 g + j (contiguous in j)
@@ -751,7 +760,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
 #pragma unroll
     for (int w = 0; w < NMATH; ++w) {
       A += (s.red[w][h][ii][jj0] + s.red[w][h][ii][16 + jj0]) + (s.red[w][h][ii][32 + jj0] + s.red[w][h][ii][48 + jj0]);
-      Lsum += (s.redl[w][0][h] + s.redl[w][1][h]) + (s.redl[w][2][h] + s.redl[w][3][h]);
+      Lsum += s.redl[w][0][h];
     }
     const double Mw = h ? m[1] : m[0];
     if (local) {
@@ -1094,7 +1103,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
         case S_QKV:
           math_qkv(lp);
           if (q.has_chunk) load_kv<BB>(tk, a, layer, xcd, q.c0, min(q.c1, q.L - 1), mw, lane);
-          else tk = TileKV{};
+          else tk = TileKV<BB>{};
           if (q.local) load_o<BB>(to, LW, layer, xcd, li, mw, lane);
           break;
         case S_ATT:
