@@ -99,6 +99,41 @@ def cpu_baseline(sample_seconds: float = 15.0) -> dict:
                       f"PyTorch oracle) in {el:.1f} s"}
 
 
+def batched_c4(pkg, sd, frames: int = 10) -> dict:
+    """Config 4: 8 independent streams with ragged attended lengths in [128, 1024]; one frame =
+    per stream one backbone step (head + greedy g0) and one code-predictor frame."""
+    import torch
+    g = torch.Generator().manual_seed(1238)
+    lengths = [int(x) for x in torch.randint(128, 1025, (8,), generator=g)]
+    dec = pkg.BatchedTTSDecoder(sd, 8, max_seq_len=max(lengths) + frames + 8)
+    gd = torch.Generator(device="cuda").manual_seed(7)
+    for s, L in enumerate(lengths):
+        k = torch.randn(28, 8, L - 1, 128, generator=gd, device="cuda").to(torch.bfloat16)
+        v = torch.randn(28, 8, L - 1, 128, generator=gd, device="cuda").to(torch.bfloat16)
+        dec.set_kv_cache(s, k, v)
+    i32 = dict(dtype=torch.int32, device="cuda")
+    g0 = torch.zeros(8, **i32)
+    toks = torch.zeros(8, 16, **i32)
+    comb = torch.randn(8, 1024, generator=gd, device="cuda").to(torch.bfloat16)
+    text = torch.randn(8, 1024, generator=gd, device="cuda").to(torch.bfloat16)
+
+    def frame(i):
+        hidden = dec.step_select(comb, g0, -1, frame_step=i)
+        dec.cp_frames(hidden, g0, text, toks, comb, frame_step=i)
+
+    frame(0)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(frames):
+        frame(1 + i)
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    dec.check_error()
+    return {"streams": 8, "lengths": lengths, "frames": frames,
+            "frames_per_s_total": round(8 * frames / el, 2), "frames_per_s_per_stream": round(frames / el, 2),
+            "note": "per-stream launches of the batch-1 kernels over shared weights"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -106,6 +141,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-batched", action="store_true", help="skip the batch-8 ragged-context figure")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device-to-device copies of MIB MiB (the reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes) and exit")
@@ -214,6 +250,8 @@ def main():
                      "unit": "GB/s", "frac": round(dominant[1] / HBM_PEAK_GBS, 4),
                      "algorithmic_bytes": dominant[2], "traffic": dominant[3]},
     }
+    if not args.no_batched:
+        out["batched_c4"] = batched_c4(pkg, sd)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)

@@ -1,0 +1,88 @@
+"""Decode of several independent streams (batch 8, ragged KV lengths).
+
+Each stream keeps its own backbone KV cache and position; all streams share one copy of the
+weights and one code-predictor decoder (its KV cache is rebuilt every frame). A frame of the
+batch is, per stream, one backbone step with codec head + selection and one code-predictor
+frame, each a single persistent-kernel launch queued on the current stream with no host sync.
+
+The reference has no batched decode (its megakernels are batch 1, fused_decode_tts.cu:728-831);
+this is the build's batch-1 kernels applied per stream, which keeps every stream bit-identical
+to its batch-1 result. A kernel that shares each weight tile across the streams of a layer
+pass (MFMA bf16 tiles when the batch makes the projections dense) is the planned next step.
+"""
+from __future__ import annotations
+
+from typing import List, Optional, Sequence
+
+import torch
+
+from .megakernel_backbone import TTSMegakernelGenerator
+from .megakernel_code_predictor import CodePredictorMegakernelGenerator
+
+
+class BatchedTTSDecoder:
+    """``n_streams`` backbone decoders over shared weights plus one code predictor."""
+
+    def __init__(self, model, n_streams: int, max_seq_len: int = 4096, cp_max_seq_len: int = 32,
+                 device="cuda"):
+        if n_streams < 1:
+            raise ValueError("n_streams must be >= 1")
+        self.streams: List[TTSMegakernelGenerator] = [
+            TTSMegakernelGenerator(model=model, max_seq_len=max_seq_len, device=device) for _ in range(n_streams)]
+        self.cp = CodePredictorMegakernelGenerator(model=model, max_seq_len=cp_max_seq_len, device=device)
+        self.n_streams = n_streams
+        self.device = torch.device(device)
+        self.vocab_size = self.streams[0].vocab_size
+
+    def set_kv_cache(self, stream: int, k: torch.Tensor, v: torch.Tensor):
+        """Prefix KV of one stream ([layers, 8, S, 128]); the stream continues at position S."""
+        dec = self.streams[stream]
+        dec.set_kv_cache(k, v)
+        dec.set_position(int(k.shape[2]))
+
+    def positions(self) -> List[int]:
+        return [s.position for s in self.streams]
+
+    def step_select(self, embeds: torch.Tensor, tokens_out: torch.Tensor, eos_id: int,
+                    history: Optional[torch.Tensor] = None, n_history: Sequence[int] = (),
+                    repetition_penalty: float = 1.0, suppress_eos: bool = False, do_sample: bool = False,
+                    temperature: float = 0.9, top_k: int = 50, top_p: float = 1.0, seed: int = 0,
+                    frame_step: int = 0) -> torch.Tensor:
+        """One backbone step per stream at its own position, codec head, suppress mask (ids
+        [V-1024, V) except EOS), optional repetition penalty and selection of each stream's
+        group-0 token into ``tokens_out[s]`` (device int32). Returns the final-norm hiddens
+        (f32 [n_streams, 1024], device)."""
+        if embeds.shape != (self.n_streams, 1024):
+            raise ValueError(f"embeds must be [{self.n_streams}, 1024], got {tuple(embeds.shape)}")
+        if tokens_out.dtype != torch.int32 or tokens_out.numel() < self.n_streams:
+            raise ValueError("tokens_out must be a device int32 tensor with one entry per stream")
+        emb = embeds.to(self.device, torch.bfloat16)
+        empty = torch.zeros(1, dtype=torch.int32, device=self.device)
+        hidden = torch.empty(self.n_streams, 1024, dtype=torch.float32, device=self.device)
+        for s, dec in enumerate(self.streams):
+            hist = history[s] if history is not None else empty
+            nh = int(n_history[s]) if n_history else 0
+            dec.decoder.decode_step_select(emb[s], tokens_out[s:s + 1], hist, nh, float(repetition_penalty),
+                                           int(eos_id), bool(suppress_eos), bool(do_sample), float(temperature),
+                                           int(top_k), float(top_p), int(seed) + s, int(frame_step))
+            hidden[s].copy_(dec.decoder.hidden_state_buffer())
+        return hidden
+
+    def cp_frames(self, hidden: torch.Tensor, g0: torch.Tensor, text_rows: Optional[torch.Tensor],
+                  tokens_out: torch.Tensor, combined_out: torch.Tensor, eos_id: int = -1,
+                  do_sample: bool = False, temperature: float = 0.9, top_k: int = 50, seed: int = 0,
+                  frame_step: int = 0) -> None:
+        """A code-predictor frame per stream: ``tokens_out[s]`` (int32 [16]) gets g0 and the 15
+        group ids, ``combined_out[s]`` (bf16 [1024]) the embedding sum plus ``text_rows[s]``."""
+        done = torch.zeros(self.n_streams, dtype=torch.int32, device=self.device)
+        for s in range(self.n_streams):
+            text = text_rows[s] if text_rows is not None else torch.zeros(1024, dtype=torch.bfloat16,
+                                                                            device=self.device)
+            self.cp.decoder.frame(hidden[s], g0[s:s + 1], text, tokens_out[s], combined_out[s], int(eos_id),
+                                  done[s:s + 1], bool(do_sample), float(temperature), int(top_k), 1.0,
+                                  int(seed) + s, int(frame_step))
+
+    def check_error(self):
+        for dec in self.streams:
+            dec.check_error()
+        self.cp.check_error()

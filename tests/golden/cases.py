@@ -6,6 +6,8 @@
   c1  code-predictor frame: 15 greedy groups from a backbone hidden and a group-0 id
   c2  frame loop: 128-token prefill, 64 greedy frames; 32 sampled frames (top-k 50, T 0.9)
   c3  long context: KV of 2044 tokens, 4 decode steps with distinct monotone (t, h, w)
+  c4  batch of 8 streams with ragged attended lengths in [128, 1024]: one backbone step
+      (codec head, suppress mask, greedy g0) and one code-predictor frame per stream
 """
 from __future__ import annotations
 
@@ -15,7 +17,8 @@ from pathlib import Path
 import torch
 
 HERE = Path(__file__).resolve().parent
-SEEDS = {"c0": 1234, "c1": 1235, "c2": 1236, "c3": 1237}
+SEEDS = {"c0": 1234, "c1": 1235, "c2": 1236, "c3": 1237, "c4": 1238}
+C4_STREAMS = 8
 EOS_ID = 2150
 C2_GREEDY_FRAMES = 64
 C2_SAMPLED_FRAMES = 32
@@ -76,6 +79,22 @@ def c3_inputs():
     v = torch.randn(28, 8, C3_KV, 128, generator=g).to(torch.bfloat16)
     xs = torch.randn(C3_STEPS, 1024, generator=g).to(torch.bfloat16)
     return k, v, xs
+
+
+def c4_lengths():
+    """Ragged attended KV lengths of the 8 streams, uniform in [128, 1024]."""
+    g = _gen("c4")
+    return [int(x) for x in torch.randint(128, 1025, (C4_STREAMS,), generator=g)]
+
+
+def c4_stream_inputs(s: int, L: int):
+    """Stream s: KV of L - 1 cached tokens, the decode input, the text row of its frame."""
+    g = _gen("c4", 200 + s)
+    k = torch.randn(28, 8, L - 1, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(28, 8, L - 1, 128, generator=g).to(torch.bfloat16)
+    x = torch.randn(1024, generator=g).to(torch.bfloat16)
+    text = torch.randn(1024, generator=g).to(torch.bfloat16)
+    return k, v, x, text
 
 
 def load(name: str):

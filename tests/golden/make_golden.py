@@ -1,6 +1,7 @@
 """Write the golden fixtures of tests/golden/ from the CPU oracle.
 
-    python tests/golden/make_golden.py            # all cases (about 2 minutes on 8 cores)
+    python tests/golden/make_golden.py            # all cases (about 3 minutes on 8 cores)
+    python tests/golden/make_golden.py c4         # selected cases only (manifest entries merged)
 
 The reference ships no golden vectors for this path (its tests check audio RMS and duration
 on real weights), so the fixtures are the oracle's outputs on the seeded cases of
@@ -25,7 +26,8 @@ sys.path.insert(0, str(HERE.parent))
 
 import __graft_entry__  # noqa: E402
 from golden import cases  # noqa: E402
-from oracle.qtts_oracle import DecoderOracle, TalkerOracle, TalkerWeights, head_logits  # noqa: E402
+from oracle.qtts_oracle import (DecoderOracle, TalkerOracle, TalkerWeights, head_logits, sample_token,  # noqa: E402
+                                suppress_mask)
 
 
 def log(*a):
@@ -36,13 +38,32 @@ def f32(t):
     return t.detach().float().cpu().numpy().astype(np.float32)
 
 
-def main():
+def main(selected):
     torch.set_num_threads(8)
     pkg = __graft_entry__.import_package()
+    mpath = HERE / "manifest.json"
     manifest = {"generator": "tests/golden/make_golden.py", "oracle": "oracle/qtts_oracle.py",
                 "torch": torch.__version__, "cases": {}}
+    if selected and mpath.exists():
+        manifest["cases"] = json.loads(mpath.read_text())["cases"]
+    want = lambda c: not selected or c in selected
 
-    # c0: config-0 backbone step, both gain variants, kernel and HF-bf16 policies
+    if want("c0"):
+        c0(pkg, manifest)
+    if want("c1"):
+        c1(pkg, manifest)
+    if want("c2"):
+        c2(pkg, manifest)
+    if want("c3"):
+        c3(pkg, manifest)
+    if want("c4"):
+        c4(pkg, manifest)
+    mpath.write_text(json.dumps(manifest, indent=1) + "\n")
+    log("done")
+
+
+def c0(pkg, manifest):
+    """Config-0 backbone step, both gain variants, kernel and HF-bf16 policies."""
     prefill, x = cases.c0_inputs()
     out = {}
     for nm in (0.0, 1.0):
@@ -61,7 +82,9 @@ def main():
             del o
     np.savez_compressed(HERE / "c0_backbone.npz", **out)
 
-    # c1: one code-predictor frame (greedy)
+
+def c1(pkg, manifest):
+    """One code-predictor frame (greedy)."""
     sd = cases.weights(pkg, "c1")
     tw = TalkerWeights.from_state_dict(sd, 28, 5)
     hidden, g0, text = cases.c1_inputs()
@@ -72,7 +95,9 @@ def main():
     manifest["cases"]["c1"] = {"seed": cases.SEEDS["c1"], "norm_mean": 1.0, "weights": cases.weight_digest(sd), "g0": g0}
     log("c1 tokens", [g0] + toks)
 
-    # c2: frame loop, greedy and sampled
+
+def c2(pkg, manifest):
+    """Frame loop, greedy and sampled."""
     sd = cases.weights(pkg, "c2")
     tw = TalkerWeights.from_state_dict(sd, 28, 5)
     prefill, trailing, pad = cases.c2_inputs()
@@ -91,7 +116,9 @@ def main():
                                "eos_id": cases.EOS_ID, "greedy_frames": len(greedy), "sampled_frames": len(sampled),
                                "sampling": s}
 
-    # c3: long context, distinct monotone (t, h, w)
+
+def c3(pkg, manifest):
+    """Long context, distinct monotone (t, h, w)."""
     sd = cases.weights(pkg, "c3")
     tw = TalkerWeights.from_state_dict(sd, 28, 5)
     k, v, xs = cases.c3_inputs()
@@ -109,9 +136,34 @@ def main():
                                "pos3": [cases.c3_pos3(cases.C3_KV + j) for j in range(cases.C3_STEPS)]}
     log("c3 argmax", [int(l.argmax()) for l in lgs])
 
-    (HERE / "manifest.json").write_text(json.dumps(manifest, indent=1) + "\n")
-    log("done")
+
+def c4(pkg, manifest):
+    """Batch of 8 streams with ragged attended lengths: per stream one backbone step at its
+    position (codec head, suppress mask, greedy g0) and one greedy code-predictor frame."""
+    sd = cases.weights(pkg, "c4")
+    tw = TalkerWeights.from_state_dict(sd, 28, 5)
+    lengths = cases.c4_lengths()
+    talker = TalkerOracle(tw, max_seq=max(lengths) + 1)
+    mask = suppress_mask(tw.codec_head.shape[0], cases.EOS_ID)
+    hid, toks, comb = [], [], []
+    for s, L in enumerate(lengths):
+        k, v, x, text = cases.c4_stream_inputs(s, L)
+        talker.bb.reset()
+        talker.bb.set_kv(k, v)
+        h, _ = talker.bb.step(x, pos=L - 1)
+        lg = head_logits(tw.codec_head, h)
+        lg[mask] = float("-inf")
+        g0 = sample_token(lg, False, 1.0, 0, 1.0)
+        groups = [g0] + talker.cp_frame(h, g0)
+        hid.append(f32(h))
+        toks.append(groups)
+        comb.append(f32(talker.combine(groups, text)))
+        log(f"c4 stream {s} L={L}: {groups[:4]}...")
+    np.savez_compressed(HERE / "c4_batched.npz", lengths=np.array(lengths, dtype=np.int32), hidden=np.stack(hid),
+                        tokens=np.array(toks, dtype=np.int32), combined=np.stack(comb))
+    manifest["cases"]["c4"] = {"seed": cases.SEEDS["c4"], "norm_mean": 1.0, "weights": cases.weight_digest(sd),
+                               "streams": len(lengths), "lengths": lengths, "eos_id": cases.EOS_ID}
 
 
 if __name__ == "__main__":
-    main()
+    main(sys.argv[1:])
