@@ -556,6 +556,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     for (int j = 0; j < 16; ++j) s.hb[16 * lane + j] = rbf(s.hb[16 * lane + j]);
   };
   // ---- poller: q/k norm, RoPE, KV write for layer `layer` at position pos
+  bool kv_pending = false;
   auto prep_att = [&](int lp, int layer, int pos, int C) {
     const int par = lp & 1;
     poll_vec<4>(P, ws->qkv[xcd][par], LROWS, tag_of(lp, T_QKV), s.stage);
@@ -592,7 +593,9 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
         kc[c] = kl; kc[c + 64] = kh;
         vc[c] = vl; vc[c + 64] = vh;
       }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      // ordered before this wave's next slot publish (prep_gu), where the wait for the stores
+      // costs nothing: the entry is read from memory only at later positions or launches
+      kv_pending = true;
     }
   };
   // ---- poller: collect the C attention partials; per head the chunk weights
@@ -617,6 +620,10 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   auto prep_gu = [&](int lp, int layer) {
     const int par = lp & 1;
     poll_parts(P, ws->opart[par], 32 * li, tag_of(lp, T_OPART), s.stage);
+    if (kv_pending) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");   // the KV entry written in prep_att
+      kv_pending = false;
+    }
     if (lane < 32) {
       // h1 = x + sum of the 8 XCD partials, added in this order in f64
       double acc = (double)s.xres[32 * li + lane];
