@@ -87,6 +87,11 @@ template <class T>
 __device__ __forceinline__ T ld_const(const T* p) {
   return *(const __attribute__((address_space(4))) T*)p;
 }
+// store through the global address space (a global_store, not a flat one)
+template <class T>
+__device__ __forceinline__ void gput(T* p, T v) {
+  *(__attribute__((address_space(1))) T*)p = v;
+}
 __device__ __forceinline__ u32x4 ldw(const bf16_t* p) { return *gmem(reinterpret_cast<const u32x4*>(p)); }
 __device__ __forceinline__ float ldbf(const bf16_t* p) { return bf2f(*gmem(p)); }
 __device__ __forceinline__ u32x4 ldw_nt(const bf16_t* p) {

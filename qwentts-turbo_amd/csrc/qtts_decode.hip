@@ -116,21 +116,21 @@ struct Lds {
   double redl[NMATH][4][2];         // their softmax sums
   double redm[2][NMATH][2];         // per (pass parity, wave, head) score max
   double wts[2][MAXC + 1];          // per head: chunk weights exp(m_c - M), then 1 / Z
-  float q[2][HDIM];
-  float knew[HDIM];
-  float vnew[HDIM];
-  float attp[MAXC * APS];  // raw attention partials of the XCD's chunks (poller -> math)
+  alignas(16) float q[2][HDIM];
+  alignas(16) float knew[HDIM];
+  alignas(16) float vnew[HDIM];
+  alignas(16) float attp[MAXC * APS];  // raw attention partials of the XCD's chunks (poller -> math)
   float attn[2 * HDIM];    // merged attention output of the XCD's two heads
   float hbv[NMATH];        // greedy head: best logit of each math wave ...
   int hbi[NMATH];          // ... and its vocabulary id
-  float xn[HID];
-  float hn[HID];
+  alignas(16) float xn[HID];
+  alignas(16) float hn[HID];
   float inter[XI];
-  float hb[HID];
+  alignas(16) float hb[HID];
   // poller-only from here
-  float xres[HID];
-  float h1res[HID];
-  float stage[MAXC * APS > MAXV ? MAXC * APS : MAXV];
+  alignas(16) float xres[HID];
+  alignas(16) float h1res[HID];
+  alignas(16) float stage[MAXC * APS > MAXV ? MAXC * APS : MAXV];
   uint32_t pen_bits[MAXV / 32];
   int tok[32];
   SelScratch sel;
@@ -290,10 +290,12 @@ __device__ __forceinline__ uint32_t ws_off(const Poll& P, const void* p) {
   return (uint32_t)(reinterpret_cast<const char*>(p) - reinterpret_cast<const char*>(P.base));
 }
 
-// Poll npair 16-byte pairs; pair i lives at byte offset off(i) of the workspace.
+// Poll npair 16-byte pairs (two tagged slots each) into registers: pair k of this lane, index
+// i = lane + 64 k (i < npair), lives at byte offset off(i) of the workspace and lands in
+// out[2 k], out[2 k + 1]. Returns false on timeout (error word set).
 template <int MAXP, typename OffF>
-__device__ bool poll_pairs(const Poll& P, int npair, uint32_t tag, float* dst, OffF off) {
-  const int lane = threadIdx.x & 63;
+__device__ bool poll_regs(const Poll& P, int npair, uint32_t tag, float (&out)[2 * MAXP], OffF off) {
+  const int lane = opaque((int)threadIdx.x & 63);   // keeps slot offsets from being hoisted and spilled
   uint32_t valid = 0;
 #pragma unroll
   for (int k = 0; k < MAXP; ++k)
@@ -304,9 +306,8 @@ __device__ bool poll_pairs(const Poll& P, int npair, uint32_t tag, float* dst, O
 #pragma unroll
     for (int k = 0; k < MAXP; ++k) {
       if ((pending & (1u << k)) && v[k].y == tag && v[k].w == tag) {
-        const int i = 2 * (lane + 64 * k);
-        dst[i] = __uint_as_float(v[k].x);
-        dst[i + 1] = __uint_as_float(v[k].z);
+        out[2 * k] = __uint_as_float(v[k].x);
+        out[2 * k + 1] = __uint_as_float(v[k].z);
         pending &= ~(1u << k);
       }
     }
@@ -350,34 +351,50 @@ __device__ bool poll_pairs(const Poll& P, int npair, uint32_t tag, float* dst, O
     }
   }
 }
+// Poll npair pairs into LDS: pair i to dst[2 i], dst[2 i + 1].
+template <int MAXP, typename OffF>
+__device__ bool poll_pairs(const Poll& P, int npair, uint32_t tag, float* dst, OffF off) {
+  float v[2 * MAXP];
+  const bool ok = poll_regs<MAXP>(P, npair, tag, v, off);
+  const int lane = opaque((int)threadIdx.x & 63);
+#pragma unroll
+  for (int k = 0; k < MAXP; ++k)
+    if (lane + 64 * k < npair) *reinterpret_cast<float2*>(dst + 2 * (lane + 64 * k)) = make_float2(v[2 * k], v[2 * k + 1]);
+  return ok;
+}
 // contiguous n slots (n even) starting at p
 template <int MAXP>
 __device__ __forceinline__ bool poll_vec(const Poll& P, const uint64_t* p, int n, uint32_t tag, float* dst) {
   const uint32_t o = ws_off(P, p);
   return poll_pairs<MAXP>(P, n >> 1, tag, dst, [o](int i) { return o + 16u * (uint32_t)i; });
 }
-// the 8 XCD partials of rows [r0, r0 + 32): dst[32 x + r]
-__device__ __forceinline__ bool poll_parts(const Poll& P, const uint64_t (*part)[HID], int r0, uint32_t tag, float* dst) {
+// contiguous 1024 slots into registers: this lane gets elements 2 (lane + 64 k) + {0, 1}
+__device__ __forceinline__ bool poll_vec_regs(const Poll& P, const uint64_t* p, uint32_t tag, float (&out)[16]) {
+  const uint32_t o = ws_off(P, p);
+  return poll_regs<8>(P, HID / 2, tag, out, [o](int i) { return o + 16u * (uint32_t)i; });
+}
+// Sum of the 8 XCD partials of rows r0 + 2 (lane & 15) + {0, 1}: lane group g = lane >> 4 polls
+// XCDs 2 g and 2 g + 1 and adds them; two exchanges (lane ^ 16, lane ^ 32) complete the sum as
+// ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7)), bit-identical in every lane and workgroup.
+__device__ __forceinline__ bool poll_sum8(const Poll& P, const uint64_t (*part)[HID], int r0, uint32_t tag, double& s0, double& s1) {
   const uint32_t o = ws_off(P, &part[0][r0]);
-  return poll_pairs<2>(P, 128, tag, dst, [o](int i) { return o + (uint32_t)(i >> 4) * (HID * 8u) + 16u * (uint32_t)(i & 15); });
+  float v[4];
+  const bool ok = poll_regs<2>(P, 128, tag, v, [o](int i) {
+    const uint32_t x = 2u * (uint32_t)((i & 63) >> 4) + (uint32_t)(i >> 6);
+    return o + x * (HID * 8u) + 16u * (uint32_t)(i & 15);
+  });
+  s0 = (double)v[0] + (double)v[2];
+  s1 = (double)v[1] + (double)v[3];
+  s0 += xlane_d<4>(s0);
+  s1 += xlane_d<4>(s1);
+  s0 += xlane_d<5>(s0);
+  s1 += xlane_d<5>(s1);
+  return ok;
 }
 
 // RMSNorm epsilon: the f32 constant 1e-6f of the reference, used in f64 arithmetic.
 constexpr double EPSD = (double)1e-6f;
 
-// one-wave RMSNorm statistic of v[0..1024): 1 / sqrt(mean(v^2) + eps), in f64
-__device__ __forceinline__ double wave_rstd(const float* v) {
-  const int lane = threadIdx.x & 63;
-  double ss = 0.0;
-#pragma unroll
-  for (int j = 0; j < HID / 64; ++j) { const double x = (double)v[lane + 64 * j]; ss = fma(x, x, ss); }
-  ss = group_sum<64>(ss);
-  return 1.0 / sqrt(ss / (double)HID + EPSD);
-}
-// normalized value (x * rstd) * gain, computed in f64 and stored as f32
-__device__ __forceinline__ float norm_f32(float x, double rstd, bf16_t g) {
-  return (float)(((double)x * rstd) * (double)bf2f(g));
-}
 
 // Workgroup barrier: makes LDS data one wave wrote visible to the others. Used at every step
 // boundary and inside the attention steps; both roles reach it the same number of times (the
@@ -458,140 +475,170 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   };
 
   // ---- poller registers: small per-layer vectors, loaded a step (or a layer) before use so
-  // that no dependent global load sits on the critical path of a step.
-  //   g_in / g_post: RMSNorm gains of elements [16 lane, 16 lane + 16) (8 packed bf16 pairs)
-  //   qn/kn: q/k-norm gains of channels lane, lane + 64; rope: cos/sin of those channels
+  // that no dependent global load sits on the critical path of a step. The poller lane owns
+  // hidden elements 2 (lane + 64 k) + {0, 1} (k < 8) and head channels c0 = 2 lane, c0 + 1.
+  //   g_in / g_post / g_fin: RMSNorm gains of the lane's 16 elements (8 packed bf16 pairs)
+  //   qn2 / kn2: q/k-norm gains of channels c0, c0 + 1 (packed); rc / rs: their cos / sin
   uint32_t g_in[8], g_post[8], g_fin[8];
-  float qn_l, qn_h, kn_l, kn_h, cl_, sl_, ch_, sh_;
-  auto load_gain16 = [&](uint32_t (&g)[8], const bf16_t* src) {
-    const u32x4 a0 = ldw(src + 16 * lane), a1 = ldw(src + 16 * lane + 8);
-    g[0] = a0.x; g[1] = a0.y; g[2] = a0.z; g[3] = a0.w; g[4] = a1.x; g[5] = a1.y; g[6] = a1.z; g[7] = a1.w;
+  uint32_t qn2, kn2;
+  float rc[2], rsn[2];
+  auto load_gain_pairs = [&](uint32_t (&g)[8], const bf16_t* src) {
+    const auto* p = gmem(reinterpret_cast<const uint32_t*>(src));
+#pragma unroll
+    for (int k = 0; k < 8; ++k) g[k] = p[lane + 64 * k];
   };
   auto load_qk_gains = [&](int layer) {
-    const bf16_t* qn = lw(LW, layer, W_QN);
-    const bf16_t* kn = lw(LW, layer, W_KN);
-    qn_l = ldbf(qn + lane); qn_h = ldbf(qn + lane + 64);
-    kn_l = ldbf(kn + lane); kn_h = ldbf(kn + lane + 64);
+    qn2 = *gmem(reinterpret_cast<const uint32_t*>(lw(LW, layer, W_QN)) + lane);
+    kn2 = *gmem(reinterpret_cast<const uint32_t*>(lw(LW, layer, W_KN)) + lane);
   };
   auto load_rope = [&](int pos) {
-    const int row = rot_row(lane, pos);
-    cl_ = ldbf(a.cos_t + (size_t)row * HDIM + lane);
-    sl_ = ldbf(a.sin_t + (size_t)row * HDIM + lane);
-    ch_ = ldbf(a.cos_t + (size_t)row * HDIM + lane + 64);
-    sh_ = ldbf(a.sin_t + (size_t)row * HDIM + lane + 64);
-  };
-  // RMSNorm of x (LDS, 1024 f32) with gains g: out[i] = f32((x_i * rstd) * g_i), f64 math
-  auto norm16 = [&](const float* x, float* out, const uint32_t (&g)[8], bool round_bf16) {
-    float xv[16];
-    double ss = 0.0;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) { xv[j] = x[16 * lane + j]; ss = fma((double)xv[j], (double)xv[j], ss); }
-    ss = group_sum<64>(ss);
-    const double rstd = 1.0 / sqrt(ss / (double)HID + EPSD);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const double gj = (j & 1) ? (double)bfhi(g[j >> 1]) : (double)bflo(g[j >> 1]);
-      const float v = (float)(((double)xv[j] * rstd) * gj);
-      out[16 * lane + j] = round_bf16 ? rbf(v) : v;
+    for (int j = 0; j < 2; ++j) {
+      const int c = 2 * lane + j;
+      const size_t row = (size_t)rot_row(c & 63, pos) * HDIM;
+      rc[j] = ldbf(a.cos_t + row + c);
+      rsn[j] = ldbf(a.sin_t + row + c);
     }
+  };
+  // RMSNorm statistic of the lane-distributed 1024-vector: 1 / sqrt(mean(x^2) + eps) in f64
+  auto rstd_of = [&](const float (&xv)[16]) -> double {
+    double s4[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) s4[j & 3] = fma((double)xv[j], (double)xv[j], s4[j & 3]);
+    const double ss = group_sum<64>((s4[0] + s4[1]) + (s4[2] + s4[3]));
+    return 1.0 / sqrt(ss / (double)HID + EPSD);
+  };
+  // normalized values f32((x * rstd) * g) of the lane's 16 elements
+  auto normed = [&](const float (&xv)[16], const uint32_t (&g)[8], float (&y)[16]) {
+    const double r = rstd_of(xv);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) y[j] = (float)(((double)xv[j] * r) * (double)((j & 1) ? bfhi(g[j >> 1]) : bflo(g[j >> 1])));
+  };
+  auto store_pairs = [&](float* dst, const float (&v)[16]) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) *reinterpret_cast<float2*>(dst + 2 * (lane + 64 * k)) = make_float2(v[2 * k], v[2 * k + 1]);
+  };
+  // one 16-byte store of two adjacent XCD-local slots
+  auto pub_local2 = [&](const uint64_t* p, float v0, float v1, uint32_t tag) {
+    const u32x4 d = {__float_as_uint(v0), tag, __float_as_uint(v1), tag};
+    __builtin_amdgcn_raw_buffer_store_b128(d, P.rs, (int)ws_off(P, p), 0, 0);
   };
 
   // ---- poller: input of layer 0 of position pi (embedding source) -> xres, xn
   auto prep_input0 = [&](int pi) {
-    const bf16_t* src = nullptr;
-    if (a.cp_frame) {
-      if (pi == 0) {
-        for (int i = lane; i < HID; i += 64) s.xres[i] = rbf(*gmem(a.bb_hidden + i));
-      } else if (pi == 1) {
-        src = a.bb_emb + (size_t)g0 * HID;
-      } else {
-        src = ld_const(a.cp_embs + (pi - 2)) + (size_t)s.tok[pi - 2] * HID;
+    float xv[16];
+    if (a.cp_frame && pi == 0) {
+      const auto* p = gmem(reinterpret_cast<const u32x2*>(a.bb_hidden));
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const u32x2 v = p[lane + 64 * k];
+        xv[2 * k] = rbf(__uint_as_float(v.x));
+        xv[2 * k + 1] = rbf(__uint_as_float(v.y));
       }
     } else {
-      src = a.in_emb != nullptr ? a.in_emb : a.embed_w + (size_t)a.in_tok * HID;
-    }
-    if (src != nullptr) {
-      const u32x4 a0 = ldw(src + 16 * lane), a1 = ldw(src + 16 * lane + 8);
-      const uint32_t w[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      const bf16_t* src;
+      if (a.cp_frame) src = pi == 1 ? a.bb_emb + (size_t)g0 * HID : ld_const(a.cp_embs + (pi - 2)) + (size_t)s.tok[pi - 2] * HID;
+      else src = a.in_emb != nullptr ? a.in_emb : a.embed_w + (size_t)a.in_tok * HID;
+      const auto* p = gmem(reinterpret_cast<const uint32_t*>(src));
 #pragma unroll
-      for (int j = 0; j < 8; ++j) { s.xres[16 * lane + 2 * j] = bflo(w[j]); s.xres[16 * lane + 2 * j + 1] = bfhi(w[j]); }
+      for (int k = 0; k < 8; ++k) { const uint32_t w = p[lane + 64 * k]; xv[2 * k] = bflo(w); xv[2 * k + 1] = bfhi(w); }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    norm16(s.xres, s.xn, g_in, false);
+    store_pairs(s.xres, xv);
+    float y[16];
+    normed(xv, g_in, y);
+    store_pairs(s.xn, y);
   };
 
   // ---- poller: AR2 of layer pass lp (down partials + residual) -> xl slots
   auto ar2 = [&](int lp) {
     const int par = lp & 1;
-    poll_parts(P, ws->dpart[par], 32 * li, tag_of(lp, T_DPART), s.stage);
-    if (lane < 32) {
-      // x' = h1 + sum of the 8 XCD partials, added in this order in f64
-      double acc = (double)s.h1res[32 * li + lane];
-#pragma unroll
-      for (int x = 0; x < NXCD; ++x) acc += (double)s.stage[32 * x + lane];
-      float xo = (float)acc;
-      if constexpr (BB) xo = rbf(xo);
-      pub_local(&ws->xl[xcd][par][32 * li + lane], xo, tag_of(lp, T_XL));
+    const int row = 32 * li + 2 * (lane & 15);
+    const float r0 = s.h1res[row], r1 = s.h1res[row + 1];
+    double s0, s1;
+    poll_sum8(P, ws->dpart[par], 32 * li, tag_of(lp, T_DPART), s0, s1);
+    if (lane < 16) {
+      // x' = h1 + the sum of the 8 XCD partials, in f64
+      float x0 = (float)((double)r0 + s0), x1 = (float)((double)r1 + s1);
+      if constexpr (BB) { x0 = rbf(x0); x1 = rbf(x1); }
+      pub_local2(&ws->xl[xcd][par][row], x0, x1, tag_of(lp, T_XL));
     }
   };
   // ---- poller: next layer input (after ar2 of lp) -> xres, xn
   auto prep_input_next = [&](int lp) {
-    poll_vec<8>(P, ws->xl[xcd][lp & 1], HID, tag_of(lp, T_XL), s.xres);
-    norm16(s.xres, s.xn, g_in, false);
+    float xv[16], y[16];
+    poll_vec_regs(P, ws->xl[xcd][lp & 1], tag_of(lp, T_XL), xv);
+    store_pairs(s.xres, xv);
+    normed(xv, g_in, y);
+    store_pairs(s.xn, y);
   };
   // ---- poller: final norm (after ar2 of lp) -> hb (bf16-rounded), outputs
   auto prep_final = [&](int lp) {
-    poll_vec<8>(P, ws->xl[xcd][lp & 1], HID, tag_of(lp, T_XL), s.xres);
-    norm16(s.xres, s.hb, g_fin, false);
+    float xv[16], y[16];
+    poll_vec_regs(P, ws->xl[xcd][lp & 1], tag_of(lp, T_XL), xv);
+    store_pairs(s.xres, xv);
+    normed(xv, g_fin, y);
     if (wg == 0) {
-      for (int i = lane; i < HID; i += 64) {
-        if (a.out_hidden) a.out_hidden[i] = s.hb[i];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int e = 2 * (lane + 64 * k);
+        if (a.out_hidden) *reinterpret_cast<float2*>(a.out_hidden + e) = make_float2(y[2 * k], y[2 * k + 1]);
         if (a.out_residual) {
-          if constexpr (BB) reinterpret_cast<bf16_t*>(a.out_residual)[i] = f2bf(s.xres[i]);
-          else reinterpret_cast<float*>(a.out_residual)[i] = s.xres[i];
+          if constexpr (BB)
+            reinterpret_cast<uint32_t*>(a.out_residual)[e >> 1] =
+                (uint32_t)f2bf(xv[2 * k]) | ((uint32_t)f2bf(xv[2 * k + 1]) << 16);
+          else
+            *reinterpret_cast<float2*>(reinterpret_cast<float*>(a.out_residual) + e) = make_float2(xv[2 * k], xv[2 * k + 1]);
         }
       }
     }
 #pragma unroll
-    for (int j = 0; j < 16; ++j) s.hb[16 * lane + j] = rbf(s.hb[16 * lane + j]);
+    for (int j = 0; j < 16; ++j) y[j] = rbf(y[j]);
+    store_pairs(s.hb, y);
   };
   // ---- poller: q/k norm, RoPE, KV write for layer `layer` at position pos
+  // The lane holds channels c0 = 2 lane, c0 + 1 of q head 0, q head 1, k and v. rotate_half pairs
+  // channel c with c + 64, which sits in lane ^ 32.
   bool kv_pending = false;
   auto prep_att = [&](int lp, int layer, int pos, int C) {
     const int par = lp & 1;
-    poll_vec<4>(P, ws->qkv[xcd][par], LROWS, tag_of(lp, T_QKV), s.stage);
-    const int c = lane;  // channels c and c + 64
-    const double cl = cl_, sl = sl_, ch = ch_, sh = sh_;
-    float outl[3], outh[3];
+    const double gq[2] = {bflo(qn2), bfhi(qn2)}, gk[2] = {bflo(kn2), bfhi(kn2)};
+    const double cs[2] = {rc[0], rc[1]}, sn[2] = {rsn[0], rsn[1]};
+    float v[8];   // [head][j]: head 0, 1 = q, 2 = k, 3 = v
+    {
+      const uint32_t o = ws_off(P, ws->qkv[xcd][par]);
+      poll_regs<4>(P, LROWS / 2, tag_of(lp, T_QKV), v, [o](int i) { return o + 16u * (uint32_t)i; });
+    }
+    double ss[3];
+#pragma unroll
+    for (int h = 0; h < 3; ++h) ss[h] = fma((double)v[2 * h], (double)v[2 * h], (double)v[2 * h + 1] * (double)v[2 * h + 1]);
+    group_sum_n<64, 3>(ss);
+    const bool lo = lane < 32;   // channels < 64
+    float out[3][2];
 #pragma unroll
     for (int h = 0; h < 3; ++h) {
-      const double xl_ = s.stage[128 * h + c], xh = s.stage[128 * h + c + 64];
-      const double ss = group_sum<64>(fma(xl_, xl_, xh * xh));
-      const double r = 1.0 / sqrt(ss / (double)HDIM + EPSD);
-      const double gl = h < 2 ? qn_l : kn_l, gh = h < 2 ? qn_h : kn_h;
-      const double nl = (xl_ * r) * gl, nh = (xh * r) * gh;
-      outl[h] = (float)(nl * cl - nh * sl);
-      outh[h] = (float)(nl * sh + nh * ch);
+      const double r = 1.0 / sqrt(ss[h] / (double)HDIM + EPSD);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const double n = ((double)v[2 * h + j] * r) * (h < 2 ? gq[j] : gk[j]);
+        const double pn = xlane_d<5>(n);   // channel c +- 64
+        out[h][j] = lo ? (float)(n * cs[j] - pn * sn[j]) : (float)(pn * sn[j] + n * cs[j]);
+      }
     }
-    s.q[0][c] = outl[0]; s.q[0][c + 64] = outh[0];
-    s.q[1][c] = outl[1]; s.q[1][c + 64] = outh[1];
-    float kl = outl[2], kh = outh[2];
-    float vl = s.stage[384 + c], vh = s.stage[384 + c + 64];
-    if constexpr (BB) { kl = rbf(kl); kh = rbf(kh); vl = rbf(vl); vh = rbf(vh); }
-    s.knew[c] = kl; s.knew[c + 64] = kh;
-    s.vnew[c] = vl; s.vnew[c + 64] = vh;
+    const int c0 = 2 * lane;
+    *reinterpret_cast<float2*>(&s.q[0][c0]) = make_float2(out[0][0], out[0][1]);
+    *reinterpret_cast<float2*>(&s.q[1][c0]) = make_float2(out[1][0], out[1][1]);
+    float k0 = out[2][0], k1 = out[2][1], v0 = v[6], v1 = v[7];
+    if constexpr (BB) { k0 = rbf(k0); k1 = rbf(k1); v0 = rbf(v0); v1 = rbf(v1); }
+    *reinterpret_cast<float2*>(&s.knew[c0]) = make_float2(k0, k1);
+    *reinterpret_cast<float2*>(&s.vnew[c0]) = make_float2(v0, v1);
     if (li == C - 1) {
-      const size_t off = (((size_t)layer * NKVH + xcd) * (size_t)a.max_seq + pos) * HDIM;
+      const size_t off = (((size_t)layer * NKVH + xcd) * (size_t)a.max_seq + pos) * HDIM + c0;
       if constexpr (BB) {
-        bf16_t* kc = reinterpret_cast<bf16_t*>(a.kc) + off;
-        bf16_t* vc = reinterpret_cast<bf16_t*>(a.vc) + off;
-        kc[c] = f2bf(kl); kc[c + 64] = f2bf(kh);
-        vc[c] = f2bf(vl); vc[c + 64] = f2bf(vh);
+        gput(reinterpret_cast<uint32_t*>(reinterpret_cast<bf16_t*>(a.kc) + off), (uint32_t)f2bf(k0) | ((uint32_t)f2bf(k1) << 16));
+        gput(reinterpret_cast<uint32_t*>(reinterpret_cast<bf16_t*>(a.vc) + off), (uint32_t)f2bf(v0) | ((uint32_t)f2bf(v1) << 16));
       } else {
-        float* kc = reinterpret_cast<float*>(a.kc) + off;
-        float* vc = reinterpret_cast<float*>(a.vc) + off;
-        kc[c] = kl; kc[c + 64] = kh;
-        vc[c] = vl; vc[c + 64] = vh;
+        gput(reinterpret_cast<u32x2*>(reinterpret_cast<float*>(a.kc) + off), u32x2{__float_as_uint(k0), __float_as_uint(k1)});
+        gput(reinterpret_cast<u32x2*>(reinterpret_cast<float*>(a.vc) + off), u32x2{__float_as_uint(v0), __float_as_uint(v1)});
       }
       // ordered before this wave's next slot publish (prep_gu), where the wait for the stores
       // costs nothing: the entry is read from memory only at later positions or launches
@@ -619,20 +666,21 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   // ---- poller: AR1 (O partials + residual) -> h1 slots; then h1 -> h1res, hn
   auto prep_gu = [&](int lp, int layer) {
     const int par = lp & 1;
-    poll_parts(P, ws->opart[par], 32 * li, tag_of(lp, T_OPART), s.stage);
+    const int row = 32 * li + 2 * (lane & 15);
+    const float r0 = s.xres[row], r1 = s.xres[row + 1];
+    double s0, s1;
+    poll_sum8(P, ws->opart[par], 32 * li, tag_of(lp, T_OPART), s0, s1);
     if (kv_pending) {
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");   // the KV entry written in prep_att
       kv_pending = false;
     }
-    if (lane < 32) {
-      // h1 = x + sum of the 8 XCD partials, added in this order in f64
-      double acc = (double)s.xres[32 * li + lane];
-#pragma unroll
-      for (int x = 0; x < NXCD; ++x) acc += (double)s.stage[32 * x + lane];
-      pub_local(&ws->h1[xcd][par][32 * li + lane], (float)acc, tag_of(lp, T_H1));
-    }
-    poll_vec<8>(P, ws->h1[xcd][par], HID, tag_of(lp, T_H1), s.h1res);
-    norm16(s.h1res, s.hn, g_post, false);
+    // h1 = x + the sum of the 8 XCD partials, in f64
+    if (lane < 16) pub_local2(&ws->h1[xcd][par][row], (float)((double)r0 + s0), (float)((double)r1 + s1), tag_of(lp, T_H1));
+    float xv[16], y[16];
+    poll_vec_regs(P, ws->h1[xcd][par], tag_of(lp, T_H1), xv);
+    store_pairs(s.h1res, xv);
+    normed(xv, g_post, y);
+    store_pairs(s.hn, y);
   };
   auto prep_down = [&](int lp) {
     poll_vec<3>(P, ws->inter[xcd][lp & 1], XI, tag_of(lp, T_INTER), s.inter);
@@ -1037,13 +1085,13 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       const int nl = layer + 1 < NL ? layer + 1 : 0;   // next layer pass (wraps to the next position)
       switch (st) {
         case S_PRO:
-          load_gain16(g_in, lw(LW, 0, W_LNIN));
-          load_gain16(g_post, lw(LW, 0, W_LNPOST));
-          load_gain16(g_fin, a.final_norm);
+          load_gain_pairs(g_in, lw(LW, 0, W_LNIN));
+          load_gain_pairs(g_post, lw(LW, 0, W_LNPOST));
+          load_gain_pairs(g_fin, a.final_norm);
           load_qk_gains(0);
           load_rope(q.pos);
           prep_input0(0);
-          load_gain16(g_in, lw(LW, NL > 1 ? 1 : 0, W_LNIN));
+          load_gain_pairs(g_in, lw(LW, NL > 1 ? 1 : 0, W_LNIN));
           break;
         case S_QKV:
           prep_att(lp, layer, q.pos, q.C);
@@ -1059,7 +1107,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           }
           if (q.local) {
             prep_gu(lp, layer);
-            load_gain16(g_post, lw(LW, nl, W_LNPOST));
+            load_gain_pairs(g_post, lw(LW, nl, W_LNPOST));
           } else {
             prep_o(lp, q.C);
           }
@@ -1067,7 +1115,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
         case S_O:
           step_barrier();   // joins the barrier after the math waves' attention merge
           prep_gu(lp, layer);
-          load_gain16(g_post, lw(LW, nl, W_LNPOST));
+          load_gain_pairs(g_post, lw(LW, nl, W_LNPOST));
           break;
         case S_GU: prep_down(lp); break;
         case S_DOWN:
@@ -1075,7 +1123,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           else if (q.head || q.last_pos) { ar2(lp); prep_final(lp); }
           else prep_input0(pi + 1);
           // g_in now serves the layer after next
-          if (layer < NL - 1 || !(q.head || q.last_pos)) load_gain16(g_in, lw(LW, (nl + 1) % NL, W_LNIN));
+          if (layer < NL - 1 || !(q.head || q.last_pos)) load_gain_pairs(g_in, lw(LW, (nl + 1) % NL, W_LNIN));
           break;
         case S_HEAD:
           if (cp_greedy) step_barrier();   // joins the math waves' head barrier
@@ -1086,7 +1134,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
               __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
               if (!q.last_pos) {
                 prep_input0(pi + 1);
-                load_gain16(g_in, lw(LW, NL > 1 ? 1 : 0, W_LNIN));
+                load_gain_pairs(g_in, lw(LW, NL > 1 ? 1 : 0, W_LNIN));
               }
             } else if (lane == 0 && a.out_token) {
               *a.out_token = tok;
