@@ -45,7 +45,11 @@ struct Workspace {
   uint64_t opart[2][NXCD][HID];
   uint64_t dpart[2][NXCD][HID];
   uint64_t logits[2][MAXV];
-  uint64_t hbest[2][2 * NWG];   // greedy code-predictor heads: per workgroup {value, tag}, {index, tag}
+  // greedy code-predictor heads, two-level candidate exchange ({value, tag, index, tag} each):
+  //   hloc: each workgroup's best, read by the 32 workgroups of its XCD
+  //   hx:   every workgroup's copy of its XCD's best, [li][xcd], read by the 8 workgroups li
+  uint64_t hloc[NXCD][2][2 * WPX];
+  uint64_t hx[2][WPX][2 * NXCD];
   uint32_t err;
   uint32_t pad[63];
 };
@@ -133,6 +137,7 @@ struct Lds {
   alignas(16) float stage[MAXC * APS > MAXV ? MAXC * APS : MAXV];
   uint32_t pen_bits[MAXV / 32];
   int tok[32];
+  const bf16_t* embp[16];   // code-predictor embedding tables, loaded once per launch
   SelScratch sel;
 };
 
@@ -506,7 +511,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) s4[j & 3] = fma((double)xv[j], (double)xv[j], s4[j & 3]);
     const double ss = group_sum<64>((s4[0] + s4[1]) + (s4[2] + s4[3]));
-    return 1.0 / sqrt(ss / (double)HID + EPSD);
+    return rsqrt_d(ss / (double)HID + EPSD);
   };
   // normalized values f32((x * rstd) * g) of the lane's 16 elements
   auto normed = [&](const float (&xv)[16], const uint32_t (&g)[8], float (&y)[16]) {
@@ -537,7 +542,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       }
     } else {
       const bf16_t* src;
-      if (a.cp_frame) src = pi == 1 ? a.bb_emb + (size_t)g0 * HID : ld_const(a.cp_embs + (pi - 2)) + (size_t)s.tok[pi - 2] * HID;
+      if (a.cp_frame) src = pi == 1 ? a.bb_emb + (size_t)g0 * HID : s.embp[pi - 2] + (size_t)s.tok[pi - 2] * HID;
       else src = a.in_emb != nullptr ? a.in_emb : a.embed_w + (size_t)a.in_tok * HID;
       const auto* p = gmem(reinterpret_cast<const uint32_t*>(src));
 #pragma unroll
@@ -616,7 +621,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     float out[3][2];
 #pragma unroll
     for (int h = 0; h < 3; ++h) {
-      const double r = 1.0 / sqrt(ss[h] / (double)HDIM + EPSD);
+      const double r = rsqrt_d(ss[h] / (double)HDIM + EPSD);
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const double n = ((double)v[2 * h + j] * r) * (h < 2 ? gq[j] : gk[j]);
@@ -941,8 +946,8 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
         int wi = s.hbi[0];
 #pragma unroll
         for (int w = 1; w < NMATH; ++w) best_merge(wv, wi, s.hbv[w], s.hbi[w]);
-        pub_cross(&ws->hbest[pi & 1][2 * wg], wv, tg);
-        pub_cross(&ws->hbest[pi & 1][2 * wg + 1], __uint_as_float((uint32_t)wi), tg);
+        const u32x4 d = {__float_as_uint(wv), tg, (uint32_t)wi, tg};
+        __builtin_amdgcn_raw_buffer_store_b128(d, P.rs, (int)ws_off(P, &ws->hloc[xcd][pi & 1][2 * li]), 0, 0);
       }
     } else if ((lane & 15) == 0 && r < nrows) {
       pub_cross(&ws->logits[pi & 1][row0 + r], (float)t, tg);
@@ -955,33 +960,19 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   // ---- poller: collect a head's logits and select a token
   auto select = [&](int pi) -> int {
     if (cp_greedy) {
-      // 256 workgroup candidates, 4 per lane, reduced in registers as they arrive
+      // Candidates {value, index} are merged by larger value, lower index on ties (an
+      // order-independent choice). Level 1: the 32 workgroup bests of this XCD (L2-local).
       const uint32_t tg = a.tag_base + TAG_HEAD + (uint32_t)pi;
-      const uint32_t o = ws_off(P, &ws->hbest[pi & 1][0]);
-      float bv = -INFINITY;
-      int bi = 0x7fffffff;
-      uint32_t pending = 0xFu, spins = 0;
-      for (;;) {
-        u32x4 v[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-          if (pending & (1u << k)) v[k] = __builtin_amdgcn_raw_buffer_load_b128(P.rs, o + 16u * (uint32_t)(lane + 64 * k), 0, 16);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          if ((pending & (1u << k)) && v[k].y == tg && v[k].w == tg) {
-            best_merge(bv, bi, __uint_as_float(v[k].x), (int)v[k].z);
-            pending &= ~(1u << k);
-          }
-        }
-        if (__ballot(pending != 0u) == 0ull) break;
-        ++spins;
-        if ((spins & 63u) == 0u && (spins > P.ec.spin_cap || err_set(P.ec))) {
-          if (lane == 0) atomicOr(P.ec.err, 1u);
-          break;
-        }
+      const int par = pi & 1;
+      float cv[2];
+      {
+        const uint32_t o = ws_off(P, &ws->hloc[xcd][par][0]);
+        poll_regs<1>(P, WPX, tg, cv, [o](int i) { return o + 16u * (uint32_t)i; });
       }
+      float bv = lane < WPX ? cv[0] : -INFINITY;
+      int bi = lane < WPX ? (int)__float_as_uint(cv[1]) : 0x7fffffff;
 #pragma unroll
-      for (int st = 0; st < 6; ++st) {
+      for (int st = 0; st < 5; ++st) {
         float ov;
         int oi;
         switch (st) {
@@ -989,12 +980,36 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           case 1: ov = xlane_f<1>(bv); oi = (int)xlane<1>((uint32_t)bi); break;
           case 2: ov = xlane_f<2>(bv); oi = (int)xlane<2>((uint32_t)bi); break;
           case 3: ov = xlane_f<3>(bv); oi = (int)xlane<3>((uint32_t)bi); break;
-          case 4: ov = xlane_f<4>(bv); oi = (int)xlane<4>((uint32_t)bi); break;
-          default: ov = xlane_f<5>(bv); oi = (int)xlane<5>((uint32_t)bi); break;
+          default: ov = xlane_f<4>(bv); oi = (int)xlane<4>((uint32_t)bi); break;
         }
         best_merge(bv, bi, ov, oi);
       }
-      return bi == 0x7fffffff ? 0 : bi;
+      // Level 2: this workgroup's copy of the XCD best goes to hx[li][xcd]; the 8 XCD bests are
+      // read from the copies of workgroup index li (each cache line has 8 readers).
+      if (lane == 0) {
+        const u32x4 d = {__float_as_uint(bv), tg, (uint32_t)bi, tg};
+        __builtin_amdgcn_raw_buffer_store_b128(d, P.rs, (int)ws_off(P, &ws->hx[par][li][2 * xcd]), 0, 16);
+      }
+      {
+        const uint32_t o = ws_off(P, &ws->hx[par][li][0]);
+        poll_regs<1>(P, NXCD, tg, cv, [o](int i) { return o + 16u * (uint32_t)i; });
+      }
+      bv = lane < NXCD ? cv[0] : -INFINITY;
+      bi = lane < NXCD ? (int)__float_as_uint(cv[1]) : 0x7fffffff;
+#pragma unroll
+      for (int st = 0; st < 3; ++st) {
+        float ov;
+        int oi;
+        switch (st) {
+          case 0: ov = xlane_f<0>(bv); oi = (int)xlane<0>((uint32_t)bi); break;
+          case 1: ov = xlane_f<1>(bv); oi = (int)xlane<1>((uint32_t)bi); break;
+          default: ov = xlane_f<2>(bv); oi = (int)xlane<2>((uint32_t)bi); break;
+        }
+        best_merge(bv, bi, ov, oi);
+      }
+      bi = __builtin_amdgcn_readfirstlane(bi);
+      // a timed-out poll leaves the error word set and may leave garbage: keep the id in range
+      return (bi >= 0 && bi < a.cp_vocab) ? bi : 0;
     }
     const int n = a.cp_frame ? a.cp_vocab : a.vocab;
     poll_vec<24>(P, ws->logits[pi & 1], n, a.tag_base + TAG_HEAD + (uint32_t)pi, s.stage);
@@ -1085,6 +1100,10 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       const int nl = layer + 1 < NL ? layer + 1 : 0;   // next layer pass (wraps to the next position)
       switch (st) {
         case S_PRO:
+          if (a.cp_frame) {
+            if (lane < a.n_groups) s.embp[lane] = a.cp_embs[lane];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          }
           load_gain_pairs(g_in, lw(LW, 0, W_LNIN));
           load_gain_pairs(g_post, lw(LW, 0, W_LNPOST));
           load_gain_pairs(g_fin, a.final_norm);
