@@ -116,7 +116,11 @@ constexpr int TRACE_STEPS = 1024;
 // register plus an immediate offset (the ds_* offset field is 16 bits); poller-only buffers
 // and the selection scratch follow.
 struct Lds {
-  double red[NMATH][2][8][64];     // attention partials [wave][head][dim % 8][lane group * 16 + dim / 8]
+  union {
+    double red[NMATH][2][8][64];   // chunked attention partials [wave][head][dim % 8][lane group * 16 + dim / 8]
+    float vst[16][HDIM];           // code-predictor local attention: V of the context positions
+  };
+  double pl[2][16];                // code-predictor local attention: p_j = exp(s_j - M) per head
   double redl[NMATH][4][2];         // their softmax sums
   double redm[2][NMATH][2];         // per (pass parity, wave, head) score max
   double wts[2][MAXC + 1];          // per head: chunk weights exp(m_c - M), then 1 / Z
@@ -836,6 +840,66 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     step_barrier();   // s.red is reused by the next attention; s.attn complete
   };
 
+  // ---- math: code-predictor attention over the whole context (L <= 16). Lane group g of math
+  // wave w takes position j = 4 w + g: its score per head (8 dims per lane, summed over the 16
+  // lanes), the workgroup maximum M, then p_j = exp(s_j - M); p and V_j go to LDS and thread
+  // (h, d) forms f32((sum_j p_j V_j[d]) * (1 / sum_j p_j)) in f64. Positions j >= L carry p = 0
+  // and V = 0 (the tile's out-of-range lanes read zeros), so the sums run over all 16 exactly.
+  auto attention_cp_local = [&](int L) {
+    const int Lold = L - 1;
+    const int d0 = 8 * (lane & 15), g = lane >> 4;
+    const int j = 4 * mw + g;
+    float kv[8], vv[8];
+    if (j == Lold) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) { kv[i] = s.knew[d0 + i]; vv[i] = s.vnew[d0 + i]; }
+    } else {
+      unpack8<BB>(tk, true, 0, kv);
+      unpack8<BB>(tk, false, 0, vv);
+    }
+    double sc[2] = {0.0, 0.0};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      sc[0] = fma((double)s.q[0][d0 + i], (double)kv[i], sc[0]);
+      sc[1] = fma((double)s.q[1][d0 + i], (double)kv[i], sc[1]);
+    }
+    group_sum_n<16>(sc);
+    double mx[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      sc[h] = j < L ? (double)(float)(sc[h] * (double)a.scale) : -INFINITY;
+      double u = xlane_d<4>(sc[h]);
+      mx[h] = u > sc[h] ? u : sc[h];
+      u = xlane_d<5>(mx[h]);
+      mx[h] = u > mx[h] ? u : mx[h];
+    }
+    if (lane == 0) { s.redm[0][mw][0] = mx[0]; s.redm[0][mw][1] = mx[1]; }
+    step_barrier();
+    double p[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      double M = s.redm[0][0][h];
+#pragma unroll
+      for (int w = 1; w < NMATH; ++w) M = s.redm[0][w][h] > M ? s.redm[0][w][h] : M;
+      p[h] = j < L ? exp(sc[h] - M) : 0.0;
+    }
+    if ((lane & 15) == 0) { s.pl[0][j] = p[0]; s.pl[1][j] = p[1]; }
+    *reinterpret_cast<float4*>(&s.vst[j][d0]) = make_float4(vv[0], vv[1], vv[2], vv[3]);
+    *reinterpret_cast<float4*>(&s.vst[j][d0 + 4]) = make_float4(vv[4], vv[5], vv[6], vv[7]);
+    step_barrier();
+    const int t = threadIdx.x;   // 0..255: head t >> 7, dim t & 127
+    const int h = t >> 7, d = t & 127;
+    double A = 0.0, Z = 0.0;
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) {
+      const double pj = s.pl[h][jj];
+      Z += pj;
+      A = fma(pj, (double)s.vst[jj][d], A);
+    }
+    s.attn[t] = (float)(A * (1.0 / Z));
+    step_barrier();   // s.attn complete; vst / pl are reused by the next attention
+  };
+
   // ---- math: GEMV stages (f64 accumulation, f32 results)
   auto load_x16 = [&](const float* x, double* xv) {
 #pragma unroll
@@ -1181,7 +1245,12 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           if (q.local) load_o<BB>(to, LW, layer, xcd, li, mw, lane);
           break;
         case S_ATT:
-          if (q.has_chunk) attention(lp, layer, q.L, q.c0, q.c1, q.local);
+          if constexpr (!BB) {
+            if (q.local) attention_cp_local(q.L);
+            else if (q.has_chunk) attention(lp, layer, q.L, q.c0, q.c1, false);
+          } else if (q.has_chunk) {
+            attention(lp, layer, q.L, q.c0, q.c1, q.local);
+          }
           if (q.local) {
             math_o(lp, true);
             load_gu<BB>(tgu, LW, layer, xcd, li, mw, lane);
