@@ -331,22 +331,25 @@ __device__ bool poll_regs(const Poll& P, int npair, uint32_t tag, float (&out)[2
     return false;
   };
   if constexpr (MAXP <= 8) {
-    // Two batches in flight: the next batch is issued before the previous one is checked, so a
-    // slot is seen about half a load latency after it lands instead of a whole one. Every
-    // batch has the same loads (lanes without a slot re-read slot 0), so the wait for the
-    // older batch is an exact vmcnt.
-    u32x4 va[MAXP], vb[MAXP];
+    // NBAT batches in flight: the next batch is issued before the oldest one is checked, so a
+    // slot is seen about 1 / NBAT of a load latency after it lands instead of a whole one.
+    // Every batch has the same loads (lanes without a slot re-read slot 0), so the wait for
+    // the oldest batch is an exact vmcnt.
+    constexpr int NBAT = MAXP <= 2 ? 4 : (MAXP <= 4 ? 3 : 2);
+    u32x4 vb[NBAT][MAXP];
     auto issue = [&](u32x4 (&v)[MAXP]) {
 #pragma unroll
       for (int k = 0; k < MAXP; ++k)
         v[k] = __builtin_amdgcn_raw_buffer_load_b128(P.rs, off((valid >> k) & 1u ? lane + 64 * k : 0), 0, 16);
     };
-    issue(va);
+#pragma unroll
+    for (int b = 0; b < NBAT - 1; ++b) issue(vb[b]);
     for (;;) {
-      issue(vb);
-      if (check(va)) return true;
-      issue(va);
-      if (check(vb)) return true;
+#pragma unroll
+      for (int b = 0; b < NBAT; ++b) {
+        issue(vb[(b + NBAT - 1) % NBAT]);
+        if (check(vb[b])) return true;
+      }
       if (timed_out()) return false;
     }
   } else {
