@@ -29,7 +29,8 @@ constexpr int NTHR = 64 * (NMATH + 1);  // + 1 poller wave
 constexpr int LROWS = 512;        // q(256) + k(128) + v(128) rows owned by one XCD
 constexpr int XI = INTER / NXCD;  // 384 intermediate rows per XCD
 constexpr int MAXC = 8;           // max attention chunks per KV head
-constexpr int APS = 260;          // attention partial: 2 heads x (m, l, acc[128])
+constexpr int APH = 130;          // attention partial of one (chunk, head): acc[128], m, l
+constexpr int APS = 2 * APH;      // partial storage per chunk (both heads)
 constexpr int SUBP = 64;          // positions per prefetched attention sub-block
 constexpr int MAXV = 3072;        // max vocabulary of a selection head
 

@@ -666,12 +666,12 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     const int h = lane >> 5, c = lane & 31;
     float M = -INFINITY;
-    for (int j = 0; j < C; ++j) M = fmaxf(M, s.attp[j * APS + 256 + 2 * h]);
-    if (c < MAXC) s.wts[h][c] = c < C ? exp((double)s.attp[c * APS + 256 + 2 * h] - (double)M) : 0.0;
+    for (int j = 0; j < C; ++j) M = fmaxf(M, s.attp[(2 * j + h) * APH + 128]);
+    if (c < MAXC) s.wts[h][c] = c < C ? exp((double)s.attp[(2 * c + h) * APH + 128] - (double)M) : 0.0;
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     if (c == 0) {
       double Z = 0.0;
-      for (int j = 0; j < C; ++j) Z += (double)s.attp[j * APS + 257 + 2 * h] * s.wts[h][j];
+      for (int j = 0; j < C; ++j) Z += (double)s.attp[(2 * j + h) * APH + 129] * s.wts[h][j];
       s.wts[h][MAXC] = 1.0 / Z;
     }
   };
@@ -698,34 +698,39 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     poll_vec<3>(P, ws->inter[xcd][lp & 1], XI, tag_of(lp, T_INTER), s.inter);
   };
 
-  // ---- math: attention over this workgroup's chunk [c0, c1) at KV length L
-  // Both query heads of the XCD share the KV head, so one pass over the K/V tile serves both.
-  // Lane group g (16 lanes x 8 dims) scores positions b0 + 4 JJ mw + 4 jj + g (jj < JJ); each
-  // wave keeps one running max per head (shared by its 4 lane groups), so lane-group partials
-  // are plain sums: they go to LDS unscaled, and the final merge weighs the 4 waves by
-  // exp(m_w - M). Every exp is branch-free (a masked argument becomes -1000, whose exp is 0).
-  auto attention = [&](int lp, int layer, int L, int c0, int c1, bool local) {
+  // ---- math: attention over this workgroup's chunk [c0, c1) at KV length L, for NH query
+  // heads: both heads of the XCD's KV head (NH = 2, one pass over the K/V tile serves both),
+  // or head hh alone (NH = 1: the chunked split gives each (chunk, head) its own workgroup).
+  // Lane group g (16 lanes x 8 dims) scores positions b0 + 4 JJ mw + 4 jj + g (jj < JJ); the
+  // workgroup shares one running max per head, so lane-group partials are plain sums: they go
+  // to LDS unscaled and thread (head, dim) adds them. Every exp is branch-free (a masked
+  // argument becomes -1000, whose exp is 0).
+  auto attention = [&](auto nh_c, int lp, int layer, int L, int c0, int c1, bool local, int hh) {
+    constexpr int NH = decltype(nh_c)::value;
     constexpr int JJ = KVGeo<BB>::JJ, SUB = KVGeo<BB>::SUB;
     constexpr double NEG = -1000.0;
     const int Lold = L - 1;
     const int d0 = 8 * (lane & 15), g = lane >> 4;
     const double scale = (double)a.scale;
     const int nsb = (c1 - c0 + SUB - 1) / SUB;
-    double qv[2][8];
+    const int hq0 = NH == 2 ? 0 : hh;   // first query head of this workgroup
+    double qv[NH][8];
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < NH; ++h)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) qv[h][i] = s.q[h][d0 + i];
-    double m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0, 0.0};
-    double acc[2][8];
+      for (int i = 0; i < 8; ++i) qv[h][i] = s.q[hq0 + h][d0 + i];
+    double m[NH], l[NH], acc[NH][8];
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < NH; ++h) {
+      m[h] = -INFINITY;
+      l[h] = 0.0;
 #pragma unroll
       for (int i = 0; i < 8; ++i) acc[h][i] = 0.0;
+    }
     for (int sb = 0; sb < nsb; ++sb) {
       const int b0 = c0 + sb * SUB;
       if (sb > 0) load_kv<BB>(tk, a, layer, xcd, b0, c1 < Lold ? c1 : Lold, mw, lane);
-      double sc[2 * JJ];
+      double sc[NH * JJ];
 #pragma unroll
       for (int jj = 0; jj < JJ; ++jj) {
         const int pos = b0 + 4 * JJ * mw + 4 * jj + g;
@@ -736,17 +741,19 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
         } else {
           unpack8<BB>(tk, true, jj, kv);
         }
-        double d_0 = 0.0, d_1 = 0.0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) { d_0 = fma(qv[0][i], (double)kv[i], d_0); d_1 = fma(qv[1][i], (double)kv[i], d_1); }
-        sc[jj] = d_0;
-        sc[JJ + jj] = d_1;
+        for (int h = 0; h < NH; ++h) {
+          double dd = 0.0;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) dd = fma(qv[h][i], (double)kv[i], dd);
+          sc[h * JJ + jj] = dd;
+        }
       }
       group_sum_n<16>(sc);
       // f32-rounded scores; masked positions -inf; wave-wide max per head
-      double mx[2];
+      double mx[NH];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < NH; ++h) {
         double mloc = -INFINITY;
 #pragma unroll
         for (int jj = 0; jj < JJ; ++jj) {
@@ -755,37 +762,38 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           sc[h * JJ + jj] = v;
           mloc = v > mloc ? v : mloc;
         }
-        mx[h] = mloc;
-      }
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        double u = xlane_d<4>(mx[h]);
-        mx[h] = u > mx[h] ? u : mx[h];
-        u = xlane_d<5>(mx[h]);
-        mx[h] = u > mx[h] ? u : mx[h];
+        double u = xlane_d<4>(mloc);
+        mloc = u > mloc ? u : mloc;
+        u = xlane_d<5>(mloc);
+        mx[h] = u > mloc ? u : mloc;
       }
       // workgroup-wide maximum of this pass (slots double-buffered by pass parity): every
       // wave and lane group then shares one running max, so their partial sums add plainly
-      if (lane == 0) { s.redm[sb & 1][mw][0] = mx[0]; s.redm[sb & 1][mw][1] = mx[1]; }
-      step_barrier();
-      double mn[2], alpha[2];
+      if (lane == 0) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < NH; ++h) s.redm[sb & 1][mw][h] = mx[h];
+      }
+      step_barrier();
+      double mn[NH];
+#pragma unroll
+      for (int h = 0; h < NH; ++h) {
         double M = m[h];
 #pragma unroll
         for (int w = 0; w < NMATH; ++w) M = s.redm[sb & 1][w][h] > M ? s.redm[sb & 1][w][h] : M;
         mn[h] = M;
-        alpha[h] = sb == 0 ? 0.0 : exp(m[h] == -INFINITY ? NEG : m[h] - mn[h]);
       }
-      double pr[2 * JJ];
+      if (sb > 0) {
 #pragma unroll
-      for (int k = 0; k < 2 * JJ; ++k) pr[k] = exp(sc[k] == -INFINITY ? NEG : sc[k] - mn[k / JJ]);
+        for (int h = 0; h < NH; ++h) {
+          const double alpha = exp(m[h] == -INFINITY ? NEG : m[h] - mn[h]);
+          l[h] *= alpha;
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        l[h] *= alpha[h];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[h][i] *= alpha[h];
+          for (int i = 0; i < 8; ++i) acc[h][i] *= alpha;
+        }
       }
+      double pr[NH * JJ];
+#pragma unroll
+      for (int k = 0; k < NH * JJ; ++k) pr[k] = exp(sc[k] == -INFINITY ? NEG : sc[k] - mn[k / JJ]);
 #pragma unroll
       for (int jj = 0; jj < JJ; ++jj) {
         const int pos = b0 + 4 * JJ * mw + 4 * jj + g;
@@ -797,24 +805,21 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           unpack8<BB>(tk, false, jj, vv);
         }
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < NH; ++h) {
           l[h] += pr[h * JJ + jj];
 #pragma unroll
           for (int i = 0; i < 8; ++i) acc[h][i] = fma(pr[h * JJ + jj], (double)vv[i], acc[h][i]);
         }
       }
-      m[0] = mn[0];
-      m[1] = mn[1];
-    }
-    // lane-major layout: each store of the wave writes 64 consecutive doubles (no bank conflicts)
-    // the wave's softmax sums (its 4 lane groups), one value per head
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < NH; ++h) m[h] = mn[h];
+    }
+    // the wave's softmax sums (its 4 lane groups), one value per head; partials lane-major (each
+    // store of the wave writes 64 consecutive doubles: no bank conflicts)
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
       l[h] += xlane_d<4>(l[h]);
       l[h] += xlane_d<5>(l[h]);
-    }
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) s.red[mw][h][i][lane] = acc[h][i];
       if (lane == 0) s.redl[mw][0][h] = l[h];
@@ -823,22 +828,23 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     // thread t merges dim d = 8 j + i of head h, reading row i at columns 16 g + j (contiguous in j)
     const int t = threadIdx.x;  // 0..255
     const int h = t >> 7, ii = (t >> 4) & 7, jj0 = t & 15, d = 8 * jj0 + ii;
-    double A = 0.0, Lsum = 0.0;
+    if (h < NH) {
+      double A = 0.0, Lsum = 0.0;
 #pragma unroll
-    for (int w = 0; w < NMATH; ++w) {
-      A += (s.red[w][h][ii][jj0] + s.red[w][h][ii][16 + jj0]) + (s.red[w][h][ii][32 + jj0] + s.red[w][h][ii][48 + jj0]);
-      Lsum += s.redl[w][0][h];
-    }
-    const double Mw = h ? m[1] : m[0];
-    if (local) {
-      // the whole context in this workgroup: f32(A * (1 / l)), no partial exchange
-      s.attn[128 * h + d] = (float)(A * (1.0 / Lsum));
-    } else {
-      const int c = li;
-      uint64_t* dst = &ws->attp[xcd][lp & 1][c * APS];
-      const uint32_t tg = tag_of(lp, T_ATT);
-      pub_local(dst + 128 * h + d, (float)A, tg);
-      if (d == 0) { pub_local(dst + 256 + 2 * h, (float)Mw, tg); pub_local(dst + 257 + 2 * h, (float)Lsum, tg); }
+      for (int w = 0; w < NMATH; ++w) {
+        A += (s.red[w][h][ii][jj0] + s.red[w][h][ii][16 + jj0]) + (s.red[w][h][ii][32 + jj0] + s.red[w][h][ii][48 + jj0]);
+        Lsum += s.redl[w][0][h];
+      }
+      if (local) {
+        // the whole context in this workgroup: f32(A * (1 / l)), no partial exchange
+        s.attn[128 * (hq0 + h) + d] = (float)(A * (1.0 / Lsum));
+      } else {
+        // partial of (chunk li >> 1, head hh): acc[128], m, l
+        uint64_t* dst = &ws->attp[xcd][lp & 1][li * APH];
+        const uint32_t tg = tag_of(lp, T_ATT);
+        pub_local(dst + d, (float)A, tg);
+        if (d == 0) { pub_local(dst + 128, (float)m[0], tg); pub_local(dst + 129, (float)Lsum, tg); }
+      }
     }
     step_barrier();   // s.red is reused by the next attention; s.attn complete
   };
@@ -925,7 +931,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       const int t = threadIdx.x, hh = t >> 7;
       float pv[MAXC];
 #pragma unroll
-      for (int c = 0; c < MAXC; ++c) pv[c] = s.attp[c * APS + t];
+      for (int c = 0; c < MAXC; ++c) pv[c] = s.attp[(2 * c + hh) * APH + (t & 127)];
       double acc = 0.0;
 #pragma unroll
       for (int c = 0; c < MAXC; ++c) acc = fma((double)pv[c], s.wts[hh][c], acc);
@@ -1149,9 +1155,10 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     q.L = q.pos + 1;
     chunking<BB>(q.L, q.C, q.P);
     q.local = att_local(pi);
-    q.has_chunk = q.local || li < q.C;
-    q.c0 = q.local ? 0 : li * q.P;
-    q.c1 = q.local ? q.L : min(q.L, (li + 1) * q.P);
+    // chunked: workgroup li takes chunk li >> 1 for query head li & 1 of the XCD
+    q.has_chunk = q.local || li < 2 * q.C;
+    q.c0 = q.local ? 0 : (li >> 1) * q.P;
+    q.c1 = q.local ? q.L : min(q.L, ((li >> 1) + 1) * q.P);
     q.last_pos = pi == a.n_pos - 1;
     q.head = has_head(pi);
     return q;
@@ -1250,9 +1257,10 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
         case S_ATT:
           if constexpr (!BB) {
             if (q.local) attention_cp_local(q.L);
-            else if (q.has_chunk) attention(lp, layer, q.L, q.c0, q.c1, false);
+            else if (q.has_chunk) attention(std::integral_constant<int, 1>{}, lp, layer, q.L, q.c0, q.c1, false, li & 1);
           } else if (q.has_chunk) {
-            attention(lp, layer, q.L, q.c0, q.c1, q.local);
+            if (q.local) attention(std::integral_constant<int, 2>{}, lp, layer, q.L, q.c0, q.c1, true, 0);
+            else attention(std::integral_constant<int, 1>{}, lp, layer, q.L, q.c0, q.c1, false, li & 1);
           }
           if (q.local) {
             math_o(lp, true);
