@@ -97,6 +97,33 @@ def test_backbone_long_context_2048(full, pkg):
     assert e < TOL
 
 
+@pytest.mark.parametrize("L", [65, 577, 4096])
+def test_backbone_context_edges(full, pkg, L):
+    """Attended lengths at the edges of the attention paths: just past the one-pass local path (65:
+    2 chunks of 33), a ragged chunk split (577: 8 chunks of 73, a full and a 9-position sub-block),
+    and the maximum context (4096 = max_seq_len: 8 chunks of 512, 8 sub-blocks each)."""
+    sd, dsd, tw = full
+    n = 2
+    orc = DecoderOracle(tw.bb_layers[:n], tw.bb_norm, L, "backbone", "kernel")
+    sd2 = {k: v for k, v in dsd.items() if not k.startswith("talker.model.layers.") or int(k.split(".")[3]) < n}
+    bb = pkg.TTSMegakernelGenerator(model=sd2, max_seq_len=L)
+    k, v = _rand_kv(n, L - 1, 40 + L, torch.bfloat16)
+    bb.set_kv_cache(k.cuda(), v.cuda())
+    bb.set_position(L - 1)
+    orc.set_kv(k, v)
+    x = torch.randn(1024, generator=torch.Generator().manual_seed(L)).to(torch.bfloat16)
+    _print(f"2-layer backbone L={L}: launching")
+    h = bb.decode_step_with_embedding(x.cuda())
+    hr, _ = orc.step(x, pos=L - 1)
+    e = rel_l2(h.cpu(), hr)
+    _print(f"2-layer backbone L={L}: hidden rel_l2 {e:.2e}")
+    bb.check_error()
+    assert e < TOL
+    # the new entry landed at the last cache slot
+    kc = bb.get_k_cache()[:, :, L - 1].float().cpu()
+    assert rel_l2(kc, orc.k[:, :, L - 1].float()) < TOL
+
+
 def test_backbone_mrope_distinct_positions(full, pkg):
     sd, dsd, tw = full
     n = 2
