@@ -138,6 +138,7 @@ struct Lds {
   // poller-only from here
   alignas(16) float xres[HID];
   alignas(16) float h1res[HID];
+  alignas(16) float comb[HID];   // code-predictor frame (workgroup 0): running embedding combine
   alignas(16) float stage[MAXC * APS > MAXV ? MAXC * APS : MAXV];
   uint32_t pen_bits[MAXV / 32];
   int tok[32];
@@ -559,6 +560,18 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     float y[16];
     normed(xv, g_in, y);
     store_pairs(s.xn, y);
+  };
+
+  // ---- poller (code-predictor frame, workgroup 0): the embedding combine, accumulated as each
+  // position's input row arrives in xres (bf16 rounding after each add, in the order
+  // emb_bb[g0] + emb_0[t_0] + emb_1[t_1] + ...; generator.py:356-362)
+  auto comb_add = [&](bool first) {
+    for (int k = 0; k < 8; ++k) {
+      const int e = 2 * (lane + 64 * k);
+      const float2 x = *reinterpret_cast<const float2*>(&s.xres[e]);
+      const float2 c = *reinterpret_cast<const float2*>(&s.comb[e]);
+      *reinterpret_cast<float2*>(&s.comb[e]) = first ? x : make_float2(rbf(c.x + x.x), rbf(c.y + x.y));
+    }
   };
 
   // ---- poller: AR2 of layer pass lp (down partials + residual) -> xl slots
@@ -1214,7 +1227,10 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
         case S_DOWN:
           if (layer < NL - 1) { ar2(lp); prep_input_next(lp); }
           else if (q.head || q.last_pos) { ar2(lp); prep_final(lp); }
-          else prep_input0(pi + 1);
+          else {
+            prep_input0(pi + 1);
+            if (a.cp_frame && wg == 0) comb_add(pi == 0);
+          }
           // g_in now serves the layer after next
           if (layer < NL - 1 || !(q.head || q.last_pos)) load_gain_pairs(g_in, lw(LW, (nl + 1) % NL, W_LNIN));
           break;
@@ -1227,6 +1243,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
               __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
               if (!q.last_pos) {
                 prep_input0(pi + 1);
+                if (wg == 0) comb_add(false);
                 load_gain_pairs(g_in, lw(LW, NL > 1 ? 1 : 0, W_LNIN));
               }
             } else if (lane == 0 && a.out_token) {
@@ -1307,11 +1324,24 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       a.out_tokens[0] = g0;
       for (int g = 0; g < a.n_groups; ++g) a.out_tokens[1 + g] = s.tok[g];
     }
-    for (int d = lane; d < HID; d += 64) {
-      float acc = ldbf(a.bb_emb + (size_t)g0 * HID + d);
-      for (int g = 0; g < a.n_groups; ++g) acc = rbf(acc + ldbf(ld_const(a.cp_embs + g) + (size_t)s.tok[g] * HID + d));
-      if (a.text_row) acc = rbf(acc + ldbf(a.text_row + d));
-      a.out_combined[d] = f2bf(acc);
+    // s.comb holds emb_bb[g0] + emb_0[t_0] + ... + emb_{n-2}[t_{n-2}] (each row was loaded as a
+    // position's input); the last group's row and the text row complete it (generator.py:356-362)
+    const int gl = a.n_groups - 1;
+    const auto* lr = gmem(reinterpret_cast<const uint32_t*>(s.embp[gl] + (size_t)s.tok[gl] * HID));
+    uint32_t wl[8], wt[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) wl[k] = lr[lane + 64 * k];
+    if (a.text_row) {
+      const auto* tr = gmem(reinterpret_cast<const uint32_t*>(a.text_row));
+#pragma unroll
+      for (int k = 0; k < 8; ++k) wt[k] = tr[lane + 64 * k];
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int e = 2 * (lane + 64 * k);
+      float a0 = rbf(s.comb[e] + bflo(wl[k])), a1 = rbf(s.comb[e + 1] + bfhi(wl[k]));
+      if (a.text_row) { a0 = rbf(a0 + bflo(wt[k])); a1 = rbf(a1 + bfhi(wt[k])); }
+      gput(reinterpret_cast<uint32_t*>(a.out_combined) + (e >> 1), (uint32_t)f2bf(a0) | ((uint32_t)f2bf(a1) << 16));
     }
   }
 }
