@@ -331,7 +331,7 @@ __device__ bool poll_regs(const Poll& P, int npair, uint32_t tag, float (&out)[2
     }
     return false;
   };
-  if constexpr (MAXP <= 8) {
+  if constexpr (MAXP <= 17) {
     // NBAT batches in flight: the next batch is issued before the oldest one is checked, so a
     // slot is seen about 1 / NBAT of a load latency after it lands instead of a whole one.
     // Every batch has the same loads (lanes without a slot re-read slot 0), so the wait for
