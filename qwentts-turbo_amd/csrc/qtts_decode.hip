@@ -677,16 +677,23 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     const int par = lp & 1;
     poll_vec<17>(P, ws->attp[xcd][par], C * APS, tag_of(lp, T_ATT), s.attp);
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    // lane (h, c): head h = lane >> 5, chunk c = lane & 31 (c < MAXC); the max and the sum run
+    // over the 8 chunk lanes with three exchanges
     const int h = lane >> 5, c = lane & 31;
-    float M = -INFINITY;
-    for (int j = 0; j < C; ++j) M = fmaxf(M, s.attp[(2 * j + h) * APH + 128]);
-    if (c < MAXC) s.wts[h][c] = c < C ? exp((double)s.attp[(2 * c + h) * APH + 128] - (double)M) : 0.0;
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    if (c == 0) {
-      double Z = 0.0;
-      for (int j = 0; j < C; ++j) Z += (double)s.attp[(2 * j + h) * APH + 129] * s.wts[h][j];
-      s.wts[h][MAXC] = 1.0 / Z;
-    }
+    const bool ok = c < C;
+    const float mc = ok ? s.attp[(2 * c + h) * APH + 128] : -INFINITY;
+    const float lc = ok ? s.attp[(2 * c + h) * APH + 129] : 0.0f;
+    float M = mc;
+    M = fmaxf(M, xlane_f<0>(M));
+    M = fmaxf(M, xlane_f<1>(M));
+    M = fmaxf(M, xlane_f<2>(M));
+    const double w = ok ? exp((double)mc - (double)M) : 0.0;
+    double Z = (double)lc * w;
+    Z += xlane_d<0>(Z);
+    Z += xlane_d<1>(Z);
+    Z += xlane_d<2>(Z);
+    if (c < MAXC) s.wts[h][c] = w;
+    if (c == 0) s.wts[h][MAXC] = 1.0 / Z;
   };
   // ---- poller: AR1 (O partials + residual) -> h1 slots; then h1 -> h1res, hn
   auto prep_gu = [&](int lp, int layer) {
