@@ -522,10 +522,15 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     return rsqrt_d(ss / (double)HID + EPSD);
   };
   // normalized values f32((x * rstd) * g) of the lane's 16 elements
-  auto normed = [&](const float (&xv)[16], const uint32_t (&g)[8], float (&y)[16]) {
+  // f64 copy of a gain slice, made before the step's poll (off the critical path)
+  auto gains_d = [&](const uint32_t (&g)[8], double (&gd)[16]) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) { gd[2 * k] = bflo(g[k]); gd[2 * k + 1] = bfhi(g[k]); }
+  };
+  auto normed = [&](const float (&xv)[16], const double (&gd)[16], float (&y)[16]) {
     const double r = rstd_of(xv);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) y[j] = (float)(((double)xv[j] * r) * (double)((j & 1) ? bfhi(g[j >> 1]) : bflo(g[j >> 1])));
+    for (int j = 0; j < 16; ++j) y[j] = (float)(((double)xv[j] * r) * gd[j]);
   };
   auto store_pairs = [&](float* dst, const float (&v)[16]) {
 #pragma unroll
@@ -539,6 +544,8 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
 
   // ---- poller: input of layer 0 of position pi (embedding source) -> xres, xn
   auto prep_input0 = [&](int pi) {
+    double gd[16];
+    gains_d(g_in, gd);
     float xv[16];
     if (a.cp_frame && pi == 0) {
       const auto* p = gmem(reinterpret_cast<const u32x2*>(a.bb_hidden));
@@ -558,7 +565,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     }
     store_pairs(s.xres, xv);
     float y[16];
-    normed(xv, g_in, y);
+    normed(xv, gd, y);
     store_pairs(s.xn, y);
   };
 
@@ -591,17 +598,21 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   // ---- poller: next layer input (after ar2 of lp) -> xres, xn
   auto prep_input_next = [&](int lp) {
     float xv[16], y[16];
+    double gd[16];
+    gains_d(g_in, gd);
     poll_vec_regs(P, ws->xl[xcd][lp & 1], tag_of(lp, T_XL), xv);
     store_pairs(s.xres, xv);
-    normed(xv, g_in, y);
+    normed(xv, gd, y);
     store_pairs(s.xn, y);
   };
   // ---- poller: final norm (after ar2 of lp) -> hb (bf16-rounded), outputs
   auto prep_final = [&](int lp) {
     float xv[16], y[16];
+    double gd[16];
+    gains_d(g_fin, gd);
     poll_vec_regs(P, ws->xl[xcd][lp & 1], tag_of(lp, T_XL), xv);
     store_pairs(s.xres, xv);
-    normed(xv, g_fin, y);
+    normed(xv, gd, y);
     if (wg == 0) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
@@ -709,9 +720,11 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     // h1 = x + the sum of the 8 XCD partials, in f64
     if (lane < 16) pub_local2(&ws->h1[xcd][par][row], (float)((double)r0 + s0), (float)((double)r1 + s1), tag_of(lp, T_H1));
     float xv[16], y[16];
+    double gd[16];
+    gains_d(g_post, gd);
     poll_vec_regs(P, ws->h1[xcd][par], tag_of(lp, T_H1), xv);
     store_pairs(s.h1res, xv);
-    normed(xv, g_post, y);
+    normed(xv, gd, y);
     store_pairs(s.hn, y);
   };
   auto prep_down = [&](int lp) {
