@@ -98,6 +98,14 @@ __device__ __forceinline__ double rsqrt_d(double x) {
   y = fma(y, fma(-(h * y), y, 0.5), y);
   return y;
 }
+// 1 / x for normal x > 0 in f64: the hardware estimate refined by two Newton steps
+// y += y (1 - x y); within a few ulps of the correctly rounded 1.0 / x.
+__device__ __forceinline__ double rcp_d(double x) {
+  double y = __builtin_amdgcn_rcp(x);
+  y = fma(y, fma(-x, y, 1.0), y);
+  y = fma(y, fma(-x, y, 1.0), y);
+  return y;
+}
 // store through the global address space (a global_store, not a flat one)
 template <class T>
 __device__ __forceinline__ void gput(T* p, T v) {

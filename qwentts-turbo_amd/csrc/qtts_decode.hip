@@ -931,14 +931,16 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     step_barrier();
     const int t = threadIdx.x;   // 0..255: head t >> 7, dim t & 127
     const int h = t >> 7, d = t & 127;
-    double A = 0.0, Z = 0.0;
+    // four independent chains (positions jj = 4 i + c), combined at the end
+    double A4[4] = {0.0, 0.0, 0.0, 0.0}, Z4[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
     for (int jj = 0; jj < 16; ++jj) {
       const double pj = s.pl[h][jj];
-      Z += pj;
-      A = fma(pj, (double)s.vst[jj][d], A);
+      Z4[jj & 3] += pj;
+      A4[jj & 3] = fma(pj, (double)s.vst[jj][d], A4[jj & 3]);
     }
-    s.attn[t] = (float)(A * (1.0 / Z));
+    const double A = (A4[0] + A4[1]) + (A4[2] + A4[3]), Z = (Z4[0] + Z4[1]) + (Z4[2] + Z4[3]);
+    s.attn[t] = (float)(A * rcp_d(Z));
     step_barrier();   // s.attn complete; vst / pl are reused by the next attention
   };
 
