@@ -489,28 +489,29 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
 
   // ---- poller registers: small per-layer vectors, loaded a step (or a layer) before use so
   // that no dependent global load sits on the critical path of a step. The poller lane owns
-  // hidden elements 2 (lane + 64 k) + {0, 1} (k < 8) and head channels c0 = 2 lane, c0 + 1.
+  // hidden elements 2 (lane + 64 k) + {0, 1} (k < 8) and head channels lane, lane + 64 (the
+  // rotate_half partners).
   //   g_in / g_post / g_fin: RMSNorm gains of the lane's 16 elements (8 packed bf16 pairs)
-  //   qn2 / kn2: q/k-norm gains of channels c0, c0 + 1 (packed); rc / rs: their cos / sin
+  //   qn / kn: q/k-norm gains of head channels lane, lane + 64; rc / rsn: their cos / sin
   uint32_t g_in[8], g_post[8], g_fin[8];
-  uint32_t qn2, kn2;
-  float rc[2], rsn[2];
+  float qn[2], kn[2], rc[2], rsn[2];
   auto load_gain_pairs = [&](uint32_t (&g)[8], const bf16_t* src) {
     const auto* p = gmem(reinterpret_cast<const uint32_t*>(src));
 #pragma unroll
     for (int k = 0; k < 8; ++k) g[k] = p[lane + 64 * k];
   };
   auto load_qk_gains = [&](int layer) {
-    qn2 = *gmem(reinterpret_cast<const uint32_t*>(lw(LW, layer, W_QN)) + lane);
-    kn2 = *gmem(reinterpret_cast<const uint32_t*>(lw(LW, layer, W_KN)) + lane);
+    const bf16_t* q = lw(LW, layer, W_QN);
+    const bf16_t* k = lw(LW, layer, W_KN);
+    qn[0] = ldbf(q + lane); qn[1] = ldbf(q + lane + 64);
+    kn[0] = ldbf(k + lane); kn[1] = ldbf(k + lane + 64);
   };
   auto load_rope = [&](int pos) {
+    const size_t row = (size_t)rot_row(lane, pos) * HDIM;   // channel lane + 64 shares the row
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int c = 2 * lane + j;
-      const size_t row = (size_t)rot_row(c & 63, pos) * HDIM;
-      rc[j] = ldbf(a.cos_t + row + c);
-      rsn[j] = ldbf(a.sin_t + row + c);
+      rc[j] = ldbf(a.cos_t + row + lane + 64 * j);
+      rsn[j] = ldbf(a.sin_t + row + lane + 64 * j);
     }
   };
   // RMSNorm statistic of the lane-distributed 1024-vector: 1 / sqrt(mean(x^2) + eps) in f64
@@ -632,14 +633,13 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     store_pairs(s.hb, y);
   };
   // ---- poller: q/k norm, RoPE, KV write for layer `layer` at position pos
-  // The lane holds channels c0 = 2 lane, c0 + 1 of q head 0, q head 1, k and v. rotate_half pairs
-  // channel c with c + 64, which sits in lane ^ 32.
+  // The lane holds channels c = lane and c + 64 (the rotate_half partners) of q head 0, q head 1,
+  // k and v (the QKV slot order pairs them).
   bool kv_pending = false;
   auto prep_att = [&](int lp, int layer, int pos, int C) {
     const int par = lp & 1;
-    const double gq[2] = {bflo(qn2), bfhi(qn2)}, gk[2] = {bflo(kn2), bfhi(kn2)};
-    const double cs[2] = {rc[0], rc[1]}, sn[2] = {rsn[0], rsn[1]};
-    float v[8];   // [head][j]: head 0, 1 = q, 2 = k, 3 = v
+    const double cl = rc[0], ch = rc[1], sl = rsn[0], sh = rsn[1];
+    float v[8];   // [head][j]: head 0, 1 = q, 2 = k, 3 = v; j = 0: channel c, 1: channel c + 64
     {
       const uint32_t o = ws_off(P, ws->qkv[xcd][par]);
       poll_regs<4>(P, LROWS / 2, tag_of(lp, T_QKV), v, [o](int i) { return o + 16u * (uint32_t)i; });
@@ -648,33 +648,34 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
 #pragma unroll
     for (int h = 0; h < 3; ++h) ss[h] = fma((double)v[2 * h], (double)v[2 * h], (double)v[2 * h + 1] * (double)v[2 * h + 1]);
     group_sum_n<64, 3>(ss);
-    const bool lo = lane < 32;   // channels < 64
-    float out[3][2];
+    float outl[3], outh[3];
 #pragma unroll
     for (int h = 0; h < 3; ++h) {
       const double r = rsqrt_d(ss[h] / (double)HDIM + EPSD);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const double n = ((double)v[2 * h + j] * r) * (h < 2 ? gq[j] : gk[j]);
-        const double pn = xlane_d<5>(n);   // channel c +- 64
-        out[h][j] = lo ? (float)(n * cs[j] - pn * sn[j]) : (float)(pn * sn[j] + n * cs[j]);
-      }
+      const double gl = h < 2 ? qn[0] : kn[0], gh = h < 2 ? qn[1] : kn[1];
+      const double nl = ((double)v[2 * h] * r) * gl, nh = ((double)v[2 * h + 1] * r) * gh;
+      outl[h] = (float)(nl * cl - nh * sl);
+      outh[h] = (float)(nl * sh + nh * ch);
     }
-    const int c0 = 2 * lane;
-    *reinterpret_cast<float2*>(&s.q[0][c0]) = make_float2(out[0][0], out[0][1]);
-    *reinterpret_cast<float2*>(&s.q[1][c0]) = make_float2(out[1][0], out[1][1]);
-    float k0 = out[2][0], k1 = out[2][1], v0 = v[6], v1 = v[7];
-    if constexpr (BB) { k0 = rbf(k0); k1 = rbf(k1); v0 = rbf(v0); v1 = rbf(v1); }
-    *reinterpret_cast<float2*>(&s.knew[c0]) = make_float2(k0, k1);
-    *reinterpret_cast<float2*>(&s.vnew[c0]) = make_float2(v0, v1);
+    const int c = lane;
+    s.q[0][c] = outl[0]; s.q[0][c + 64] = outh[0];
+    s.q[1][c] = outl[1]; s.q[1][c + 64] = outh[1];
+    float kl = outl[2], kh = outh[2], vl = v[6], vh = v[7];
+    if constexpr (BB) { kl = rbf(kl); kh = rbf(kh); vl = rbf(vl); vh = rbf(vh); }
+    s.knew[c] = kl; s.knew[c + 64] = kh;
+    s.vnew[c] = vl; s.vnew[c + 64] = vh;
     if (li == C - 1) {
-      const size_t off = (((size_t)layer * NKVH + xcd) * (size_t)a.max_seq + pos) * HDIM + c0;
+      const size_t off = (((size_t)layer * NKVH + xcd) * (size_t)a.max_seq + pos) * HDIM + c;
       if constexpr (BB) {
-        gput(reinterpret_cast<uint32_t*>(reinterpret_cast<bf16_t*>(a.kc) + off), (uint32_t)f2bf(k0) | ((uint32_t)f2bf(k1) << 16));
-        gput(reinterpret_cast<uint32_t*>(reinterpret_cast<bf16_t*>(a.vc) + off), (uint32_t)f2bf(v0) | ((uint32_t)f2bf(v1) << 16));
+        bf16_t* kc = reinterpret_cast<bf16_t*>(a.kc) + off;
+        bf16_t* vc = reinterpret_cast<bf16_t*>(a.vc) + off;
+        gput(kc, f2bf(kl)); gput(kc + 64, f2bf(kh));
+        gput(vc, f2bf(vl)); gput(vc + 64, f2bf(vh));
       } else {
-        gput(reinterpret_cast<u32x2*>(reinterpret_cast<float*>(a.kc) + off), u32x2{__float_as_uint(k0), __float_as_uint(k1)});
-        gput(reinterpret_cast<u32x2*>(reinterpret_cast<float*>(a.vc) + off), u32x2{__float_as_uint(v0), __float_as_uint(v1)});
+        float* kc = reinterpret_cast<float*>(a.kc) + off;
+        float* vc = reinterpret_cast<float*>(a.vc) + off;
+        gput(kc, kl); gput(kc + 64, kh);
+        gput(vc, vl); gput(vc + 64, vh);
       }
       // ordered before this wave's next slot publish (prep_gu), where the wait for the stores
       // costs nothing: the entry is read from memory only at later positions or launches
@@ -957,7 +958,10 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) v[r] = dot8d(tq.p[2 * r + 1], xv + 8, dot8d(tq.p[2 * r], xv, 0.0));
     const double t = rs_sum<5, 4>(v, lane);   // row lane >> 4 in lanes 0, 16, 32, 48
-    if ((lane & 15) == 0) pub_local(&ws->qkv[xcd][lp & 1][16 * li + 4 * mw + (lane >> 4)], (float)t, tg);
+    // slot order pairs the rotate_half partners: channel c' of head h goes to slot
+    // 128 h + 2 (c' mod 64) + c' / 64, so one 16-byte pair holds channels c and c + 64
+    const int lr = 16 * li + 4 * mw + (lane >> 4), cc = lr & 127;
+    if ((lane & 15) == 0) pub_local(&ws->qkv[xcd][lp & 1][(lr & ~127) + 2 * (cc & 63) + (cc >> 6)], (float)t, tg);
   };
   auto math_o = [&](int lp, bool merged) {
     // chunked attention: merge, one column per thread: f32((sum_c acc_c w_c) * (1 / Z)); chunks
