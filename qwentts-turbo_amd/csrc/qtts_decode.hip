@@ -58,6 +58,35 @@ enum TagSlot { T_QKV = 0, T_ATT, T_OPART, T_H1, T_INTER, T_DPART, T_XL, T_NSLOT 
 constexpr uint32_t TAG_HEAD = 3584;   // head logits tags: TAG_HEAD + position index
 constexpr int MAX_LAYER_PASSES = 440; // layer passes per launch: 8 * 440 < TAG_HEAD
 
+// Per-stream launch arguments. A batch-1 launch fills io[0]; a launch with one stream per XCD
+// fills io[x] for the stream of XCD x.
+constexpr int NSTREAM = NXCD;
+struct StreamIO {
+  Workspace* ws;
+  void* kc;
+  void* vc;
+  int pos0;        // cache slot of the first position
+  int pos3[3];     // rotary (t, h, w) of a single backbone position
+  const bf16_t* in_emb;    // bf16 [1024] input of the first position
+  int in_tok;              // token-id gather when in_emb == nullptr
+  float* out_hidden;       // f32 [1024] final-norm hidden
+  void* out_residual;      // bf16 (backbone) / f32 (CP) [1024], may be null
+  float* out_logits;
+  int* out_token;
+  const int* history;
+  int n_history;
+  const int* skip;
+  // code-predictor frame
+  const float* bb_hidden;
+  const int* g0;
+  const bf16_t* text_row;
+  int* out_tokens;
+  int* hist_slot;
+  bf16_t* out_combined;
+  int* done;
+  uint64_t seed;           // sampler key
+};
+
 // Per-launch arguments (passed by value).
 struct KArgs {
   const TTSLayerWeights* layers;
@@ -65,49 +94,29 @@ struct KArgs {
   const bf16_t* final_norm;
   const bf16_t* cos_t;
   const bf16_t* sin_t;
-  void* kc;
-  void* vc;
   int max_seq;
   float scale;
-  Workspace* ws;
   uint32_t tag_base;
   uint32_t spin_cap;
-  int pos0;        // cache slot of the first position
   int n_pos;       // positions processed by this launch
-  int pos3[3];     // rotary (t, h, w) of a single backbone position
-  const bf16_t* in_emb;    // bf16 [1024] input of the first position
-  const bf16_t* embed_w;   // token-id gather when in_emb == nullptr
-  int in_tok;
-  float* out_hidden;       // f32 [1024] final-norm hidden
-  void* out_residual;      // bf16 (backbone) / f32 (CP) [1024], may be null
+  const bf16_t* embed_w;   // token-id gather table
   // backbone codec head + selection
   const bf16_t* head;
   int vocab;
-  float* out_logits;
-  int* out_token;
   int mask_tail;
-  const int* history;
-  int n_history;
   float rep_penalty;
   int eos_id;
   int suppress_eos;
-  const int* skip;
   // code-predictor frame
   int cp_frame;
-  const float* bb_hidden;
-  const int* g0;
   const bf16_t* bb_emb;
   const bf16_t* const* cp_heads;
   const bf16_t* const* cp_embs;
   int n_groups;
   int cp_vocab;
-  const bf16_t* text_row;
-  int* out_tokens;
-  int* hist_slot;
-  bf16_t* out_combined;
-  int* done;
-  SelParams sel;
+  SelParams sel;           // sampling parameters (the key is per stream)
   uint64_t* trace;         // optional step timeline: [wg][step][role] s_memrealtime stamps
+  StreamIO io[NSTREAM];
 };
 constexpr int TRACE_STEPS = 1024;
 
@@ -245,7 +254,7 @@ __device__ __forceinline__ void load_head(TileQKV& t, const bf16_t* W, int row0,
 
 // KV sub-block [b0, b0 + SUB) of the chunk, restricted to old positions (< min(bend, Lold)).
 template <bool BB>
-__device__ __forceinline__ void load_kv(TileKV<BB>& t, const KArgs& a, int layer, int kvh, int b0, int lim, int mw, int lane) {
+__device__ __forceinline__ void load_kv(TileKV<BB>& t, const KArgs& a, int si, int layer, int kvh, int b0, int lim, int mw, int lane) {
   constexpr int JJ = KVGeo<BB>::JJ, PPP = KVGeo<BB>::PPP;
   const size_t head_base = ((size_t)layer * NKVH + kvh) * (size_t)a.max_seq;
 #pragma unroll
@@ -257,15 +266,15 @@ __device__ __forceinline__ void load_kv(TileKV<BB>& t, const KArgs& a, int layer
     for (int pp = 0; pp < PPP; ++pp) {
       if constexpr (BB) {
         const size_t off = (head_base + (size_t)pos) * HDIM + 8 * (lane & 15);
-        t.k[jj] = ok ? ldw(reinterpret_cast<const bf16_t*>(a.kc) + off) : u32x4{0, 0, 0, 0};
-        t.v[jj] = ok ? ldw(reinterpret_cast<const bf16_t*>(a.vc) + off) : u32x4{0, 0, 0, 0};
+        t.k[jj] = ok ? ldw(reinterpret_cast<const bf16_t*>(a.io[si].kc) + off) : u32x4{0, 0, 0, 0};
+        t.v[jj] = ok ? ldw(reinterpret_cast<const bf16_t*>(a.io[si].vc) + off) : u32x4{0, 0, 0, 0};
       } else {
         // The code-predictor cache is rewritten inside one frame launch and read by other
         // CUs, so its loads are L2-coherent (sc1: no L1 line of an older write is used).
         // Lanes without a position read past the buffer end, which returns zeros.
         const uint32_t bytes = (uint32_t)((size_t)a.num_layers * NKVH * (size_t)a.max_seq * HDIM * 4);
-        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(a.kc, (short)0, (int)bytes, 0x00020000);
-        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(a.vc, (short)0, (int)bytes, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(a.io[si].kc, (short)0, (int)bytes, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(a.io[si].vc, (short)0, (int)bytes, 0x00020000);
         const uint32_t off = ok ? (uint32_t)(((head_base + (size_t)pos0_) * HDIM + 8 * (lane & 15) + 4 * pp) * 4) : 0xFFFFFFF0u;
         t.k[PPP * jj + pp] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 16);
         t.v[PPP * jj + pp] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 16);
@@ -432,16 +441,17 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   const bool poller = wave == NMATH;
   const int mw = __builtin_amdgcn_readfirstlane(wave);   // wave-uniform: row bases stay in SGPRs
   const int xcd = (int)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15u);  // HW_REG_XCC_ID
+  constexpr int si = 0;   // stream of this workgroup
   const int li = blockIdx.x >> 3;
   const int wg = blockIdx.x;
-  Workspace* ws = a.ws;
+  Workspace* ws = a.io[si].ws;
 
-  if (a.skip != nullptr && *a.skip != 0) return;
+  if (a.io[si].skip != nullptr && *a.io[si].skip != 0) return;
   int g0 = 0;
   if (a.cp_frame) {
-    g0 = *a.g0;
+    g0 = *a.io[si].g0;
     if (a.eos_id >= 0 && g0 == a.eos_id) {
-      if (wg == 0 && threadIdx.x == 0) *a.done = 1;
+      if (wg == 0 && threadIdx.x == 0) *a.io[si].done = 1;
       return;
     }
   }
@@ -481,7 +491,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   auto rot_row = [&](int c, int pos) -> int {
     if constexpr (BB) {
       const int sec = (c < 60 && c % 3 == 1) ? 1 : ((c < 60 && c % 3 == 2) ? 2 : 0);
-      return a.n_pos == 1 ? a.pos3[sec] : pos;
+      return a.n_pos == 1 ? a.io[si].pos3[sec] : pos;
     } else {
       return pos;
     }
@@ -549,7 +559,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     gains_d(g_in, gd);
     float xv[16];
     if (a.cp_frame && pi == 0) {
-      const auto* p = gmem(reinterpret_cast<const u32x2*>(a.bb_hidden));
+      const auto* p = gmem(reinterpret_cast<const u32x2*>(a.io[si].bb_hidden));
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const u32x2 v = p[lane + 64 * k];
@@ -559,7 +569,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     } else {
       const bf16_t* src;
       if (a.cp_frame) src = pi == 1 ? a.bb_emb + (size_t)g0 * HID : s.embp[pi - 2] + (size_t)s.tok[pi - 2] * HID;
-      else src = a.in_emb != nullptr ? a.in_emb : a.embed_w + (size_t)a.in_tok * HID;
+      else src = a.io[si].in_emb != nullptr ? a.io[si].in_emb : a.embed_w + (size_t)a.io[si].in_tok * HID;
       const auto* p = gmem(reinterpret_cast<const uint32_t*>(src));
 #pragma unroll
       for (int k = 0; k < 8; ++k) { const uint32_t w = p[lane + 64 * k]; xv[2 * k] = bflo(w); xv[2 * k + 1] = bfhi(w); }
@@ -618,13 +628,13 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const int e = 2 * (lane + 64 * k);
-        if (a.out_hidden) *reinterpret_cast<float2*>(a.out_hidden + e) = make_float2(y[2 * k], y[2 * k + 1]);
-        if (a.out_residual) {
+        if (a.io[si].out_hidden) *reinterpret_cast<float2*>(a.io[si].out_hidden + e) = make_float2(y[2 * k], y[2 * k + 1]);
+        if (a.io[si].out_residual) {
           if constexpr (BB)
-            reinterpret_cast<uint32_t*>(a.out_residual)[e >> 1] =
+            reinterpret_cast<uint32_t*>(a.io[si].out_residual)[e >> 1] =
                 (uint32_t)f2bf(xv[2 * k]) | ((uint32_t)f2bf(xv[2 * k + 1]) << 16);
           else
-            *reinterpret_cast<float2*>(reinterpret_cast<float*>(a.out_residual) + e) = make_float2(xv[2 * k], xv[2 * k + 1]);
+            *reinterpret_cast<float2*>(reinterpret_cast<float*>(a.io[si].out_residual) + e) = make_float2(xv[2 * k], xv[2 * k + 1]);
         }
       }
     }
@@ -667,13 +677,13 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     if (li == C - 1) {
       const size_t off = (((size_t)layer * NKVH + xcd) * (size_t)a.max_seq + pos) * HDIM + c;
       if constexpr (BB) {
-        bf16_t* kc = reinterpret_cast<bf16_t*>(a.kc) + off;
-        bf16_t* vc = reinterpret_cast<bf16_t*>(a.vc) + off;
+        bf16_t* kc = reinterpret_cast<bf16_t*>(a.io[si].kc) + off;
+        bf16_t* vc = reinterpret_cast<bf16_t*>(a.io[si].vc) + off;
         gput(kc, f2bf(kl)); gput(kc + 64, f2bf(kh));
         gput(vc, f2bf(vl)); gput(vc + 64, f2bf(vh));
       } else {
-        float* kc = reinterpret_cast<float*>(a.kc) + off;
-        float* vc = reinterpret_cast<float*>(a.vc) + off;
+        float* kc = reinterpret_cast<float*>(a.io[si].kc) + off;
+        float* vc = reinterpret_cast<float*>(a.io[si].vc) + off;
         gput(kc, kl); gput(kc + 64, kh);
         gput(vc, vl); gput(vc + 64, vh);
       }
@@ -763,7 +773,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     }
     for (int sb = 0; sb < nsb; ++sb) {
       const int b0 = c0 + sb * SUB;
-      if (sb > 0) load_kv<BB>(tk, a, layer, xcd, b0, c1 < Lold ? c1 : Lold, mw, lane);
+      if (sb > 0) load_kv<BB>(tk, a, si, layer, xcd, b0, c1 < Lold ? c1 : Lold, mw, lane);
       double sc[NH * JJ];
 #pragma unroll
       for (int jj = 0; jj < JJ; ++jj) {
@@ -1063,7 +1073,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       }
     } else if ((lane & 15) == 0 && r < nrows) {
       pub_cross(&ws->logits[pi & 1][row0 + r], (float)t, tg);
-      if (!a.cp_frame && a.out_logits) a.out_logits[row0 + r] = (float)t;
+      if (!a.cp_frame && a.io[si].out_logits) a.io[si].out_logits[row0 + r] = (float)t;
     }
   };
   auto head_weights = [&](int pi) -> const bf16_t* {
@@ -1126,6 +1136,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     const int n = a.cp_frame ? a.cp_vocab : a.vocab;
     poll_vec<24>(P, ws->logits[pi & 1], n, a.tag_base + TAG_HEAD + (uint32_t)pi, s.stage);
     SelParams sp = a.sel;
+    sp.seed = a.io[si].seed;
     if (a.cp_frame) {
       sp.group = pi;   // CP head pi-1 selects codebook group pi
     } else {
@@ -1134,11 +1145,11 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
         for (int i = lane; i < n; i += 64)
           if (i >= n - 1024 && i != a.eos_id) s.stage[i] = -INFINITY;
       // repetition penalty, once per distinct id (generator.py:161-167)
-      if (a.rep_penalty != 1.0f && a.n_history > 0) {
+      if (a.rep_penalty != 1.0f && a.io[si].n_history > 0) {
         for (int i = lane; i < MAXV / 32; i += 64) s.pen_bits[i] = 0u;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        for (int i = lane; i < a.n_history; i += 64) {
-          const int id = a.history[i];
+        for (int i = lane; i < a.io[si].n_history; i += 64) {
+          const int id = a.io[si].history[i];
           if (id >= 0 && id < n) atomicOr(&s.pen_bits[id >> 5], 1u << (id & 31));
         }
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
@@ -1172,7 +1183,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   };
   // attention over the whole context in every workgroup when it fits one pass of the math
   // waves (attention and O projection then share a step); split into chunks otherwise
-  auto att_local = [&](int pi) { return a.pos0 + pi + 1 <= KVGeo<BB>::SUB; };
+  auto att_local = [&](int pi) { return a.io[si].pos0 + pi + 1 <= KVGeo<BB>::SUB; };
   auto walk = [&](auto&& act) {
     act(S_PRO, 0, 0); stamp();
     step_barrier();
@@ -1190,7 +1201,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   struct PosInfo { int pos, L, C, P, c0, c1; bool local, has_chunk, last_pos, head; };
   auto pinfo = [&](int pi) {
     PosInfo q;
-    q.pos = a.pos0 + pi;
+    q.pos = a.io[si].pos0 + pi;
     q.L = q.pos + 1;
     chunking<BB>(q.L, q.C, q.P);
     q.local = att_local(pi);
@@ -1272,8 +1283,8 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
                 if (wg == 0) comb_add(false);
                 load_gain_pairs(g_in, lw(LW, NL > 1 ? 1 : 0, W_LNIN));
               }
-            } else if (lane == 0 && a.out_token) {
-              *a.out_token = tok;
+            } else if (lane == 0 && a.io[si].out_token) {
+              *a.io[si].out_token = tok;
             }
           }
           break;
@@ -1293,7 +1304,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           break;
         case S_QKV:
           math_qkv(lp);
-          if (q.has_chunk) load_kv<BB>(tk, a, layer, xcd, q.c0, min(q.c1, q.L - 1), mw, lane);
+          if (q.has_chunk) load_kv<BB>(tk, a, si, layer, xcd, q.c0, min(q.c1, q.L - 1), mw, lane);
           else tk = TileKV<BB>{};
           if (q.local) load_o<BB>(to, LW, layer, xcd, li, mw, lane);
           break;
@@ -1346,9 +1357,9 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   // ---- code-predictor frame epilogue: tokens and the bf16 embedding combine
   if (a.cp_frame && wg == 0 && poller) {
     if (lane == 0) {
-      if (a.hist_slot) *a.hist_slot = g0;
-      a.out_tokens[0] = g0;
-      for (int g = 0; g < a.n_groups; ++g) a.out_tokens[1 + g] = s.tok[g];
+      if (a.io[si].hist_slot) *a.io[si].hist_slot = g0;
+      a.io[si].out_tokens[0] = g0;
+      for (int g = 0; g < a.n_groups; ++g) a.io[si].out_tokens[1 + g] = s.tok[g];
     }
     // s.comb holds emb_bb[g0] + emb_0[t_0] + ... + emb_{n-2}[t_{n-2}] (each row was loaded as a
     // position's input); the last group's row and the text row complete it (generator.py:356-362)
@@ -1357,8 +1368,8 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     uint32_t wl[8], wt[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) wl[k] = lr[lane + 64 * k];
-    if (a.text_row) {
-      const auto* tr = gmem(reinterpret_cast<const uint32_t*>(a.text_row));
+    if (a.io[si].text_row) {
+      const auto* tr = gmem(reinterpret_cast<const uint32_t*>(a.io[si].text_row));
 #pragma unroll
       for (int k = 0; k < 8; ++k) wt[k] = tr[lane + 64 * k];
     }
@@ -1366,8 +1377,8 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     for (int k = 0; k < 8; ++k) {
       const int e = 2 * (lane + 64 * k);
       float a0 = rbf(s.comb[e] + bflo(wl[k])), a1 = rbf(s.comb[e + 1] + bfhi(wl[k]));
-      if (a.text_row) { a0 = rbf(a0 + bflo(wt[k])); a1 = rbf(a1 + bfhi(wt[k])); }
-      gput(reinterpret_cast<uint32_t*>(a.out_combined) + (e >> 1), (uint32_t)f2bf(a0) | ((uint32_t)f2bf(a1) << 16));
+      if (a.io[si].text_row) { a0 = rbf(a0 + bflo(wt[k])); a1 = rbf(a1 + bfhi(wt[k])); }
+      gput(reinterpret_cast<uint32_t*>(a.io[si].out_combined) + (e >> 1), (uint32_t)f2bf(a0) | ((uint32_t)f2bf(a1) << 16));
     }
   }
 }
@@ -1460,9 +1471,9 @@ hipError_t launch(bool bb, KArgs& a, hipStream_t stream) {
   if (e != hipSuccess) return e;
   if ((e = check_device(dev)) != hipSuccess) return e;
   if (a.num_layers < 1 || a.n_pos < 1 || a.num_layers * a.n_pos > qtts::MAX_LAYER_PASSES) return hipErrorInvalidValue;
-  if (a.pos0 < 0 || a.pos0 + a.n_pos > a.max_seq) return hipErrorInvalidValue;
+  if (a.io[0].pos0 < 0 || a.io[0].pos0 + a.n_pos > a.max_seq) return hipErrorInvalidValue;
   hipError_t ze = hipSuccess;
-  a.tag_base = next_tag_base(a.ws, stream, &ze);
+  a.tag_base = next_tag_base(a.io[0].ws, stream, &ze);
   if (ze != hipSuccess) return ze;
   a.spin_cap = kSpinCap;
   a.trace = g_trace;
@@ -1493,8 +1504,8 @@ void base_args(KArgs& a, const TTSLayerWeights* layers, int num_layers, const vo
   a.final_norm = reinterpret_cast<const qtts::bf16_t*>(final_norm);
   a.cos_t = reinterpret_cast<const qtts::bf16_t*>(cos_t);
   a.sin_t = reinterpret_cast<const qtts::bf16_t*>(sin_t);
-  a.kc = kc;
-  a.vc = vc;
+  a.io[0].kc = kc;
+  a.io[0].vc = vc;
   a.max_seq = max_seq;
   a.scale = 0.08838834764831845f;
   a.eos_id = -1;
@@ -1517,14 +1528,14 @@ hipError_t ref_launch(bool bb, int token, const void* embed, const void* emb, co
   KArgs a;
   base_args(a, layers, num_layers, final_norm, cos_t, sin_t, kc, vc, max_seq_len);
   a.scale = attn_scale;
-  a.ws = reinterpret_cast<Workspace*>(ws);
-  a.pos0 = position;
-  a.pos3[0] = a.pos3[1] = a.pos3[2] = position;
-  a.in_emb = reinterpret_cast<const qtts::bf16_t*>(emb);
+  a.io[0].ws = reinterpret_cast<Workspace*>(ws);
+  a.io[0].pos0 = position;
+  a.io[0].pos3[0] = a.io[0].pos3[1] = a.io[0].pos3[2] = position;
+  a.io[0].in_emb = reinterpret_cast<const qtts::bf16_t*>(emb);
   a.embed_w = reinterpret_cast<const qtts::bf16_t*>(embed);
-  a.in_tok = token;
-  a.out_hidden = reinterpret_cast<float*>(g_normalized);
-  a.out_residual = hidden_buffer;
+  a.io[0].in_tok = token;
+  a.io[0].out_hidden = reinterpret_cast<float*>(g_normalized);
+  a.io[0].out_residual = hidden_buffer;
   return launch(bb, a, stream);
 }
 
@@ -1610,24 +1621,24 @@ hipError_t qtts_backbone_step(void* workspace, const TTSLayerWeights* layer_weig
   if (n_history < 0 || (n_history > 0 && history == nullptr)) return hipErrorInvalidValue;
   KArgs a;
   base_args(a, layer_weights, num_layers, final_norm_weight, cos_table, sin_table, k_cache, v_cache, max_seq_len);
-  a.ws = reinterpret_cast<Workspace*>(workspace);
-  a.pos0 = position;
-  for (int i = 0; i < 3; ++i) a.pos3[i] = pos3 ? pos3[i] : position;
+  a.io[0].ws = reinterpret_cast<Workspace*>(workspace);
+  a.io[0].pos0 = position;
+  for (int i = 0; i < 3; ++i) a.io[0].pos3[i] = pos3 ? pos3[i] : position;
   for (int i = 0; i < 3; ++i)
-    if (a.pos3[i] < 0 || a.pos3[i] >= max_seq_len) return hipErrorInvalidValue;
-  a.in_emb = reinterpret_cast<const qtts::bf16_t*>(input_embedding);
+    if (a.io[0].pos3[i] < 0 || a.io[0].pos3[i] >= max_seq_len) return hipErrorInvalidValue;
+  a.io[0].in_emb = reinterpret_cast<const qtts::bf16_t*>(input_embedding);
   a.embed_w = reinterpret_cast<const qtts::bf16_t*>(embed_weight);
-  a.in_tok = input_token_id;
-  a.out_hidden = out_hidden;
-  a.out_residual = out_residual;
+  a.io[0].in_tok = input_token_id;
+  a.io[0].out_hidden = out_hidden;
+  a.io[0].out_residual = out_residual;
   a.head = reinterpret_cast<const qtts::bf16_t*>(codec_head);
   a.vocab = vocab;
-  a.out_logits = out_logits;
-  a.out_token = out_token;
+  a.io[0].out_logits = out_logits;
+  a.io[0].out_token = out_token;
   a.mask_tail = mask_tail;
-  a.skip = skip_if;
-  a.history = history;
-  a.n_history = n_history;
+  a.io[0].skip = skip_if;
+  a.io[0].history = history;
+  a.io[0].n_history = n_history;
   a.rep_penalty = repetition_penalty;
   a.eos_id = eos_id;
   a.suppress_eos = suppress_eos;
@@ -1636,7 +1647,7 @@ hipError_t qtts_backbone_step(void* workspace, const TTSLayerWeights* layer_weig
     a.sel.temperature = sampling->temperature;
     a.sel.top_k = sampling->top_k;
     a.sel.top_p = sampling->top_p;
-    a.sel.seed = sampling->seed;
+    a.io[0].seed = sampling->seed;
   }
   a.sel.frame_step = frame_step;
   return launch(true, a, stream);
@@ -1649,11 +1660,11 @@ hipError_t qtts_cp_step(void* workspace, const CPLayerWeights* layer_weights, in
   if (workspace == nullptr || input_embedding == nullptr) return hipErrorInvalidValue;
   KArgs a;
   base_args(a, layer_weights, num_layers, final_norm_weight, cos_table, sin_table, k_cache, v_cache, max_seq_len);
-  a.ws = reinterpret_cast<Workspace*>(workspace);
-  a.pos0 = position;
-  a.in_emb = reinterpret_cast<const qtts::bf16_t*>(input_embedding);
-  a.out_hidden = out_hidden;
-  a.out_residual = out_residual;
+  a.io[0].ws = reinterpret_cast<Workspace*>(workspace);
+  a.io[0].pos0 = position;
+  a.io[0].in_emb = reinterpret_cast<const qtts::bf16_t*>(input_embedding);
+  a.io[0].out_hidden = out_hidden;
+  a.io[0].out_residual = out_residual;
   return launch(false, a, stream);
 }
 
@@ -1671,29 +1682,29 @@ hipError_t qtts_cp_frame(void* workspace, const CPLayerWeights* layer_weights, i
   if (cp_vocab <= 0 || cp_vocab > qtts::MAXV || cp_vocab % (qtts::NWG * qtts::NMATH) != 0) return hipErrorInvalidValue;
   KArgs a;
   base_args(a, layer_weights, num_layers, final_norm_weight, cos_table, sin_table, k_cache, v_cache, max_seq_len);
-  a.ws = reinterpret_cast<Workspace*>(workspace);
-  a.pos0 = 0;
+  a.io[0].ws = reinterpret_cast<Workspace*>(workspace);
+  a.io[0].pos0 = 0;
   a.n_pos = n_groups + 1;
   a.cp_frame = 1;
-  a.bb_hidden = bb_hidden;
-  a.g0 = g0;
+  a.io[0].bb_hidden = bb_hidden;
+  a.io[0].g0 = g0;
   a.bb_emb = reinterpret_cast<const qtts::bf16_t*>(bb_embedding);
   a.cp_heads = reinterpret_cast<const qtts::bf16_t* const*>(lm_heads);
   a.cp_embs = reinterpret_cast<const qtts::bf16_t* const*>(cp_embeddings);
   a.n_groups = n_groups;
   a.cp_vocab = cp_vocab;
-  a.text_row = reinterpret_cast<const qtts::bf16_t*>(text_row);
-  a.out_tokens = out_tokens;
-  a.hist_slot = g0_history_slot;
-  a.out_combined = reinterpret_cast<qtts::bf16_t*>(out_combined);
+  a.io[0].text_row = reinterpret_cast<const qtts::bf16_t*>(text_row);
+  a.io[0].out_tokens = out_tokens;
+  a.io[0].hist_slot = g0_history_slot;
+  a.io[0].out_combined = reinterpret_cast<qtts::bf16_t*>(out_combined);
   a.eos_id = eos_id;
-  a.done = done;
+  a.io[0].done = done;
   if (sampling) {
     a.sel.do_sample = sampling->do_sample;
     a.sel.temperature = sampling->temperature;
     a.sel.top_k = sampling->top_k;
     a.sel.top_p = sampling->top_p;
-    a.sel.seed = sampling->seed;
+    a.io[0].seed = sampling->seed;
   }
   a.sel.frame_step = frame_step;
   return launch(false, a, stream);
