@@ -131,7 +131,7 @@ def batched_c4(pkg, sd, frames: int = 10) -> dict:
     dec.check_error()
     return {"streams": 8, "lengths": lengths, "frames": frames,
             "frames_per_s_total": round(8 * frames / el, 2), "frames_per_s_per_stream": round(frames / el, 2),
-            "note": "per-stream launches of the batch-1 kernels over shared weights"}
+            "note": "backbone: one batch-1 launch per stream; code predictor: one launch for all streams, stream s on XCD s"}
 
 
 def main():

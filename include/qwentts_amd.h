@@ -182,6 +182,24 @@ hipError_t qtts_cp_frame(
     const void* text_row, int* out_tokens, void* out_combined, int* g0_history_slot,
     int eos_id, int* done, const QttsSampling* sampling, int frame_step, hipStream_t stream);
 
+/* Code-predictor frames of n_streams (1..8) independent streams in one launch; no counterpart in the
+ * reference, whose decode is batch 1 (fused_decode_code_predictor.cu:565-668 runs one stream). Stream s
+ * runs on XCD s alone (its 32 workgroups, every exchange in that XCD's L2) and computes exactly what
+ * qtts_cp_frame computes for it. Per-stream data is contiguous with fixed strides:
+ *   workspaces: n_streams x qtts_workspace_bytes(), 256-byte aligned, zero-filled before first use;
+ *   k_caches / v_caches: n_streams x (num_layers x 8 x max_seq_len x 128) f32;
+ *   bb_hidden [n, 1024] f32; g0 [n] int32; text_rows [n, 1024] bf16 or NULL;
+ *   out_tokens [n, n_groups + 1] int32; out_combined [n, 1024] bf16; done [n] int32.
+ * Stream s draws with key sampling->seed + s. n_groups + 1 <= 16 (one attention pass). */
+hipError_t qtts_cp_frame_streams(
+    int n_streams, void* workspaces, const CPLayerWeights* layer_weights, int num_layers,
+    const void* final_norm_weight, const void* cos_table, const void* sin_table,
+    void* k_caches, void* v_caches, int max_seq_len,
+    const float* bb_hidden, const int* g0, const void* bb_embedding,
+    const void* const* lm_heads, const void* const* cp_embeddings, int n_groups, int cp_vocab,
+    const void* text_rows, int* out_tokens, void* out_combined,
+    int eos_id, int* done, const QttsSampling* sampling, int frame_step, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,14 +1,14 @@
 """Decode of several independent streams (batch 8, ragged KV lengths).
 
 Each stream keeps its own backbone KV cache and position; all streams share one copy of the
-weights and one code-predictor decoder (its KV cache is rebuilt every frame). A frame of the
-batch is, per stream, one backbone step with codec head + selection and one code-predictor
-frame, each a single persistent-kernel launch queued on the current stream with no host sync.
+weights and one code-predictor decoder. A frame of the batch is one backbone step per stream
+(codec head + selection, a batch-1 launch each) and one launch for the code-predictor frames of
+up to 8 streams: stream s runs on XCD s alone, its 32 workgroups acting as the 8 virtual XCDs
+of the batch-1 decomposition, so every exchange stays in that XCD's L2. Everything is queued on
+the current stream with no host sync, and every stream's results are bit-identical to its
+batch-1 results.
 
-The reference has no batched decode (its megakernels are batch 1, fused_decode_tts.cu:728-831);
-this is the build's batch-1 kernels applied per stream, which keeps every stream bit-identical
-to its batch-1 result. A kernel that shares each weight tile across the streams of a layer
-pass (MFMA bf16 tiles when the batch makes the projections dense) is the planned next step.
+The reference has no batched decode (its megakernels are batch 1, fused_decode_tts.cu:728-831).
 """
 from __future__ import annotations
 
@@ -22,6 +22,8 @@ from .megakernel_code_predictor import CodePredictorMegakernelGenerator
 
 class BatchedTTSDecoder:
     """``n_streams`` backbone decoders over shared weights plus one code predictor."""
+
+    MAX_PER_LAUNCH = 8   # code-predictor frames per launch: one stream per XCD
 
     def __init__(self, model, n_streams: int, max_seq_len: int = 4096, cp_max_seq_len: int = 32,
                  device="cuda"):
@@ -73,16 +75,22 @@ class BatchedTTSDecoder:
                   do_sample: bool = False, temperature: float = 0.9, top_k: int = 50, seed: int = 0,
                   frame_step: int = 0) -> None:
         """A code-predictor frame per stream: ``tokens_out[s]`` (int32 [16]) gets g0 and the 15
-        group ids, ``combined_out[s]`` (bf16 [1024]) the embedding sum plus ``text_rows[s]``."""
-        done = torch.zeros(self.n_streams, dtype=torch.int32, device=self.device)
-        for s in range(self.n_streams):
-            text = text_rows[s] if text_rows is not None else torch.zeros(1024, dtype=torch.bfloat16,
-                                                                            device=self.device)
-            self.cp.decoder.frame(hidden[s], g0[s:s + 1], text, tokens_out[s], combined_out[s], int(eos_id),
-                                  done[s:s + 1], bool(do_sample), float(temperature), int(top_k), 1.0,
-                                  int(seed) + s, int(frame_step))
+        group ids, ``combined_out[s]`` (bf16 [1024]) the embedding sum plus ``text_rows[s]``.
+        Up to 8 streams share one launch, stream s on XCD s (``frames_streams``); stream s draws
+        with key ``seed + s``."""
+        n = self.n_streams
+        done = torch.zeros(n, dtype=torch.int32, device=self.device)
+        hid = hidden.to(self.device, torch.float32).contiguous()
+        g = g0.to(self.device, torch.int32).contiguous()
+        tr = text_rows.to(self.device, torch.bfloat16).contiguous() if text_rows is not None else None
+        for b in range(0, n, self.MAX_PER_LAUNCH):
+            e = min(n, b + self.MAX_PER_LAUNCH)
+            self.cp.decoder.frames_streams(hid[b:e], g[b:e], tr[b:e] if tr is not None else None, tokens_out[b:e],
+                                           combined_out[b:e], int(eos_id), done[b:e], bool(do_sample),
+                                           float(temperature), int(top_k), 1.0, int(seed) + b, int(frame_step))
 
     def check_error(self):
         for dec in self.streams:
             dec.check_error()
         self.cp.check_error()
+        self.cp.decoder.check_error_streams()

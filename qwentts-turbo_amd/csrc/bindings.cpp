@@ -18,6 +18,7 @@
 namespace {
 
 constexpr int kHidden = 1024, kKVHeads = 8, kHeadDim = 128, kInter = 3072, kQ = 2048;
+constexpr int kMaxStreams = 8;   // streams of one frames_streams() launch (one per XCD)
 
 hipStream_t cur_stream() { return c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream(); }
 
@@ -337,6 +338,61 @@ class MegakernelCodePredictorDecoder {
               "qtts_cp_frame");
   }
 
+  // Extended: frames of n (1..8) independent streams in one launch, stream s on XCD s (its own
+  // workspace and KV cache, allocated on first use); row s of each argument belongs to stream s.
+  void frames_streams(torch::Tensor bb_hidden, torch::Tensor g0, c10::optional<torch::Tensor> text_rows,
+                      torch::Tensor out_tokens, torch::Tensor out_combined, int64_t eos_id, torch::Tensor done,
+                      bool do_sample, double temperature, int64_t top_k, double top_p, int64_t seed, int64_t frame_step) {
+    TORCH_CHECK(!heads_.empty(), "call set_heads() before frames_streams()");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(dev_);
+    const int64_t n = bb_hidden.size(0);
+    const int64_t groups = (int64_t)heads_.size();
+    TORCH_CHECK(n >= 1 && n <= kMaxStreams, "1..", kMaxStreams, " streams per launch, got ", n);
+    TORCH_CHECK(bb_hidden.is_cuda() && bb_hidden.scalar_type() == torch::kFloat32 && bb_hidden.dim() == 2 &&
+                    bb_hidden.size(1) == kHidden && bb_hidden.is_contiguous(), "bb_hidden must be contiguous f32 [n, 1024]");
+    TORCH_CHECK(g0.is_cuda() && g0.scalar_type() == torch::kInt32 && g0.numel() == n && g0.is_contiguous(), "g0 must be int32 [n]");
+    TORCH_CHECK(out_tokens.is_cuda() && out_tokens.scalar_type() == torch::kInt32 && out_tokens.dim() == 2 &&
+                    out_tokens.size(0) == n && out_tokens.size(1) == groups + 1 && out_tokens.is_contiguous(),
+                "out_tokens must be contiguous int32 [n, groups + 1]");
+    TORCH_CHECK(out_combined.is_cuda() && out_combined.scalar_type() == torch::kBFloat16 && out_combined.dim() == 2 &&
+                    out_combined.size(0) == n && out_combined.size(1) == kHidden && out_combined.is_contiguous(),
+                "out_combined must be contiguous bf16 [n, 1024]");
+    TORCH_CHECK(done.is_cuda() && done.scalar_type() == torch::kInt32 && done.numel() == n && done.is_contiguous(), "done must be int32 [n]");
+    const void* tr = nullptr;
+    if (text_rows.has_value()) {
+      TORCH_CHECK(text_rows->is_cuda() && text_rows->scalar_type() == torch::kBFloat16 && text_rows->dim() == 2 &&
+                      text_rows->size(0) == n && text_rows->size(1) == kHidden && text_rows->is_contiguous(),
+                  "text_rows must be contiguous bf16 [n, 1024]");
+      tr = text_rows->data_ptr();
+    }
+    if (!ws_streams_.defined()) {
+      ws_streams_ = torch::zeros({(int64_t)(kMaxStreams * qtts_workspace_bytes())}, torch::dtype(torch::kUInt8).device(dev_));
+      hip_check(qtts_workspace_init(ws_streams_.data_ptr(), dev_.index()), "qtts_workspace_init");
+      auto f32 = torch::dtype(torch::kFloat32).device(dev_);
+      k_streams_ = torch::zeros({kMaxStreams, num_layers_, kKVHeads, max_seq_len_, kHeadDim}, f32);
+      v_streams_ = torch::zeros({kMaxStreams, num_layers_, kKVHeads, max_seq_len_, kHeadDim}, f32);
+    }
+    QttsSampling smp = sampling(do_sample, temperature, top_k, top_p, seed);
+    hip_check(qtts_cp_frame_streams((int)n, ws_streams_.data_ptr(), reinterpret_cast<const CPLayerWeights*>(d_layer_weights_.data_ptr()),
+                                    num_layers_, final_norm_weight_.data_ptr(), cos_table_.data_ptr(), sin_table_.data_ptr(),
+                                    k_streams_.data_ptr(), v_streams_.data_ptr(), max_seq_len_, bb_hidden.data_ptr<float>(),
+                                    g0.data_ptr<int>(), bb_emb_.data_ptr(), reinterpret_cast<const void* const*>(d_heads_.data_ptr()),
+                                    reinterpret_cast<const void* const*>(d_embs_.data_ptr()), (int)groups, cp_vocab_, tr,
+                                    out_tokens.data_ptr<int>(), out_combined.data_ptr(), (int)eos_id, done.data_ptr<int>(), &smp,
+                                    (int)frame_step, cur_stream()),
+              "qtts_cp_frame_streams");
+  }
+  void check_error_streams() const {
+    if (!ws_streams_.defined()) return;
+    for (int st = 0; st < kMaxStreams; ++st) {
+      unsigned int code = 0;
+      hip_check(qtts_workspace_check(static_cast<uint8_t*>(ws_streams_.data_ptr()) + st * qtts_workspace_bytes(), &code, cur_stream()),
+                "qtts_workspace_check");
+      TORCH_CHECK(code == 0, "stream ", st, ": decode kernel reported a device-side wait timeout (error word ", code, ")");
+    }
+  }
+
+
   void reset() {
     position_ = 0;
     k_cache_.zero_();
@@ -370,6 +426,7 @@ class MegakernelCodePredictorDecoder {
   std::vector<torch::Tensor> layer_weights_tensors_, heads_, embs_;
   torch::Tensor bb_emb_, d_heads_, d_embs_;
   torch::Tensor k_cache_, v_cache_, hidden_buffer_, g_normalized_, ws_;
+  torch::Tensor ws_streams_, k_streams_, v_streams_;   // frames_streams(): per-stream workspaces and KV caches
 };
 
 }  // namespace
@@ -409,6 +466,11 @@ PYBIND11_MODULE(_qwentts_amd_C, m) {
       .def(py::init<std::vector<torch::Tensor>, torch::Tensor, torch::Tensor, torch::Tensor, int64_t, int64_t>())
       .def("decode_step_with_embedding", &MegakernelCodePredictorDecoder::decode_step_with_embedding)
       .def("set_heads", &MegakernelCodePredictorDecoder::set_heads)
+      .def("frames_streams", &MegakernelCodePredictorDecoder::frames_streams, py::arg("bb_hidden"), py::arg("g0"),
+           py::arg("text_rows"), py::arg("out_tokens"), py::arg("out_combined"), py::arg("eos_id"), py::arg("done"),
+           py::arg("do_sample"), py::arg("temperature"), py::arg("top_k"), py::arg("top_p"), py::arg("seed"),
+           py::arg("frame_step"))
+      .def("check_error_streams", &MegakernelCodePredictorDecoder::check_error_streams)
       .def("frame", &MegakernelCodePredictorDecoder::frame, py::arg("bb_hidden"), py::arg("g0"), py::arg("text_row"),
            py::arg("out_tokens"), py::arg("out_combined"), py::arg("eos_id"), py::arg("done"), py::arg("do_sample"),
            py::arg("temperature"), py::arg("top_k"), py::arg("top_p"), py::arg("seed"), py::arg("frame_step"),

@@ -33,6 +33,11 @@
 
 namespace qtts {
 
+// Forced inlining for the step lambdas the compiler would otherwise call (their one-stream-per-XCD
+// branches make them large): a real call passes the by-value launch arguments by address, which
+// copies them to scratch memory.
+#define QTTS_INLINE __attribute__((always_inline))
+
 // ---------------------------------------------------------------------------------------
 // Workspace (device): exchange slots, double-buffered by layer-pass parity.
 // ---------------------------------------------------------------------------------------
@@ -254,7 +259,7 @@ __device__ __forceinline__ void load_head(TileQKV& t, const bf16_t* W, int row0,
 
 // KV sub-block [b0, b0 + SUB) of the chunk, restricted to old positions (< min(bend, Lold)).
 template <bool BB>
-__device__ __forceinline__ void load_kv(TileKV<BB>& t, const KArgs& a, int si, int layer, int kvh, int b0, int lim, int mw, int lane) {
+__device__ __forceinline__ void load_kv(TileKV<BB>& t, const KArgs& a, const void* kcp, const void* vcp, int layer, int kvh, int b0, int lim, int mw, int lane) {
   constexpr int JJ = KVGeo<BB>::JJ, PPP = KVGeo<BB>::PPP;
   const size_t head_base = ((size_t)layer * NKVH + kvh) * (size_t)a.max_seq;
 #pragma unroll
@@ -266,15 +271,15 @@ __device__ __forceinline__ void load_kv(TileKV<BB>& t, const KArgs& a, int si, i
     for (int pp = 0; pp < PPP; ++pp) {
       if constexpr (BB) {
         const size_t off = (head_base + (size_t)pos) * HDIM + 8 * (lane & 15);
-        t.k[jj] = ok ? ldw(reinterpret_cast<const bf16_t*>(a.io[si].kc) + off) : u32x4{0, 0, 0, 0};
-        t.v[jj] = ok ? ldw(reinterpret_cast<const bf16_t*>(a.io[si].vc) + off) : u32x4{0, 0, 0, 0};
+        t.k[jj] = ok ? ldw(reinterpret_cast<const bf16_t*>(kcp) + off) : u32x4{0, 0, 0, 0};
+        t.v[jj] = ok ? ldw(reinterpret_cast<const bf16_t*>(vcp) + off) : u32x4{0, 0, 0, 0};
       } else {
         // The code-predictor cache is rewritten inside one frame launch and read by other
         // CUs, so its loads are L2-coherent (sc1: no L1 line of an older write is used).
         // Lanes without a position read past the buffer end, which returns zeros.
         const uint32_t bytes = (uint32_t)((size_t)a.num_layers * NKVH * (size_t)a.max_seq * HDIM * 4);
-        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(a.io[si].kc, (short)0, (int)bytes, 0x00020000);
-        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(a.io[si].vc, (short)0, (int)bytes, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(kcp), (short)0, (int)bytes, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(vcp), (short)0, (int)bytes, 0x00020000);
         const uint32_t off = ok ? (uint32_t)(((head_base + (size_t)pos0_) * HDIM + 8 * (lane & 15) + 4 * pp) * 4) : 0xFFFFFFF0u;
         t.k[PPP * jj + pp] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 16);
         t.v[PPP * jj + pp] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 16);
@@ -413,6 +418,27 @@ __device__ __forceinline__ bool poll_sum8(const Poll& P, const uint64_t (*part)[
   s1 += xlane_d<5>(s1);
   return ok;
 }
+// One stream per XCD: the 8 partials of rows r0 + 2 (lane + 64 k) + {0, 1} (k < 2, 256 rows) in
+// this lane, summed as ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7)), the order of poll_sum8.
+// sum[2 k + j] is row r0 + 2 (lane + 64 k) + j.
+__device__ __forceinline__ bool poll_sum8_rows(const Poll& P, const uint64_t (*part)[HID], int r0, uint32_t tag, double (&sum)[4]) {
+  const uint32_t o = ws_off(P, &part[0][r0]);
+  float v[32];
+  const bool ok = poll_regs<16>(P, 1024, tag, v, [o](int i) {
+    const uint32_t q = (uint32_t)i >> 6, l = (uint32_t)i & 63u;   // q = 8 k + x
+    return o + (q & 7u) * (HID * 8u) + 16u * (l + 64u * (q >> 3));
+  });
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      double p[NXCD];
+#pragma unroll
+      for (int x = 0; x < NXCD; ++x) p[x] = (double)v[2 * (8 * k + x) + j];
+      sum[2 * k + j] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+    }
+  return ok;
+}
 
 // RMSNorm epsilon: the f32 constant 1e-6f of the reference, used in f64 arithmetic.
 constexpr double EPSD = (double)1e-6f;
@@ -430,7 +456,11 @@ __device__ __forceinline__ void step_barrier() {
 // ---------------------------------------------------------------------------------------
 // The kernel
 // ---------------------------------------------------------------------------------------
-template <bool BB>
+// XL = one stream per XCD: stream x runs on the 32 workgroups of XCD x, which act as 8 virtual
+// XCDs of 4 workgroups each (workgroup l of the XCD is virtual XCD l & 7 and takes its row groups
+// 8 (l >> 3) .. 8 (l >> 3) + 7, one after another). The exchange slots and their order are those
+// of the batch-1 decomposition, so every stream computes exactly what a batch-1 launch does.
+template <bool BB, bool XL>
 __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   __shared__ Lds s;
   // lane index, re-derived opaquely at every step (see walk) so that lane-dependent slot
@@ -440,18 +470,30 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   const int wave = threadIdx.x >> 6;
   const bool poller = wave == NMATH;
   const int mw = __builtin_amdgcn_readfirstlane(wave);   // wave-uniform: row bases stay in SGPRs
-  const int xcd = (int)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15u);  // HW_REG_XCC_ID
-  constexpr int si = 0;   // stream of this workgroup
-  const int li = blockIdx.x >> 3;
+  const int xcd_hw = (int)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15u);  // HW_REG_XCC_ID
+  const int li_hw = blockIdx.x >> 3;
+  const int si = XL ? xcd_hw : 0;              // stream of this workgroup
+  // this stream's block, read through the kernel-argument segment with a uniform offset (scalar
+  // loads); indexing the by-value argument with a run-time index would copy it to scratch
+  const __attribute__((address_space(4))) StreamIO* IO =
+      (const __attribute__((address_space(4))) StreamIO*)((const __attribute__((address_space(4))) char*)
+                                                          __builtin_amdgcn_kernarg_segment_ptr() + offsetof(KArgs, io)) + si;
+  // per-stream field: XL through IO, batch 1 at its constant offset in the by-value arguments
+#define SIO(f) (XL ? IO->f : a.io[0].f)
+  const int xcd = XL ? (li_hw & 7) : xcd_hw;   // (virtual) XCD: KV head and row ownership
+  const int li = XL ? 8 * (li_hw >> 3) : li_hw;  // first row group of this workgroup
+  constexpr int NSUB = XL ? 8 : 1;             // row groups per workgroup
   const int wg = blockIdx.x;
-  Workspace* ws = a.io[si].ws;
+  const bool lead = XL ? li_hw == 0 : wg == 0;   // the stream's lead workgroup
+  Workspace* ws = SIO(ws);
+  if (XL && ws == nullptr) return;   // no stream on this XCD
 
-  if (a.io[si].skip != nullptr && *a.io[si].skip != 0) return;
+  if (SIO(skip) != nullptr && *SIO(skip) != 0) return;
   int g0 = 0;
   if (a.cp_frame) {
-    g0 = *a.io[si].g0;
+    g0 = *SIO(g0);
     if (a.eos_id >= 0 && g0 == a.eos_id) {
-      if (wg == 0 && threadIdx.x == 0) *a.io[si].done = 1;
+      if (lead && threadIdx.x == 0) *SIO(done) = 1;
       return;
     }
   }
@@ -472,7 +514,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   };
   auto pub_cross = [&](const uint64_t* p, float v, uint32_t tag) {
     const u32x2 d = {__float_as_uint(v), tag};
-    __builtin_amdgcn_raw_buffer_store_b64(d, P.rs, (int)ws_off(P, p), 0, 16);
+    __builtin_amdgcn_raw_buffer_store_b64(d, P.rs, (int)ws_off(P, p), 0, XL ? 0 : 16);   // XL: all in one XCD
   };
   const TTSLayerWeights* LW = a.layers;
   const int NL = a.num_layers;
@@ -491,7 +533,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   auto rot_row = [&](int c, int pos) -> int {
     if constexpr (BB) {
       const int sec = (c < 60 && c % 3 == 1) ? 1 : ((c < 60 && c % 3 == 2) ? 2 : 0);
-      return a.n_pos == 1 ? a.io[si].pos3[sec] : pos;
+      return a.n_pos == 1 ? SIO(pos3[sec]) : pos;
     } else {
       return pos;
     }
@@ -559,7 +601,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     gains_d(g_in, gd);
     float xv[16];
     if (a.cp_frame && pi == 0) {
-      const auto* p = gmem(reinterpret_cast<const u32x2*>(a.io[si].bb_hidden));
+      const auto* p = gmem(reinterpret_cast<const u32x2*>(SIO(bb_hidden)));
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const u32x2 v = p[lane + 64 * k];
@@ -569,7 +611,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     } else {
       const bf16_t* src;
       if (a.cp_frame) src = pi == 1 ? a.bb_emb + (size_t)g0 * HID : s.embp[pi - 2] + (size_t)s.tok[pi - 2] * HID;
-      else src = a.io[si].in_emb != nullptr ? a.io[si].in_emb : a.embed_w + (size_t)a.io[si].in_tok * HID;
+      else src = SIO(in_emb) != nullptr ? SIO(in_emb) : a.embed_w + (size_t)SIO(in_tok) * HID;
       const auto* p = gmem(reinterpret_cast<const uint32_t*>(src));
 #pragma unroll
       for (int k = 0; k < 8; ++k) { const uint32_t w = p[lane + 64 * k]; xv[2 * k] = bflo(w); xv[2 * k + 1] = bfhi(w); }
@@ -593,8 +635,26 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   };
 
   // ---- poller: AR2 of layer pass lp (down partials + residual) -> xl slots
-  auto ar2 = [&](int lp) {
+  auto ar2 = [&](int lp) QTTS_INLINE {
     const int par = lp & 1;
+    if constexpr (XL) {
+      // the workgroup's 8 row groups: rows 32 li + 2 (lane + 64 k) + {0, 1}
+      double sm[4];
+      float r[4];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        r[2 * k] = s.h1res[32 * li + 2 * (lane + 64 * k)];
+        r[2 * k + 1] = s.h1res[32 * li + 2 * (lane + 64 * k) + 1];
+      }
+      poll_sum8_rows(P, ws->dpart[par], 32 * li, tag_of(lp, T_DPART), sm);
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        float x0 = (float)((double)r[2 * k] + sm[2 * k]), x1 = (float)((double)r[2 * k + 1] + sm[2 * k + 1]);
+        if constexpr (BB) { x0 = rbf(x0); x1 = rbf(x1); }
+        pub_local2(&ws->xl[xcd][par][32 * li + 2 * (lane + 64 * k)], x0, x1, tag_of(lp, T_XL));
+      }
+      return;
+    }
     const int row = 32 * li + 2 * (lane & 15);
     const float r0 = s.h1res[row], r1 = s.h1res[row + 1];
     double s0, s1;
@@ -624,17 +684,17 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     poll_vec_regs(P, ws->xl[xcd][lp & 1], tag_of(lp, T_XL), xv);
     store_pairs(s.xres, xv);
     normed(xv, gd, y);
-    if (wg == 0) {
+    if (lead) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const int e = 2 * (lane + 64 * k);
-        if (a.io[si].out_hidden) *reinterpret_cast<float2*>(a.io[si].out_hidden + e) = make_float2(y[2 * k], y[2 * k + 1]);
-        if (a.io[si].out_residual) {
+        if (SIO(out_hidden)) *reinterpret_cast<float2*>(SIO(out_hidden) + e) = make_float2(y[2 * k], y[2 * k + 1]);
+        if (SIO(out_residual)) {
           if constexpr (BB)
-            reinterpret_cast<uint32_t*>(a.io[si].out_residual)[e >> 1] =
+            reinterpret_cast<uint32_t*>(SIO(out_residual))[e >> 1] =
                 (uint32_t)f2bf(xv[2 * k]) | ((uint32_t)f2bf(xv[2 * k + 1]) << 16);
           else
-            *reinterpret_cast<float2*>(reinterpret_cast<float*>(a.io[si].out_residual) + e) = make_float2(xv[2 * k], xv[2 * k + 1]);
+            *reinterpret_cast<float2*>(reinterpret_cast<float*>(SIO(out_residual)) + e) = make_float2(xv[2 * k], xv[2 * k + 1]);
         }
       }
     }
@@ -674,16 +734,16 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     if constexpr (BB) { kl = rbf(kl); kh = rbf(kh); vl = rbf(vl); vh = rbf(vh); }
     s.knew[c] = kl; s.knew[c + 64] = kh;
     s.vnew[c] = vl; s.vnew[c + 64] = vh;
-    if (li == C - 1) {
+    if (C - 1 >= li && C - 1 < li + NSUB) {
       const size_t off = (((size_t)layer * NKVH + xcd) * (size_t)a.max_seq + pos) * HDIM + c;
       if constexpr (BB) {
-        bf16_t* kc = reinterpret_cast<bf16_t*>(a.io[si].kc) + off;
-        bf16_t* vc = reinterpret_cast<bf16_t*>(a.io[si].vc) + off;
+        bf16_t* kc = reinterpret_cast<bf16_t*>(SIO(kc)) + off;
+        bf16_t* vc = reinterpret_cast<bf16_t*>(SIO(vc)) + off;
         gput(kc, f2bf(kl)); gput(kc + 64, f2bf(kh));
         gput(vc, f2bf(vl)); gput(vc + 64, f2bf(vh));
       } else {
-        float* kc = reinterpret_cast<float*>(a.io[si].kc) + off;
-        float* vc = reinterpret_cast<float*>(a.io[si].vc) + off;
+        float* kc = reinterpret_cast<float*>(SIO(kc)) + off;
+        float* vc = reinterpret_cast<float*>(SIO(vc)) + off;
         gput(kc, kl); gput(kc + 64, kh);
         gput(vc, vl); gput(vc + 64, vh);
       }
@@ -718,18 +778,37 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     if (c == 0) s.wts[h][MAXC] = 1.0 / Z;
   };
   // ---- poller: AR1 (O partials + residual) -> h1 slots; then h1 -> h1res, hn
-  auto prep_gu = [&](int lp, int layer) {
+  auto prep_gu = [&](int lp, int layer) QTTS_INLINE {
     const int par = lp & 1;
-    const int row = 32 * li + 2 * (lane & 15);
-    const float r0 = s.xres[row], r1 = s.xres[row + 1];
-    double s0, s1;
-    poll_sum8(P, ws->opart[par], 32 * li, tag_of(lp, T_OPART), s0, s1);
-    if (kv_pending) {
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");   // the KV entry written in prep_att
-      kv_pending = false;
-    }
     // h1 = x + the sum of the 8 XCD partials, in f64
-    if (lane < 16) pub_local2(&ws->h1[xcd][par][row], (float)((double)r0 + s0), (float)((double)r1 + s1), tag_of(lp, T_H1));
+    if constexpr (XL) {
+      double sm[4];
+      float r[4];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        r[2 * k] = s.xres[32 * li + 2 * (lane + 64 * k)];
+        r[2 * k + 1] = s.xres[32 * li + 2 * (lane + 64 * k) + 1];
+      }
+      poll_sum8_rows(P, ws->opart[par], 32 * li, tag_of(lp, T_OPART), sm);
+      if (kv_pending) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");   // the KV entry written in prep_att
+        kv_pending = false;
+      }
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        pub_local2(&ws->h1[xcd][par][32 * li + 2 * (lane + 64 * k)], (float)((double)r[2 * k] + sm[2 * k]),
+                   (float)((double)r[2 * k + 1] + sm[2 * k + 1]), tag_of(lp, T_H1));
+    } else {
+      const int row = 32 * li + 2 * (lane & 15);
+      const float r0 = s.xres[row], r1 = s.xres[row + 1];
+      double s0, s1;
+      poll_sum8(P, ws->opart[par], 32 * li, tag_of(lp, T_OPART), s0, s1);
+      if (kv_pending) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");   // the KV entry written in prep_att
+        kv_pending = false;
+      }
+      if (lane < 16) pub_local2(&ws->h1[xcd][par][row], (float)((double)r0 + s0), (float)((double)r1 + s1), tag_of(lp, T_H1));
+    }
     float xv[16], y[16];
     double gd[16];
     gains_d(g_post, gd);
@@ -773,7 +852,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     }
     for (int sb = 0; sb < nsb; ++sb) {
       const int b0 = c0 + sb * SUB;
-      if (sb > 0) load_kv<BB>(tk, a, si, layer, xcd, b0, c1 < Lold ? c1 : Lold, mw, lane);
+      if (sb > 0) load_kv<BB>(tk, a, SIO(kc), SIO(vc), layer, xcd, b0, c1 < Lold ? c1 : Lold, mw, lane);
       double sc[NH * JJ];
 #pragma unroll
       for (int jj = 0; jj < JJ; ++jj) {
@@ -960,7 +1039,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) { xv[i] = x[8 * lane + i]; xv[8 + i] = x[512 + 8 * lane + i]; }
   };
-  auto math_qkv = [&](int lp) {
+  auto math_qkv = [&](int lp, int lg, const TileQKV& tq) {
     double xv[16];
     load_x16(s.xn, xv);
     const uint32_t tg = tag_of(lp, T_QKV);
@@ -970,13 +1049,13 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     const double t = rs_sum<5, 4>(v, lane);   // row lane >> 4 in lanes 0, 16, 32, 48
     // slot order pairs the rotate_half partners: channel c' of head h goes to slot
     // 128 h + 2 (c' mod 64) + c' / 64, so one 16-byte pair holds channels c and c + 64
-    const int lr = 16 * li + 4 * mw + (lane >> 4), cc = lr & 127;
+    const int lr = 16 * lg + 4 * mw + (lane >> 4), cc = lr & 127;
     if ((lane & 15) == 0) pub_local(&ws->qkv[xcd][lp & 1][(lr & ~127) + 2 * (cc & 63) + (cc >> 6)], (float)t, tg);
   };
-  auto math_o = [&](int lp, bool merged) {
-    // chunked attention: merge, one column per thread: f32((sum_c acc_c w_c) * (1 / Z)); chunks
-    // c >= C carry weight 0 (their partials are finite: zero-initialised or older)
-    if (!merged) {
+  // chunked attention: merge, one column per thread: f32((sum_c acc_c w_c) * (1 / Z)); chunks
+  // c >= C carry weight 0 (their partials are finite: zero-initialised or older)
+  auto merge_attn = [&]() {
+    {
       const int t = threadIdx.x, hh = t >> 7;
       float pv[MAXC];
 #pragma unroll
@@ -987,6 +1066,8 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       s.attn[t] = (float)(acc * s.wts[hh][MAXC]);
       step_barrier();
     }
+  };
+  auto math_o = [&](int lp, int lg, const TileO& to) {
     const int col = 8 * (lane & 31);
     double xv[8];
 #pragma unroll
@@ -998,9 +1079,9 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     // per half-wave: row pair j = (lane >> 3) & 3 ends in lanes 0, 8, 16, 24 (+32)
     const double t = rs_sum<4, 4>(v, lane);
     if ((lane & 7) == 0)
-      pub_cross(&ws->opart[lp & 1][xcd][32 * li + 8 * mw + 2 * ((lane >> 3) & 3) + (lane >> 5)], (float)t, tg);
+      pub_cross(&ws->opart[lp & 1][xcd][32 * lg + 8 * mw + 2 * ((lane >> 3) & 3) + (lane >> 5)], (float)t, tg);
   };
-  auto math_gu = [&](int lp) {
+  auto math_gu = [&](int lp, int lg, const TileGU& tgu) {
     double xv[16];
     load_x16(s.hn, xv);
     const uint32_t tg = tag_of(lp, T_INTER);
@@ -1014,10 +1095,10 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     const int r = lane >> 4;
     if ((lane & 15) == 0 && r < 3) {
       const double act = t.a / (1.0 + exp(-t.a)) * t.b;
-      pub_local(&ws->inter[xcd][lp & 1][12 * li + 3 * mw + r], (float)act, tg);
+      pub_local(&ws->inter[xcd][lp & 1][12 * lg + 3 * mw + r], (float)act, tg);
     }
   };
-  auto math_down = [&](int lp) {
+  auto math_down = [&](int lp, int lg, const TileD& td) {
     double xv[24];
 #pragma unroll
     for (int j = 0; j < 3; ++j)
@@ -1034,17 +1115,20 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     // per 16-lane group: row set g = (lane >> 3) & 1 ends in lanes 0 and 8
     const double t = rs_sum<3, 2>(v, lane);
     if ((lane & 7) == 0)
-      pub_cross(&ws->dpart[lp & 1][xcd][32 * li + 8 * mw + 4 * ((lane >> 3) & 1) + (lane >> 4)], (float)t, tg);
+      pub_cross(&ws->dpart[lp & 1][xcd][32 * lg + 8 * mw + 4 * ((lane >> 3) & 1) + (lane >> 4)], (float)t, tg);
   };
-  // head rows of this workgroup: backbone codec head 12 rows (3 per wave), CP head 8 (2 per wave)
-  auto head_rows = [&](int& row0, int& nrows) {
+  // head rows of a workgroup (of its row group sub in XL): backbone codec head 12 rows (3 per
+  // wave), CP head 8 (2 per wave)
+  auto head_rows = [&](int sub, int& row0, int& nrows) {
     const int per_wg = (a.cp_frame ? a.cp_vocab : a.vocab) / NWG;
     nrows = per_wg / NMATH;
-    row0 = wg * per_wg + mw * nrows;
+    row0 = (XL ? 8 * li_hw + sub : wg) * per_wg + mw * nrows;
   };
-  auto math_head = [&](int pi) {
+  // head logits of row group sub from tile tq: greedy code-predictor heads fold them into the
+  // wave's best (bv, bi) (larger value, lowest id on ties); the other heads publish them
+  auto head_group = [&](int pi, int sub, const TileQKV& tq, float& bv, int& bi) {
     int row0, nrows;
-    head_rows(row0, nrows);
+    head_rows(sub, row0, nrows);
     double xv[16];
     load_x16(s.hb, xv);
     const uint32_t tg = a.tag_base + TAG_HEAD + (uint32_t)pi;
@@ -1055,25 +1139,30 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     const double t = rs_sum<5, 4>(v, lane);   // row lane >> 4 in lanes 0, 16, 32, 48
     const int r = lane >> 4;
     if (cp_greedy) {
-      // greedy code-predictor head: only the workgroup's best (value, lowest id on ties) is
-      // published; the selecting waves reduce 256 candidates instead of the whole vocabulary
-      float bv = ((lane & 15) == 0 && r < nrows) ? (float)t : -INFINITY;
-      int bi = row0 + r;
-      best_merge(bv, bi, xlane_f<4>(bv), (int)xlane<4>((uint32_t)bi));
-      best_merge(bv, bi, xlane_f<5>(bv), (int)xlane<5>((uint32_t)bi));
-      if (lane == 0) { s.hbv[mw] = bv; s.hbi[mw] = bi; }
-      step_barrier();
-      if (mw == 0 && lane == 0) {
-        float wv = s.hbv[0];
-        int wi = s.hbi[0];
-#pragma unroll
-        for (int w = 1; w < NMATH; ++w) best_merge(wv, wi, s.hbv[w], s.hbi[w]);
-        const u32x4 d = {__float_as_uint(wv), tg, (uint32_t)wi, tg};
-        __builtin_amdgcn_raw_buffer_store_b128(d, P.rs, (int)ws_off(P, &ws->hloc[xcd][pi & 1][2 * li]), 0, 0);
-      }
+      float cv = ((lane & 15) == 0 && r < nrows) ? (float)t : -INFINITY;
+      int ci = row0 + r;
+      best_merge(cv, ci, xlane_f<4>(cv), (int)xlane<4>((uint32_t)ci));
+      best_merge(cv, ci, xlane_f<5>(cv), (int)xlane<5>((uint32_t)ci));
+      best_merge(bv, bi, cv, ci);
     } else if ((lane & 15) == 0 && r < nrows) {
       pub_cross(&ws->logits[pi & 1][row0 + r], (float)t, tg);
-      if (!a.cp_frame && a.io[si].out_logits) a.io[si].out_logits[row0 + r] = (float)t;
+      if (!a.cp_frame && SIO(out_logits)) SIO(out_logits[row0 + r]) = (float)t;
+    }
+  };
+  // greedy code-predictor head: only the workgroup's best (value, lowest id on ties) is published;
+  // the selecting waves reduce the workgroup candidates instead of the whole vocabulary
+  auto head_publish = [&](int pi, float bv, int bi) {
+    if (!cp_greedy) return;
+    const uint32_t tg = a.tag_base + TAG_HEAD + (uint32_t)pi;
+    if (lane == 0) { s.hbv[mw] = bv; s.hbi[mw] = bi; }
+    step_barrier();
+    if (mw == 0 && lane == 0) {
+      float wv = s.hbv[0];
+      int wi = s.hbi[0];
+#pragma unroll
+      for (int w = 1; w < NMATH; ++w) best_merge(wv, wi, s.hbv[w], s.hbi[w]);
+      const u32x4 d = {__float_as_uint(wv), tg, (uint32_t)wi, tg};
+      __builtin_amdgcn_raw_buffer_store_b128(d, P.rs, (int)ws_off(P, &ws->hloc[XL ? 0 : xcd][pi & 1][2 * (XL ? li_hw : li)]), 0, 0);
     }
   };
   auto head_weights = [&](int pi) -> const bf16_t* {
@@ -1088,7 +1177,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       const int par = pi & 1;
       float cv[2];
       {
-        const uint32_t o = ws_off(P, &ws->hloc[xcd][par][0]);
+        const uint32_t o = ws_off(P, &ws->hloc[XL ? 0 : xcd][par][0]);
         poll_regs<1>(P, WPX, tg, cv, [o](int i) { return o + 16u * (uint32_t)i; });
       }
       float bv = lane < WPX ? cv[0] : -INFINITY;
@@ -1105,6 +1194,11 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           default: ov = xlane_f<4>(bv); oi = (int)xlane<4>((uint32_t)bi); break;
         }
         best_merge(bv, bi, ov, oi);
+      }
+      if constexpr (XL) {
+        // one stream per XCD: the XCD's best is the stream's
+        bi = __builtin_amdgcn_readfirstlane(bi);
+        return (bi >= 0 && bi < a.cp_vocab) ? bi : 0;
       }
       // Level 2: this workgroup's copy of the XCD best goes to hx[li][xcd]; the 8 XCD bests are
       // read from the copies of workgroup index li (each cache line has 8 readers).
@@ -1136,7 +1230,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     const int n = a.cp_frame ? a.cp_vocab : a.vocab;
     poll_vec<24>(P, ws->logits[pi & 1], n, a.tag_base + TAG_HEAD + (uint32_t)pi, s.stage);
     SelParams sp = a.sel;
-    sp.seed = a.io[si].seed;
+    sp.seed = SIO(seed);
     if (a.cp_frame) {
       sp.group = pi;   // CP head pi-1 selects codebook group pi
     } else {
@@ -1145,11 +1239,11 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
         for (int i = lane; i < n; i += 64)
           if (i >= n - 1024 && i != a.eos_id) s.stage[i] = -INFINITY;
       // repetition penalty, once per distinct id (generator.py:161-167)
-      if (a.rep_penalty != 1.0f && a.io[si].n_history > 0) {
+      if (a.rep_penalty != 1.0f && SIO(n_history) > 0) {
         for (int i = lane; i < MAXV / 32; i += 64) s.pen_bits[i] = 0u;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        for (int i = lane; i < a.io[si].n_history; i += 64) {
-          const int id = a.io[si].history[i];
+        for (int i = lane; i < SIO(n_history); i += 64) {
+          const int id = SIO(history[i]);
           if (id >= 0 && id < n) atomicOr(&s.pen_bits[id >> 5], 1u << (id & 31));
         }
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
@@ -1183,7 +1277,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   };
   // attention over the whole context in every workgroup when it fits one pass of the math
   // waves (attention and O projection then share a step); split into chunks otherwise
-  auto att_local = [&](int pi) { return a.io[si].pos0 + pi + 1 <= KVGeo<BB>::SUB; };
+  auto att_local = [&](int pi) { return SIO(pos0) + pi + 1 <= KVGeo<BB>::SUB; };
   auto walk = [&](auto&& act) {
     act(S_PRO, 0, 0); stamp();
     step_barrier();
@@ -1201,7 +1295,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   struct PosInfo { int pos, L, C, P, c0, c1; bool local, has_chunk, last_pos, head; };
   auto pinfo = [&](int pi) {
     PosInfo q;
-    q.pos = a.io[si].pos0 + pi;
+    q.pos = SIO(pos0) + pi;
     q.L = q.pos + 1;
     chunking<BB>(q.L, q.C, q.P);
     q.local = att_local(pi);
@@ -1266,25 +1360,25 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           else if (q.head || q.last_pos) { ar2(lp); prep_final(lp); }
           else {
             prep_input0(pi + 1);
-            if (a.cp_frame && wg == 0) comb_add(pi == 0);
+            if (a.cp_frame && lead) comb_add(pi == 0);
           }
           // g_in now serves the layer after next
           if (layer < NL - 1 || !(q.head || q.last_pos)) load_gain_pairs(g_in, lw(LW, (nl + 1) % NL, W_LNIN));
           break;
         case S_HEAD:
           if (cp_greedy) step_barrier();   // joins the math waves' head barrier
-          if (a.cp_frame || wg == 0) {
+          if (a.cp_frame || lead) {
             const int tok = select(pi);
             if (a.cp_frame) {
               if (lane == 0) s.tok[pi - 1] = tok;
               __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
               if (!q.last_pos) {
                 prep_input0(pi + 1);
-                if (wg == 0) comb_add(false);
+                if (lead) comb_add(false);
                 load_gain_pairs(g_in, lw(LW, NL > 1 ? 1 : 0, W_LNIN));
               }
-            } else if (lane == 0 && a.io[si].out_token) {
-              *a.io[si].out_token = tok;
+            } else if (lane == 0 && SIO(out_token)) {
+              *SIO(out_token) = tok;
             }
           }
           break;
@@ -1298,13 +1392,93 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       const bool last_layer = layer == NL - 1;
       // Each tile is loaded one step ahead of its use, right after the step's own compute,
       // so at most the tile in use and the next one are live.
+      // XL: a GEMV stage runs the workgroup's 8 row groups; each group's tile is issued one group
+      // ahead into the second register set (the first group's a step ahead, as in batch 1)
+      auto qkv_stage = [&](int layer_) {
+        if constexpr (XL) {
+          TileQKV t1;
+#pragma unroll 1
+          for (int sub = 0; sub < NSUB; sub += 2) {
+            load_qkv<BB>(t1, LW, layer_, xcd, li + sub + 1, mw, lane);
+            math_qkv(lp, li + sub, tq);
+            if (sub + 2 < NSUB) load_qkv<BB>(tq, LW, layer_, xcd, li + sub + 2, mw, lane);
+            math_qkv(lp, li + sub + 1, t1);
+          }
+        } else {
+          math_qkv(lp, li, tq);
+        }
+      };
+      auto o_stage = [&](int layer_) {
+        if constexpr (XL) {
+          TileO t1;
+#pragma unroll 1
+          for (int sub = 0; sub < NSUB; sub += 2) {
+            load_o<BB>(t1, LW, layer_, xcd, li + sub + 1, mw, lane);
+            math_o(lp, li + sub, to);
+            if (sub + 2 < NSUB) load_o<BB>(to, LW, layer_, xcd, li + sub + 2, mw, lane);
+            math_o(lp, li + sub + 1, t1);
+          }
+        } else {
+          math_o(lp, li, to);
+        }
+      };
+      auto gu_stage = [&](int layer_) {
+        if constexpr (XL) {
+          TileGU t1;
+#pragma unroll 1
+          for (int sub = 0; sub < NSUB; sub += 2) {
+            load_gu<BB>(t1, LW, layer_, xcd, li + sub + 1, mw, lane);
+            math_gu(lp, li + sub, tgu);
+            if (sub + 2 < NSUB) load_gu<BB>(tgu, LW, layer_, xcd, li + sub + 2, mw, lane);
+            math_gu(lp, li + sub + 1, t1);
+          }
+        } else {
+          math_gu(lp, li, tgu);
+        }
+      };
+      auto down_stage = [&](int layer_) {
+        if constexpr (XL) {
+          TileD t1;
+#pragma unroll 1
+          for (int sub = 0; sub < NSUB; sub += 2) {
+            load_d<BB>(t1, LW, layer_, xcd, li + sub + 1, mw, lane);
+            math_down(lp, li + sub, td);
+            if (sub + 2 < NSUB) load_d<BB>(td, LW, layer_, xcd, li + sub + 2, mw, lane);
+            math_down(lp, li + sub + 1, t1);
+          }
+        } else {
+          math_down(lp, li, td);
+        }
+      };
+      auto head_stage = [&]() {
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+        if constexpr (XL) {
+          TileQKV t1;
+          int row0, nrows;
+#pragma unroll 1
+          for (int sub = 0; sub < NSUB; sub += 2) {
+            head_rows(sub + 1, row0, nrows);
+            load_head<BB>(t1, head_weights(pi), row0, nrows, lane);
+            head_group(pi, sub, tq, bv, bi);
+            if (sub + 2 < NSUB) {
+              head_rows(sub + 2, row0, nrows);
+              load_head<BB>(tq, head_weights(pi), row0, nrows, lane);
+            }
+            head_group(pi, sub + 1, t1, bv, bi);
+          }
+        } else {
+          head_group(pi, 0, tq, bv, bi);
+        }
+        head_publish(pi, bv, bi);
+      };
       switch (st) {
         case S_PRO:
           load_qkv<BB>(tq, LW, 0, xcd, li, mw, lane);
           break;
         case S_QKV:
-          math_qkv(lp);
-          if (q.has_chunk) load_kv<BB>(tk, a, si, layer, xcd, q.c0, min(q.c1, q.L - 1), mw, lane);
+          qkv_stage(layer);
+          if (q.has_chunk) load_kv<BB>(tk, a, SIO(kc), SIO(vc), layer, xcd, q.c0, min(q.c1, q.L - 1), mw, lane);
           else tk = TileKV<BB>{};
           if (q.local) load_o<BB>(to, LW, layer, xcd, li, mw, lane);
           break;
@@ -1317,27 +1491,28 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
             else attention(std::integral_constant<int, 1>{}, lp, layer, q.L, q.c0, q.c1, false, li & 1);
           }
           if (q.local) {
-            math_o(lp, true);
+            o_stage(layer);
             load_gu<BB>(tgu, LW, layer, xcd, li, mw, lane);
           } else {
             load_o<BB>(to, LW, layer, xcd, li, mw, lane);
           }
           break;
         case S_O:
-          math_o(lp, false);
+          merge_attn();
+          o_stage(layer);
           load_gu<BB>(tgu, LW, layer, xcd, li, mw, lane);
           break;
         case S_GU:
-          math_gu(lp);
+          gu_stage(layer);
           load_d<BB>(td, LW, layer, xcd, li, mw, lane);
           break;
         case S_DOWN:
-          math_down(lp);
+          down_stage(layer);
           if (!last_layer) {
             load_qkv<BB>(tq, LW, layer + 1, xcd, li, mw, lane);
           } else if (q.head) {
             int row0, nrows;
-            head_rows(row0, nrows);
+            head_rows(0, row0, nrows);
             load_head<BB>(tq, head_weights(pi), row0, nrows, lane);
           } else if (!q.last_pos) {
             load_qkv<BB>(tq, LW, 0, xcd, li, mw, lane);
@@ -1346,7 +1521,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           }
           break;
         case S_HEAD:
-          math_head(pi);
+          head_stage();
           if (!q.last_pos) load_qkv<BB>(tq, LW, 0, xcd, li, mw, lane);
           else tq = TileQKV{};
           break;
@@ -1355,11 +1530,11 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   }
 
   // ---- code-predictor frame epilogue: tokens and the bf16 embedding combine
-  if (a.cp_frame && wg == 0 && poller) {
+  if (a.cp_frame && lead && poller) {
     if (lane == 0) {
-      if (a.io[si].hist_slot) *a.io[si].hist_slot = g0;
-      a.io[si].out_tokens[0] = g0;
-      for (int g = 0; g < a.n_groups; ++g) a.io[si].out_tokens[1 + g] = s.tok[g];
+      if (SIO(hist_slot)) *SIO(hist_slot) = g0;
+      SIO(out_tokens[0]) = g0;
+      for (int g = 0; g < a.n_groups; ++g) SIO(out_tokens[1 + g]) = s.tok[g];
     }
     // s.comb holds emb_bb[g0] + emb_0[t_0] + ... + emb_{n-2}[t_{n-2}] (each row was loaded as a
     // position's input); the last group's row and the text row complete it (generator.py:356-362)
@@ -1368,8 +1543,8 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     uint32_t wl[8], wt[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) wl[k] = lr[lane + 64 * k];
-    if (a.io[si].text_row) {
-      const auto* tr = gmem(reinterpret_cast<const uint32_t*>(a.io[si].text_row));
+    if (SIO(text_row)) {
+      const auto* tr = gmem(reinterpret_cast<const uint32_t*>(SIO(text_row)));
 #pragma unroll
       for (int k = 0; k < 8; ++k) wt[k] = tr[lane + 64 * k];
     }
@@ -1377,14 +1552,17 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     for (int k = 0; k < 8; ++k) {
       const int e = 2 * (lane + 64 * k);
       float a0 = rbf(s.comb[e] + bflo(wl[k])), a1 = rbf(s.comb[e + 1] + bfhi(wl[k]));
-      if (a.io[si].text_row) { a0 = rbf(a0 + bflo(wt[k])); a1 = rbf(a1 + bfhi(wt[k])); }
-      gput(reinterpret_cast<uint32_t*>(a.io[si].out_combined) + (e >> 1), (uint32_t)f2bf(a0) | ((uint32_t)f2bf(a1) << 16));
+      if (SIO(text_row)) { a0 = rbf(a0 + bflo(wt[k])); a1 = rbf(a1 + bfhi(wt[k])); }
+      gput(reinterpret_cast<uint32_t*>(SIO(out_combined)) + (e >> 1), (uint32_t)f2bf(a0) | ((uint32_t)f2bf(a1) << 16));
     }
   }
 }
 
-template __global__ void qtts_decode_kernel<true>(const KArgs a);
-template __global__ void qtts_decode_kernel<false>(const KArgs a);
+#undef SIO
+
+template __global__ void qtts_decode_kernel<true, false>(const KArgs a);
+template __global__ void qtts_decode_kernel<false, false>(const KArgs a);
+template __global__ void qtts_decode_kernel<false, true>(const KArgs a);
 
 }  // namespace qtts
 
@@ -1429,9 +1607,11 @@ hipError_t check_device(int device) {
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0 || prop.multiProcessorCount != qtts::NWG || !prop.cooperativeLaunch)
     return dc.status = hipErrorInvalidDevice;
   int occ = 0;
-  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)qtts::qtts_decode_kernel<true>, qtts::NTHR, 0);
+  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)qtts::qtts_decode_kernel<true, false>, qtts::NTHR, 0);
   if (e != hipSuccess || occ < 1) return dc.status = (e != hipSuccess ? e : hipErrorInvalidDevice);
-  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)qtts::qtts_decode_kernel<false>, qtts::NTHR, 0);
+  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)qtts::qtts_decode_kernel<false, false>, qtts::NTHR, 0);
+  if (e != hipSuccess || occ < 1) return dc.status = (e != hipSuccess ? e : hipErrorInvalidDevice);
+  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)qtts::qtts_decode_kernel<false, true>, qtts::NTHR, 0);
   if (e != hipSuccess || occ < 1) return dc.status = (e != hipSuccess ? e : hipErrorInvalidDevice);
   int* d = nullptr;
   if ((e = hipMalloc(&d, qtts::NWG * sizeof(int))) != hipSuccess) return dc.status = e;
@@ -1452,12 +1632,12 @@ hipError_t check_device(int device) {
   return dc.status = hipSuccess;
 }
 
-uint32_t next_tag_base(void* ws, hipStream_t stream, hipError_t* err) {
+uint32_t next_tag_base(void* ws, size_t bytes, hipStream_t stream, hipError_t* err) {
   std::lock_guard<std::mutex> lk(g_mu);
   uint32_t& seq = g_seq[ws];
   if (seq == 0 || seq >= (1u << 20) - 1u) {
     // first use (or tag wrap): clear every exchange slot with a fill kernel
-    const size_t n16 = sizeof(Workspace) / 16;
+    const size_t n16 = bytes / 16;
     hipLaunchKernelGGL(zero_kernel, dim3(256), dim3(256), 0, stream, reinterpret_cast<uint4*>(ws), n16);
     *err = hipGetLastError();
     seq = 1;
@@ -1465,7 +1645,8 @@ uint32_t next_tag_base(void* ws, hipStream_t stream, hipError_t* err) {
   return (seq++) << 12;
 }
 
-hipError_t launch(bool bb, KArgs& a, hipStream_t stream) {
+// xl: one stream per XCD, n_streams workspaces of one block starting at a.io[0].ws
+hipError_t launch(bool bb, KArgs& a, hipStream_t stream, bool xl = false, int n_streams = 1) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
@@ -1473,12 +1654,13 @@ hipError_t launch(bool bb, KArgs& a, hipStream_t stream) {
   if (a.num_layers < 1 || a.n_pos < 1 || a.num_layers * a.n_pos > qtts::MAX_LAYER_PASSES) return hipErrorInvalidValue;
   if (a.io[0].pos0 < 0 || a.io[0].pos0 + a.n_pos > a.max_seq) return hipErrorInvalidValue;
   hipError_t ze = hipSuccess;
-  a.tag_base = next_tag_base(a.io[0].ws, stream, &ze);
+  a.tag_base = next_tag_base(a.io[0].ws, (size_t)n_streams * sizeof(Workspace), stream, &ze);
   if (ze != hipSuccess) return ze;
   a.spin_cap = kSpinCap;
   a.trace = g_trace;
   void* args[] = {&a};
-  const void* fn = bb ? (const void*)qtts::qtts_decode_kernel<true> : (const void*)qtts::qtts_decode_kernel<false>;
+  const void* fn = bb ? (const void*)qtts::qtts_decode_kernel<true, false>
+                      : (xl ? (const void*)qtts::qtts_decode_kernel<false, true> : (const void*)qtts::qtts_decode_kernel<false, false>);
   return hipLaunchCooperativeKernel(fn, dim3(qtts::NWG), dim3(qtts::NTHR), args, 0, stream);
 }
 
@@ -1708,6 +1890,55 @@ hipError_t qtts_cp_frame(void* workspace, const CPLayerWeights* layer_weights, i
   }
   a.sel.frame_step = frame_step;
   return launch(false, a, stream);
+}
+
+hipError_t qtts_cp_frame_streams(int n_streams, void* workspaces, const CPLayerWeights* layer_weights, int num_layers,
+                                 const void* final_norm_weight, const void* cos_table, const void* sin_table,
+                                 void* k_caches, void* v_caches, int max_seq_len, const float* bb_hidden, const int* g0,
+                                 const void* bb_embedding, const void* const* lm_heads, const void* const* cp_embeddings,
+                                 int n_groups, int cp_vocab, const void* text_rows, int* out_tokens, void* out_combined,
+                                 int eos_id, int* done, const QttsSampling* sampling, int frame_step, hipStream_t stream) {
+  if (n_streams < 1 || n_streams > qtts::NSTREAM) return hipErrorInvalidValue;
+  if (workspaces == nullptr || (reinterpret_cast<uintptr_t>(workspaces) & 255u) != 0 || k_caches == nullptr ||
+      v_caches == nullptr || bb_hidden == nullptr || g0 == nullptr || bb_embedding == nullptr || lm_heads == nullptr ||
+      cp_embeddings == nullptr || out_tokens == nullptr || out_combined == nullptr || done == nullptr)
+    return hipErrorInvalidValue;
+  // every position of the frame within one attention pass (the local path)
+  if (n_groups < 1 || n_groups + 1 > qtts::KVGeo<false>::SUB || n_groups + 1 > max_seq_len) return hipErrorInvalidValue;
+  if (cp_vocab <= 0 || cp_vocab > qtts::MAXV || cp_vocab % (qtts::NWG * qtts::NMATH) != 0) return hipErrorInvalidValue;
+  KArgs a;
+  base_args(a, layer_weights, num_layers, final_norm_weight, cos_table, sin_table, nullptr, nullptr, max_seq_len);
+  a.n_pos = n_groups + 1;
+  a.cp_frame = 1;
+  a.bb_emb = reinterpret_cast<const qtts::bf16_t*>(bb_embedding);
+  a.cp_heads = reinterpret_cast<const qtts::bf16_t* const*>(lm_heads);
+  a.cp_embs = reinterpret_cast<const qtts::bf16_t* const*>(cp_embeddings);
+  a.n_groups = n_groups;
+  a.cp_vocab = cp_vocab;
+  a.eos_id = eos_id;
+  if (sampling) {
+    a.sel.do_sample = sampling->do_sample;
+    a.sel.temperature = sampling->temperature;
+    a.sel.top_k = sampling->top_k;
+    a.sel.top_p = sampling->top_p;
+  }
+  a.sel.frame_step = frame_step;
+  const size_t kv = (size_t)num_layers * qtts::NKVH * (size_t)max_seq_len * qtts::HDIM;   // floats per stream
+  for (int st = 0; st < n_streams; ++st) {
+    qtts::StreamIO& io = a.io[st];
+    io.ws = reinterpret_cast<Workspace*>(workspaces) + st;
+    io.kc = reinterpret_cast<float*>(k_caches) + kv * st;
+    io.vc = reinterpret_cast<float*>(v_caches) + kv * st;
+    io.pos0 = 0;
+    io.bb_hidden = bb_hidden + (size_t)qtts::HID * st;
+    io.g0 = g0 + st;
+    io.text_row = text_rows ? reinterpret_cast<const qtts::bf16_t*>(text_rows) + (size_t)qtts::HID * st : nullptr;
+    io.out_tokens = out_tokens + (size_t)(n_groups + 1) * st;
+    io.out_combined = reinterpret_cast<qtts::bf16_t*>(out_combined) + (size_t)qtts::HID * st;
+    io.done = done + st;
+    io.seed = sampling ? sampling->seed + (uint64_t)st : 0;
+  }
+  return launch(false, a, stream, true, n_streams);
 }
 
 }  // extern "C"
