@@ -182,6 +182,35 @@ hipError_t qtts_cp_frame(
     const void* text_row, int* out_tokens, void* out_combined, int* g0_history_slot,
     int eos_id, int* done, const QttsSampling* sampling, int frame_step, hipStream_t stream);
 
+/* One stream of qtts_backbone_step_streams (host memory; device pointers inside). */
+typedef struct QttsBackboneStream {
+    void* k_cache;                /* bf16 [num_layers, 8, max_seq_len, 128] of this stream */
+    void* v_cache;
+    int position;                 /* cache slot written; attention covers slots 0..position */
+    int pos3[3];                  /* rotary (t, h, w) */
+    const void* input_embedding;  /* bf16 [1024] */
+    float* out_hidden;            /* f32 [1024] final-norm hidden, or NULL */
+    void* out_residual;           /* bf16 [1024] pre-norm residual, or NULL */
+    float* out_logits;            /* f32 [vocab], or NULL */
+    int* out_token;               /* int32 [1] selected group-0 token, or NULL */
+    const int* history;           /* int32 [n_history] previously generated group-0 tokens */
+    int n_history;
+    unsigned long long seed;      /* sampler key */
+} QttsBackboneStream;
+
+/* Backbone steps (codec head + selection as in qtts_backbone_step) of n_streams (1..8) independent
+ * streams in one launch; no counterpart in the reference, whose decode is batch 1
+ * (fused_decode_tts.cu:728-831). Stream s runs on XCD s alone (its 32 workgroups, every exchange in
+ * that XCD's L2) with its own KV cache, position and length, and computes exactly what
+ * qtts_backbone_step computes for it. workspaces: n_streams x qtts_workspace_bytes(), 256-byte
+ * aligned, zero-filled before first use. */
+hipError_t qtts_backbone_step_streams(
+    int n_streams, void* workspaces, const TTSLayerWeights* layer_weights, int num_layers,
+    const void* final_norm_weight, const void* cos_table, const void* sin_table, int max_seq_len,
+    const QttsBackboneStream* streams, const void* codec_head, int vocab, int mask_tail,
+    float repetition_penalty, int eos_id, int suppress_eos, const QttsSampling* sampling,
+    int frame_step, hipStream_t stream);
+
 /* Code-predictor frames of n_streams (1..8) independent streams in one launch; no counterpart in the
  * reference, whose decode is batch 1 (fused_decode_code_predictor.cu:565-668 runs one stream). Stream s
  * runs on XCD s alone (its 32 workgroups, every exchange in that XCD's L2) and computes exactly what

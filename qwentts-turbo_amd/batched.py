@@ -1,10 +1,10 @@
 """Decode of several independent streams (batch 8, ragged KV lengths).
 
 Each stream keeps its own backbone KV cache and position; all streams share one copy of the
-weights and one code-predictor decoder. A frame of the batch is one backbone step per stream
-(codec head + selection, a batch-1 launch each) and one launch for the code-predictor frames of
-up to 8 streams: stream s runs on XCD s alone, its 32 workgroups acting as the 8 virtual XCDs
-of the batch-1 decomposition, so every exchange stays in that XCD's L2. Everything is queued on
+weights and one code-predictor decoder. A frame of the batch is two launches per 8 streams: the
+backbone steps (codec head + selection) and the code-predictor frames. In both, stream s runs
+on XCD s alone, its 32 workgroups acting as the 8 virtual XCDs of the batch-1 decomposition,
+so every exchange stays in that XCD's L2. Everything is queued on
 the current stream with no host sync, and every stream's results are bit-identical to its
 batch-1 results.
 
@@ -23,14 +23,16 @@ from .megakernel_code_predictor import CodePredictorMegakernelGenerator
 class BatchedTTSDecoder:
     """``n_streams`` backbone decoders over shared weights plus one code predictor."""
 
-    MAX_PER_LAUNCH = 8   # code-predictor frames per launch: one stream per XCD
+    MAX_PER_LAUNCH = 8   # streams per launch: one per XCD
 
     def __init__(self, model, n_streams: int, max_seq_len: int = 4096, cp_max_seq_len: int = 32,
                  device="cuda"):
         if n_streams < 1:
             raise ValueError("n_streams must be >= 1")
-        self.streams: List[TTSMegakernelGenerator] = [
-            TTSMegakernelGenerator(model=model, max_seq_len=max_seq_len, device=device) for _ in range(n_streams)]
+        first = TTSMegakernelGenerator(model=model, max_seq_len=max_seq_len, device=device)
+        self.streams: List[TTSMegakernelGenerator] = [first] + [
+            TTSMegakernelGenerator(max_seq_len=max_seq_len, device=device, shared_weights=first.weights)
+            for _ in range(n_streams - 1)]
         self.cp = CodePredictorMegakernelGenerator(model=model, max_seq_len=cp_max_seq_len, device=device)
         self.n_streams = n_streams
         self.device = torch.device(device)
@@ -51,23 +53,25 @@ class BatchedTTSDecoder:
                     temperature: float = 0.9, top_k: int = 50, top_p: float = 1.0, seed: int = 0,
                     frame_step: int = 0) -> torch.Tensor:
         """One backbone step per stream at its own position, codec head, suppress mask (ids
-        [V-1024, V) except EOS), optional repetition penalty and selection of each stream's
-        group-0 token into ``tokens_out[s]`` (device int32). Returns the final-norm hiddens
-        (f32 [n_streams, 1024], device)."""
+        [V-1024, V) except EOS), optional repetition penalty over ``history[s][:n_history[s]]``
+        and selection of each stream's group-0 token into ``tokens_out[s]`` (device int32), with
+        sampling key ``seed + s``. Up to 8 streams share one launch, stream s on XCD s
+        (``decode_steps_streams``). Returns the final-norm hiddens (f32 [n_streams, 1024], device)."""
         if embeds.shape != (self.n_streams, 1024):
             raise ValueError(f"embeds must be [{self.n_streams}, 1024], got {tuple(embeds.shape)}")
         if tokens_out.dtype != torch.int32 or tokens_out.numel() < self.n_streams:
             raise ValueError("tokens_out must be a device int32 tensor with one entry per stream")
-        emb = embeds.to(self.device, torch.bfloat16)
-        empty = torch.zeros(1, dtype=torch.int32, device=self.device)
+        emb = embeds.to(self.device, torch.bfloat16).contiguous()
+        hist = history.to(self.device, torch.int32).contiguous() if history is not None else None
+        nh = [int(x) for x in n_history] if n_history else [0] * self.n_streams
         hidden = torch.empty(self.n_streams, 1024, dtype=torch.float32, device=self.device)
-        for s, dec in enumerate(self.streams):
-            hist = history[s] if history is not None else empty
-            nh = int(n_history[s]) if n_history else 0
-            dec.decoder.decode_step_select(emb[s], tokens_out[s:s + 1], hist, nh, float(repetition_penalty),
-                                           int(eos_id), bool(suppress_eos), bool(do_sample), float(temperature),
-                                           int(top_k), float(top_p), int(seed) + s, int(frame_step))
-            hidden[s].copy_(dec.decoder.hidden_state_buffer())
+        lead = self.streams[0].decoder
+        for b in range(0, self.n_streams, self.MAX_PER_LAUNCH):
+            e = min(self.n_streams, b + self.MAX_PER_LAUNCH)
+            lead.decode_steps_streams([d.decoder for d in self.streams[b:e]], emb[b:e], tokens_out[b:e],
+                                      hidden[b:e], hist[b:e] if hist is not None else None, nh[b:e],
+                                      float(repetition_penalty), int(eos_id), bool(suppress_eos), bool(do_sample),
+                                      float(temperature), int(top_k), float(top_p), int(seed) + b, int(frame_step))
         return hidden
 
     def cp_frames(self, hidden: torch.Tensor, g0: torch.Tensor, text_rows: Optional[torch.Tensor],
@@ -92,5 +96,6 @@ class BatchedTTSDecoder:
     def check_error(self):
         for dec in self.streams:
             dec.check_error()
+        self.streams[0].decoder.check_error_streams()
         self.cp.check_error()
         self.cp.decoder.check_error_streams()

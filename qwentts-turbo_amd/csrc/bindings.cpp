@@ -180,6 +180,88 @@ class MegakernelTTSDecoder {
         sampling(do_sample, temperature, top_k, top_p, seed), (int)frame_step, false, out_token.data_ptr<int>(), skip);
   }
 
+  // Extended: decode_step_select for up to 8 independent decoders `decs` (sharing this decoder's
+  // weights) in one launch, decoder s on XCD s, each at its own position with its own KV cache.
+  // out_tokens[s] gets stream s's token and hidden_out[s] (f32 [n, 1024]) its final-norm hidden;
+  // the residual and logits go to each decoder's own buffers. Stream s samples with key seed + s
+  // and applies the repetition penalty over history[s][0 : n_history[s]]. Each position advances
+  // by one. The launch uses this decoder's block of per-stream workspaces.
+  void decode_steps_streams(std::vector<MegakernelTTSDecoder*> decs, torch::Tensor embeds, torch::Tensor out_tokens,
+                            torch::Tensor hidden_out, c10::optional<torch::Tensor> history, std::vector<int64_t> n_history,
+                            double repetition_penalty, int64_t eos_id, bool suppress_eos, bool do_sample,
+                            double temperature, int64_t top_k, double top_p, int64_t seed, int64_t frame_step) {
+    const int64_t n = (int64_t)decs.size();
+    TORCH_CHECK(n >= 1 && n <= kMaxStreams, "decode_steps_streams takes 1..", kMaxStreams, " decoders, got ", n);
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(dev_);
+    check_bf16(embeds, {n, kHidden}, "embeds");
+    TORCH_CHECK(embeds.device() == dev_, "embeds must be on ", dev_);
+    TORCH_CHECK(out_tokens.is_cuda() && out_tokens.scalar_type() == torch::kInt32 && out_tokens.is_contiguous() &&
+                    out_tokens.numel() >= n, "out_tokens must be a contiguous int32 GPU tensor with >= ", n, " entries");
+    TORCH_CHECK(hidden_out.is_cuda() && hidden_out.scalar_type() == torch::kFloat32 && hidden_out.is_contiguous() &&
+                    hidden_out.sizes() == torch::IntArrayRef({n, kHidden}), "hidden_out must be a contiguous f32 [", n, ", 1024] GPU tensor");
+    TORCH_CHECK(n_history.empty() || (int64_t)n_history.size() == n, "n_history needs one entry per decoder");
+    int64_t hist_stride = 0;
+    if (history.has_value()) {
+      TORCH_CHECK(history->is_cuda() && history->scalar_type() == torch::kInt32 && history->is_contiguous() &&
+                      history->dim() == 2 && history->size(0) >= n, "history must be a contiguous int32 [n, H] GPU tensor");
+      hist_stride = history->size(1);
+    }
+    std::vector<QttsBackboneStream> io(n);
+    for (int64_t st = 0; st < n; ++st) {
+      MegakernelTTSDecoder* d = decs[st];
+      TORCH_CHECK(d != nullptr, "decoder ", st, " is None");
+      TORCH_CHECK(d->dev_ == dev_ && d->num_layers_ == num_layers_ && d->max_seq_len_ == max_seq_len_ &&
+                      d->layer_weights_tensors_.size() == layer_weights_tensors_.size() &&
+                      d->codec_head_weight_.data_ptr() == codec_head_weight_.data_ptr() &&
+                      d->final_norm_weight_.data_ptr() == final_norm_weight_.data_ptr() &&
+                      d->cos_table_.data_ptr() == cos_table_.data_ptr() && d->sin_table_.data_ptr() == sin_table_.data_ptr(),
+                  "decoder ", st, " does not share this decoder's weights");
+      for (size_t j = 0; j < layer_weights_tensors_.size(); ++j)
+        TORCH_CHECK(d->layer_weights_tensors_[j].data_ptr() == layer_weights_tensors_[j].data_ptr(),
+                    "decoder ", st, " does not share this decoder's layer weights");
+      for (int64_t o = 0; o < st; ++o) TORCH_CHECK(decs[o] != d, "decoder ", st, " appears twice");
+      TORCH_CHECK(d->position_ < max_seq_len_, "decoder ", st, ": position ", d->position_, " >= max_seq_len ",
+                  max_seq_len_, " (KV cache full)");
+      const int nh = n_history.empty() ? 0 : (int)n_history[st];
+      TORCH_CHECK(nh >= 0 && nh <= hist_stride, "n_history[", st, "] = ", nh, " outside [0, ", hist_stride, "]");
+      QttsBackboneStream& q = io[st];
+      q.k_cache = d->k_cache_.data_ptr();
+      q.v_cache = d->v_cache_.data_ptr();
+      q.position = d->position_;
+      q.pos3[0] = q.pos3[1] = q.pos3[2] = d->position_;
+      q.input_embedding = static_cast<const uint16_t*>(embeds.data_ptr()) + st * kHidden;
+      q.out_hidden = hidden_out.data_ptr<float>() + st * kHidden;
+      q.out_residual = d->hidden_buffer_.data_ptr();
+      q.out_logits = d->logits_.data_ptr<float>();
+      q.out_token = out_tokens.data_ptr<int>() + st;
+      q.history = nh > 0 ? history->data_ptr<int>() + st * hist_stride : nullptr;
+      q.n_history = nh;
+      q.seed = (unsigned long long)(seed + st);
+    }
+    if (!ws_streams_.defined()) {
+      ws_streams_ = torch::zeros({(int64_t)(kMaxStreams * qtts_workspace_bytes())}, torch::dtype(torch::kUInt8).device(dev_));
+      hip_check(qtts_workspace_init(ws_streams_.data_ptr(), dev_.index()), "qtts_workspace_init");
+    }
+    QttsSampling samp = sampling(do_sample, temperature, top_k, top_p, seed);
+    hip_check(qtts_backbone_step_streams((int)n, ws_streams_.data_ptr(), reinterpret_cast<const TTSLayerWeights*>(d_layer_weights_.data_ptr()),
+                                         num_layers_, final_norm_weight_.data_ptr(), cos_table_.data_ptr(), sin_table_.data_ptr(),
+                                         max_seq_len_, io.data(), codec_head_weight_.data_ptr(), (int)codec_head_weight_.size(0),
+                                         1, (float)repetition_penalty, (int)eos_id, suppress_eos ? 1 : 0, &samp, (int)frame_step,
+                                         cur_stream()),
+              "qtts_backbone_step_streams");
+    for (auto* d : decs) d->position_++;
+  }
+  // the wait-timeout error words of the decode_steps_streams() workspaces
+  void check_error_streams() const {
+    if (!ws_streams_.defined()) return;
+    for (int st = 0; st < kMaxStreams; ++st) {
+      unsigned int code = 0;
+      hip_check(qtts_workspace_check(static_cast<uint8_t*>(ws_streams_.data_ptr()) + st * qtts_workspace_bytes(), &code, cur_stream()),
+                "qtts_workspace_check");
+      TORCH_CHECK(code == 0, "decode kernel reported a device-side wait timeout in stream ", st, " (error word ", code, ")");
+    }
+  }
+
   void reset() {
     position_ = 0;
     k_cache_.zero_();
@@ -233,6 +315,7 @@ class MegakernelTTSDecoder {
   torch::Tensor embed_weight_, final_norm_weight_, codec_head_weight_, cos_table_, sin_table_, d_layer_weights_;
   std::vector<torch::Tensor> layer_weights_tensors_;
   torch::Tensor k_cache_, v_cache_, hidden_buffer_, g_normalized_, logits_, token_, ws_;
+  torch::Tensor ws_streams_;   // decode_steps_streams(): per-stream workspaces
 };
 
 // ---------------------------------------------------------------------------------------
@@ -461,6 +544,11 @@ PYBIND11_MODULE(_qwentts_amd_C, m) {
       .def("hidden_state_buffer", &MegakernelTTSDecoder::hidden_state_buffer)
       .def("residual_buffer", &MegakernelTTSDecoder::residual_buffer)
       .def("logits_buffer", &MegakernelTTSDecoder::logits_buffer)
+      .def("decode_steps_streams", &MegakernelTTSDecoder::decode_steps_streams, py::arg("decoders"), py::arg("embeds"),
+           py::arg("out_tokens"), py::arg("hidden_out"), py::arg("history"), py::arg("n_history"),
+           py::arg("repetition_penalty"), py::arg("eos_id"), py::arg("suppress_eos"), py::arg("do_sample"),
+           py::arg("temperature"), py::arg("top_k"), py::arg("top_p"), py::arg("seed"), py::arg("frame_step"))
+      .def("check_error_streams", &MegakernelTTSDecoder::check_error_streams)
       .def("check_error", &MegakernelTTSDecoder::check_error);
   py::class_<MegakernelCodePredictorDecoder>(m, "MegakernelCodePredictorDecoder")
       .def(py::init<std::vector<torch::Tensor>, torch::Tensor, torch::Tensor, torch::Tensor, int64_t, int64_t>())

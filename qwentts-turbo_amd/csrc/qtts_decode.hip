@@ -828,7 +828,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   // workgroup shares one running max per head, so lane-group partials are plain sums: they go
   // to LDS unscaled and thread (head, dim) adds them. Every exp is branch-free (a masked
   // argument becomes -1000, whose exp is 0).
-  auto attention = [&](auto nh_c, int lp, int layer, int L, int c0, int c1, bool local, int hh) {
+  auto attention = [&](auto nh_c, int lp, int layer, int L, int c0, int c1, bool local, int hh, int unit) {
     constexpr int NH = decltype(nh_c)::value;
     constexpr int JJ = KVGeo<BB>::JJ, SUB = KVGeo<BB>::SUB;
     constexpr double NEG = -1000.0;
@@ -962,8 +962,8 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
         // the whole context in this workgroup: f32(A * (1 / l)), no partial exchange
         s.attn[128 * (hq0 + h) + d] = (float)(A * (1.0 / Lsum));
       } else {
-        // partial of (chunk li >> 1, head hh): acc[128], m, l
-        uint64_t* dst = &ws->attp[xcd][lp & 1][li * APH];
+        // partial of (chunk unit >> 1, head hh = unit & 1): acc[128], m, l
+        uint64_t* dst = &ws->attp[xcd][lp & 1][unit * APH];
         const uint32_t tg = tag_of(lp, T_ATT);
         pub_local(dst + d, (float)A, tg);
         if (d == 0) { pub_local(dst + 128, (float)m[0], tg); pub_local(dst + 129, (float)Lsum, tg); }
@@ -1299,10 +1299,12 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     q.L = q.pos + 1;
     chunking<BB>(q.L, q.C, q.P);
     q.local = att_local(pi);
-    // chunked: workgroup li takes chunk li >> 1 for query head li & 1 of the XCD
-    q.has_chunk = q.local || li < 2 * q.C;
-    q.c0 = q.local ? 0 : (li >> 1) * q.P;
-    q.c1 = q.local ? q.L : min(q.L, ((li >> 1) + 1) * q.P);
+    // chunked: unit u = (chunk u >> 1, query head u & 1) of the XCD's KV head; workgroup li takes
+    // unit li (XL: units lu, lu + 4, lu + 8, lu + 12 with lu = li_hw >> 3; these fields are lu's)
+    const int lu = XL ? (li_hw >> 3) : li;
+    q.has_chunk = q.local || lu < 2 * q.C;
+    q.c0 = q.local ? 0 : (lu >> 1) * q.P;
+    q.c1 = q.local ? q.L : min(q.L, ((lu >> 1) + 1) * q.P);
     q.last_pos = pi == a.n_pos - 1;
     q.head = has_head(pi);
     return q;
@@ -1339,7 +1341,14 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           // the math waves' attention synchronises the whole workgroup (passes + 2 times);
           // this wave's inputs for the step are produced after those points anyway
           if (q.has_chunk) {
-            const int nb = (q.c1 - q.c0 + KVGeo<BB>::SUB - 1) / KVGeo<BB>::SUB + 2;
+            int nb = (q.c1 - q.c0 + KVGeo<BB>::SUB - 1) / KVGeo<BB>::SUB + 2;
+            if (XL && !q.local) {
+              // the workgroup's further units
+              for (int u = (li_hw >> 3) + 4; u < 2 * q.C; u += 4) {
+                const int c0 = (u >> 1) * q.P, c1 = min(q.L, c0 + q.P);
+                nb += (c1 - c0 + KVGeo<BB>::SUB - 1) / KVGeo<BB>::SUB + 2;
+              }
+            }
             for (int b = 0; b < nb; ++b) step_barrier();
           }
           if (q.local) {
@@ -1485,10 +1494,20 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
         case S_ATT:
           if constexpr (!BB) {
             if (q.local) attention_cp_local(q.L);
-            else if (q.has_chunk) attention(std::integral_constant<int, 1>{}, lp, layer, q.L, q.c0, q.c1, false, li & 1);
+            else if (q.has_chunk) attention(std::integral_constant<int, 1>{}, lp, layer, q.L, q.c0, q.c1, false, li & 1, li);
           } else if (q.has_chunk) {
-            if (q.local) attention(std::integral_constant<int, 2>{}, lp, layer, q.L, q.c0, q.c1, true, 0);
-            else attention(std::integral_constant<int, 1>{}, lp, layer, q.L, q.c0, q.c1, false, li & 1);
+            if (q.local) {
+              attention(std::integral_constant<int, 2>{}, lp, layer, q.L, q.c0, q.c1, true, 0, li);
+            } else if constexpr (XL) {
+              // units lu, lu + 4, ... (the first one's KV tile was issued in the QKV step)
+              for (int u = li_hw >> 3; u < 2 * q.C; u += 4) {
+                const int c0 = (u >> 1) * q.P, c1 = min(q.L, c0 + q.P);
+                if (u >= 4) load_kv<BB>(tk, a, SIO(kc), SIO(vc), layer, xcd, c0, min(c1, q.L - 1), mw, lane);
+                attention(std::integral_constant<int, 1>{}, lp, layer, q.L, c0, c1, false, u & 1, u);
+              }
+            } else {
+              attention(std::integral_constant<int, 1>{}, lp, layer, q.L, q.c0, q.c1, false, li & 1, li);
+            }
           }
           if (q.local) {
             o_stage(layer);
@@ -1563,6 +1582,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
 template __global__ void qtts_decode_kernel<true, false>(const KArgs a);
 template __global__ void qtts_decode_kernel<false, false>(const KArgs a);
 template __global__ void qtts_decode_kernel<false, true>(const KArgs a);
+template __global__ void qtts_decode_kernel<true, true>(const KArgs a);
 
 }  // namespace qtts
 
@@ -1582,7 +1602,11 @@ struct DeviceCheck {
 };
 std::mutex g_mu;
 std::unordered_map<int, DeviceCheck> g_dev;
-std::unordered_map<const void*, uint32_t> g_seq;   // launch sequence per workspace
+struct TagSeq {
+  uint32_t seq = 0;    // launch sequence number
+  size_t bytes = 0;    // widest block cleared on a wrap
+};
+std::unordered_map<const void*, TagSeq> g_seq;   // launch sequence per workspace (block)
 std::unordered_map<int, void*> g_lib_ws;           // library-owned workspace per device
 uint64_t* g_trace = nullptr;                       // optional step timeline buffer
 
@@ -1613,6 +1637,8 @@ hipError_t check_device(int device) {
   if (e != hipSuccess || occ < 1) return dc.status = (e != hipSuccess ? e : hipErrorInvalidDevice);
   e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)qtts::qtts_decode_kernel<false, true>, qtts::NTHR, 0);
   if (e != hipSuccess || occ < 1) return dc.status = (e != hipSuccess ? e : hipErrorInvalidDevice);
+  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)qtts::qtts_decode_kernel<true, true>, qtts::NTHR, 0);
+  if (e != hipSuccess || occ < 1) return dc.status = (e != hipSuccess ? e : hipErrorInvalidDevice);
   int* d = nullptr;
   if ((e = hipMalloc(&d, qtts::NWG * sizeof(int))) != hipSuccess) return dc.status = e;
   void* args[] = {&d};
@@ -1634,10 +1660,14 @@ hipError_t check_device(int device) {
 
 uint32_t next_tag_base(void* ws, size_t bytes, hipStream_t stream, hipError_t* err) {
   std::lock_guard<std::mutex> lk(g_mu);
-  uint32_t& seq = g_seq[ws];
+  TagSeq& ts = g_seq[ws];
+  uint32_t& seq = ts.seq;
+  // the widest block any launch has used from this address: a wrap clears all of it, so no
+  // workspace of a multi-stream block keeps a tag of the previous cycle
+  ts.bytes = bytes > ts.bytes ? bytes : ts.bytes;
   if (seq == 0 || seq >= (1u << 20) - 1u) {
     // first use (or tag wrap): clear every exchange slot with a fill kernel
-    const size_t n16 = bytes / 16;
+    const size_t n16 = ts.bytes / 16;
     hipLaunchKernelGGL(zero_kernel, dim3(256), dim3(256), 0, stream, reinterpret_cast<uint4*>(ws), n16);
     *err = hipGetLastError();
     seq = 1;
@@ -1659,7 +1689,7 @@ hipError_t launch(bool bb, KArgs& a, hipStream_t stream, bool xl = false, int n_
   a.spin_cap = kSpinCap;
   a.trace = g_trace;
   void* args[] = {&a};
-  const void* fn = bb ? (const void*)qtts::qtts_decode_kernel<true, false>
+  const void* fn = bb ? (xl ? (const void*)qtts::qtts_decode_kernel<true, true> : (const void*)qtts::qtts_decode_kernel<true, false>)
                       : (xl ? (const void*)qtts::qtts_decode_kernel<false, true> : (const void*)qtts::qtts_decode_kernel<false, false>);
   return hipLaunchCooperativeKernel(fn, dim3(qtts::NWG), dim3(qtts::NTHR), args, 0, stream);
 }
@@ -1833,6 +1863,57 @@ hipError_t qtts_backbone_step(void* workspace, const TTSLayerWeights* layer_weig
   }
   a.sel.frame_step = frame_step;
   return launch(true, a, stream);
+}
+
+hipError_t qtts_backbone_step_streams(int n_streams, void* workspaces, const TTSLayerWeights* layer_weights, int num_layers,
+                                      const void* final_norm_weight, const void* cos_table, const void* sin_table,
+                                      int max_seq_len, const QttsBackboneStream* streams, const void* codec_head, int vocab,
+                                      int mask_tail, float repetition_penalty, int eos_id, int suppress_eos,
+                                      const QttsSampling* sampling, int frame_step, hipStream_t stream) {
+  if (n_streams < 1 || n_streams > qtts::NSTREAM || streams == nullptr) return hipErrorInvalidValue;
+  if (workspaces == nullptr || (reinterpret_cast<uintptr_t>(workspaces) & 255u) != 0) return hipErrorInvalidValue;
+  if (codec_head != nullptr && (vocab <= 0 || vocab > qtts::MAXV || vocab % (qtts::NWG * qtts::NMATH) != 0))
+    return hipErrorInvalidValue;
+  KArgs a;
+  base_args(a, layer_weights, num_layers, final_norm_weight, cos_table, sin_table, nullptr, nullptr, max_seq_len);
+  a.head = reinterpret_cast<const qtts::bf16_t*>(codec_head);
+  a.vocab = vocab;
+  a.mask_tail = mask_tail;
+  a.rep_penalty = repetition_penalty;
+  a.eos_id = eos_id;
+  a.suppress_eos = suppress_eos;
+  if (sampling) {
+    a.sel.do_sample = sampling->do_sample;
+    a.sel.temperature = sampling->temperature;
+    a.sel.top_k = sampling->top_k;
+    a.sel.top_p = sampling->top_p;
+  }
+  a.sel.frame_step = frame_step;
+  for (int st = 0; st < n_streams; ++st) {
+    const QttsBackboneStream& in = streams[st];
+    if (in.k_cache == nullptr || in.v_cache == nullptr || in.input_embedding == nullptr) return hipErrorInvalidValue;
+    if (in.position < 0 || in.position >= max_seq_len) return hipErrorInvalidValue;
+    if (in.n_history < 0 || (in.n_history > 0 && in.history == nullptr)) return hipErrorInvalidValue;
+    qtts::StreamIO& io = a.io[st];
+    io.ws = reinterpret_cast<Workspace*>(workspaces) + st;
+    io.kc = in.k_cache;
+    io.vc = in.v_cache;
+    io.pos0 = in.position;
+    for (int i = 0; i < 3; ++i) {
+      io.pos3[i] = in.pos3[i];
+      if (io.pos3[i] < 0 || io.pos3[i] >= max_seq_len) return hipErrorInvalidValue;
+    }
+    io.in_emb = reinterpret_cast<const qtts::bf16_t*>(in.input_embedding);
+    io.out_hidden = in.out_hidden;
+    io.out_residual = in.out_residual;
+    io.out_logits = in.out_logits;
+    io.out_token = in.out_token;
+    io.history = in.history;
+    io.n_history = in.n_history;
+    io.seed = in.seed;
+  }
+  // stream 0's position is the one launch() validates; the others were checked above
+  return launch(true, a, stream, true, n_streams);
 }
 
 hipError_t qtts_cp_step(void* workspace, const CPLayerWeights* layer_weights, int num_layers,

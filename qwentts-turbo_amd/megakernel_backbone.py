@@ -46,12 +46,20 @@ class TTSMegakernelGenerator:
     """High-level backbone decoder (megakernel_backbone.py:412-488)."""
 
     def __init__(self, model_path: Optional[str] = None, model=None, max_seq_len: int = 4096,
-                 rope_theta: float = ROPE_THETA, device="cuda"):
-        if model is None:
-            if model_path is None:
-                raise ValueError("pass model (state dict / module) or a local model_path")
-            model = load_local(model_path)
-        w = _extract_tts_backbone_weights(model, max_seq_len, rope_theta, device)
+                 rope_theta: float = ROPE_THETA, device="cuda", shared_weights: Optional[dict] = None):
+        """``shared_weights``: the ``weights`` of another generator built with the same
+        ``max_seq_len``, reused instead of extracting a copy (the decoders of a batch share one
+        copy, which one multi-stream launch requires)."""
+        if shared_weights is not None:
+            if shared_weights["cos_table"].shape[0] < max_seq_len:
+                raise ValueError("shared_weights were built for a shorter max_seq_len")
+            w = shared_weights
+        else:
+            if model is None:
+                if model_path is None:
+                    raise ValueError("pass model (state dict / module) or a local model_path")
+                model = load_local(model_path)
+            w = _extract_tts_backbone_weights(model, max_seq_len, rope_theta, device)
         kernel = _ext.load()
         self.decoder = kernel.MegakernelTTSDecoder(
             w["embed_weight"], w["layer_weights"], w["final_norm_weight"], w["codec_head_weight"],

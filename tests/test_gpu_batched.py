@@ -46,3 +46,66 @@ def test_c4_batch8_ragged(pkg):
     assert np.array_equal(toks.cpu().numpy(), fx["tokens"])
     assert np.array_equal(comb.float().cpu().numpy(), fx["combined"])
     assert dec.positions() == lengths
+
+
+def _batched_pair(pkg, lengths, seed):
+    """Two BatchedTTSDecoders over one 2-layer synthetic model with identical per-stream KV
+    prefixes: stream s attends lengths[s] positions (its new entry at slot lengths[s] - 1)."""
+    cfg = pkg.SyntheticConfig(n_bb_layers=2, n_cp_layers=1, n_groups=1)
+    dsd = {k: v.cuda() for k, v in pkg.synthetic_state_dict(seed=seed, cfg=cfg).items()}
+    n, S = len(lengths), max(lengths)
+    decs = [pkg.BatchedTTSDecoder(dsd, n, max_seq_len=S) for _ in range(2)]
+    g = torch.Generator().manual_seed(seed)
+    for s, L in enumerate(lengths):
+        k = torch.randn(2, 8, L - 1, 128, generator=g).to(torch.bfloat16).cuda()
+        v = torch.randn(2, 8, L - 1, 128, generator=g).to(torch.bfloat16).cuda()
+        for d in decs:
+            if L > 1:
+                d.set_kv_cache(s, k, v)
+            else:
+                d.streams[s].set_position(0)
+    return decs
+
+
+@pytest.mark.parametrize("lengths,sample", [
+    ([1, 33, 64, 65, 577, 4096, 200, 2, 1500], False),
+    ([4096, 129, 1000], True),
+], ids=["greedy9", "sampled3"])
+def test_backbone_streams_match_batch1(pkg, lengths, sample):
+    """One launch of up to 8 backbone streams (stream s on XCD s, decode_steps_streams) against
+    batch-1 decode_step_select on a copy of each stream: token, final-norm hidden, residual,
+    logits and the new KV entry bit-identical. Lengths mix the one-pass local attention (<= 64)
+    and the chunked split up to 32 (chunk, head) units (4096: 8 per workgroup); 9 streams take
+    two launches (8 + 1); the sampled case adds top-k / top-p, temperature and a repetition
+    penalty over per-stream histories of different lengths."""
+    n = len(lengths)
+    xl, ref = _batched_pair(pkg, lengths, 70 + n)
+    g = torch.Generator().manual_seed(n)
+    x = torch.randn(n, 1024, generator=g).to(torch.bfloat16).cuda()
+    vocab = xl.vocab_size
+    hist = torch.randint(0, vocab, (n, 24), generator=g, dtype=torch.int32).cuda()
+    n_hist = [24, 0, 7][:n] if sample else []
+    kw = dict(repetition_penalty=1.3 if sample else 1.0, suppress_eos=False, do_sample=sample, temperature=0.8,
+              top_k=40, top_p=0.9, frame_step=3)
+    i32 = dict(dtype=torch.int32, device="cuda")
+    tok = torch.full((n,), -1, **i32)
+    print(f"backbone streams {lengths} sample={sample}: launching", flush=True)
+    hidden = xl.step_select(x, tok, cases.EOS_ID, history=hist if sample else None, n_history=n_hist, seed=5, **kw)
+    for s, dec in enumerate(ref.streams):
+        t1 = torch.full((1,), -1, **i32)
+        dec.decoder.decode_step_select(x[s], t1, hist[s], n_hist[s] if sample else 0, kw["repetition_penalty"],
+                                       cases.EOS_ID, False, sample, kw["temperature"], kw["top_k"], kw["top_p"], 5 + s,
+                                       kw["frame_step"])
+        torch.cuda.synchronize()
+        assert torch.equal(tok[s:s + 1], t1), f"stream {s} (L={lengths[s]}): token {tok[s].item()} vs {t1.item()}"
+        assert torch.equal(hidden[s], dec.decoder.hidden_state_buffer()), f"stream {s}: hidden differs"
+        xd = xl.streams[s].decoder
+        assert torch.equal(xd.residual_buffer(), dec.decoder.residual_buffer()), f"stream {s}: residual differs"
+        assert torch.equal(xd.logits_buffer(), dec.decoder.logits_buffer()), f"stream {s}: logits differ"
+        L = lengths[s]
+        assert torch.equal(xd.get_k_cache()[:, :, L - 1], dec.decoder.get_k_cache()[:, :, L - 1])
+        assert torch.equal(xd.get_v_cache()[:, :, L - 1], dec.decoder.get_v_cache()[:, :, L - 1])
+    xl.check_error()
+    ref.check_error()
+    assert xl.positions() == ref.positions() == lengths
+    print(f"backbone streams {lengths}: tokens {tok.tolist()}", flush=True)
