@@ -36,7 +36,7 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch measured with rocprofv3 PMC counters on the same workload
 # (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000 KiB, both factors from a plain 512 MiB device copy);
 # the summary with the commands is profiles/qtts_decode_kernel_frame512_pmc_traffic.md.
-PMC_TRAFFIC = {"cp_frame": 2_787_152_961, "backbone_step": 1_004_330_762}
+PMC_TRAFFIC = {"cp_frame": 2_786_333_845, "backbone_step": 996_280_718}
 
 
 def backbone_bytes(L: int) -> int:
@@ -131,7 +131,7 @@ def batched_c4(pkg, sd, frames: int = 10) -> dict:
     dec.check_error()
     return {"streams": 8, "lengths": lengths, "frames": frames,
             "frames_per_s_total": round(8 * frames / el, 2), "frames_per_s_per_stream": round(frames / el, 2),
-            "note": "backbone: one batch-1 launch per stream; code predictor: one launch for all streams, stream s on XCD s"}
+            "note": "one backbone launch and one code-predictor launch for all streams per frame, stream s on XCD s"}
 
 
 def main():
@@ -218,9 +218,9 @@ def main():
     t_bb = sum(e[1].elapsed_time(e[2]) for e in ev) / n_ev * 1e-3
     cp_gbs = cp_frame_bytes() / t_cp / 1e9
     bb_gbs = backbone_bytes(512) / t_bb / 1e9
-    dominant = ("qtts_decode_kernel<false> (code-predictor frame)", cp_gbs, cp_frame_bytes(), PMC_TRAFFIC["cp_frame"]) \
+    dominant = ("qtts_decode_kernel<false, false> (code-predictor frame)", cp_gbs, cp_frame_bytes(), PMC_TRAFFIC["cp_frame"]) \
         if t_cp >= t_bb else \
-        ("qtts_decode_kernel<true> (backbone step, L=512)", bb_gbs, backbone_bytes(512), PMC_TRAFFIC["backbone_step"])
+        ("qtts_decode_kernel<true, false> (backbone step, L=512)", bb_gbs, backbone_bytes(512), PMC_TRAFFIC["backbone_step"])
 
     fps = args.steps / el
     out = {
