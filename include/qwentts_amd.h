@@ -211,6 +211,29 @@ hipError_t qtts_backbone_step_streams(
     float repetition_penalty, int eos_id, int suppress_eos, const QttsSampling* sampling,
     int frame_step, hipStream_t stream);
 
+/* Backbone prefill: n_tokens prompt embeddings (bf16 [n_tokens, 1024], device) through all
+ * layers at once, replacing the reference's PyTorch talker prefill and KV handoff
+ * (generator.py:209-225, :245-257; megakernel_backbone.py:285-294). K/V of cache positions
+ * position .. position + n_tokens - 1 are written into k_cache / v_cache (bf16
+ * [num_layers, 8, max_seq_len, 128], the decode layout); attention covers cache positions
+ * 0 .. position + n_tokens - 1 (causal), so a prefix already in the cache is attended.
+ * Arithmetic follows the transformers bf16 forward (bf16 storage after every op, f32 sums on
+ * bf16 MFMA). pos3: NULL (t = h = w = position of the token) or device int32 [3][n_tokens]
+ * rotary (t, h, w) rows of the bf16 tables (clamped to [0, max_seq_len)). out_hidden: f32 [1024],
+ * the final-norm hidden of the last token (bf16 values). When codec_head is not NULL the first
+ * group-0 token is selected from bf16(codec_head . hidden) as in generator.py:113-119 (suppress
+ * mask when mask_tail, EOS removed when suppress_eos, greedy or sampled) into out_token; the
+ * logits go to out_logits when not NULL. workspace: >= qtts_prefill_workspace_bytes(n_tokens,
+ * vocab) bytes, 256-byte aligned (contents need no initialisation). */
+size_t qtts_prefill_workspace_bytes(int n_tokens, int vocab);
+hipError_t qtts_backbone_prefill(
+    void* workspace, size_t workspace_bytes, const TTSLayerWeights* layer_weights, int num_layers,
+    const void* final_norm_weight, const void* cos_table, const void* sin_table, void* k_cache,
+    void* v_cache, int max_seq_len, int position, int n_tokens, const int* pos3,
+    const void* input_embeddings, float* out_hidden, const void* codec_head, int vocab,
+    float* out_logits, int* out_token, int mask_tail, int eos_id, int suppress_eos,
+    const QttsSampling* sampling, int frame_step, hipStream_t stream);
+
 /* Code-predictor frames of n_streams (1..8) independent streams in one launch; no counterpart in the
  * reference, whose decode is batch 1 (fused_decode_code_predictor.cu:565-668 runs one stream). Stream s
  * runs on XCD s alone (its 32 workgroups, every exchange in that XCD's L2) and computes exactly what

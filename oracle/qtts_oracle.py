@@ -33,7 +33,12 @@ Precision policies (``policy=``):
     values transformers' rotary embedding produces); used to pin the math against
     transformers' Qwen3 modules run in float64.
   * ``"hf_bf16"`` -- the HF PyTorch bf16 path (transformers Qwen3DecoderLayer op order in bf16),
-    i.e. what the reference's ``backend="pytorch"`` computes.
+    i.e. what the reference's ``backend="pytorch"`` and its prefill (generator.py:209-225)
+    compute. ``hf_sums="f64"`` keeps every bf16 rounding point but forms the projection sums in
+    f64 instead of torch's f32 order: the spread between the two is this path's sensitivity to
+    summation order alone (a 1-ulp bf16 flip in one op perturbs the next op's sums and flips a
+    few percent of its outputs, so the spread grows with depth), the floor any bf16
+    implementation with its own summation order (cuBLAS, MFMA) sits at.
 
 Pinning (see tests/test_oracle_*.py): layer math against transformers ``Qwen3DecoderLayer``
 (fp32 and bf16), interleaved mRoPE against transformers ``Qwen3VLTextRotaryEmbedding``,
@@ -247,9 +252,11 @@ class DecoderOracle:
 
     def __init__(self, layer_weights: Sequence[Sequence[torch.Tensor]], final_norm: torch.Tensor,
                  max_seq: int, kind: str = "backbone", policy: str = "kernel",
-                 dims: Dims = Dims()):
+                 dims: Dims = Dims(), hf_sums: str = "torch"):
         assert kind in ("backbone", "cp") and policy in ("kernel", "exact", "hf_bf16")
+        assert hf_sums in ("torch", "f64")
         self.kind, self.policy, self.d = kind, policy, dims
+        self.hf_sums = hf_sums
         wdt = torch.bfloat16 if policy == "hf_bf16" else torch.float64
         self.layers = [LayerW.from_list(lw, wdt) for lw in layer_weights]
         self.final_norm = final_norm.detach().to("cpu", wdt)
@@ -348,14 +355,21 @@ class DecoderOracle:
         return out
 
     # -- one layer, HF bf16 policy (transformers Qwen3DecoderLayer op order) ----------------
+    def _linear(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        """bf16 projection: torch's own (f32 sums in its order), or f64 sums rounded once."""
+        if self.hf_sums == "torch":
+            return torch.nn.functional.linear(x, w)
+        return (x.double() @ w.double().t()).to(torch.float32).to(x.dtype)
+
     def _layer_hf(self, li: int, x: torch.Tensor, pos: int, cos, sin, trace):
         d, w = self.d, self.layers[li]
+        lin = self._linear
         bf = torch.bfloat16
         cos_b, sin_b = cos.to(bf), sin.to(bf)
         h = rms_norm_hf(x, w.ln_in, d.eps)
-        q = torch.nn.functional.linear(h, w.q).view(d.n_q, d.head_dim)
-        k = torch.nn.functional.linear(h, w.k).view(d.n_kv, d.head_dim)
-        v = torch.nn.functional.linear(h, w.v).view(d.n_kv, d.head_dim)
+        q = lin(h, w.q).view(d.n_q, d.head_dim)
+        k = lin(h, w.k).view(d.n_kv, d.head_dim)
+        v = lin(h, w.v).view(d.n_kv, d.head_dim)
         q = rms_norm_hf(q, w.qn, d.eps)
         k = rms_norm_hf(k, w.kn, d.eps)
         half = d.head_dim // 2
@@ -372,12 +386,12 @@ class DecoderOracle:
         sc = torch.matmul(qb, K[kv_of_q].transpose(1, 2).contiguous()) * scale
         p = torch.softmax(sc, dim=-1, dtype=torch.float32).to(bf)
         attn = torch.matmul(p, V[kv_of_q]).reshape(-1)
-        o = torch.nn.functional.linear(attn, w.o)
+        o = lin(attn, w.o)
         h1 = x + o
         hn = rms_norm_hf(h1, w.ln_post, d.eps)
-        g = torch.nn.functional.linear(hn, w.gate)
-        a = torch.nn.functional.silu(g) * torch.nn.functional.linear(hn, w.up)
-        out = h1 + torch.nn.functional.linear(a, w.down)
+        g = lin(hn, w.gate)
+        a = torch.nn.functional.silu(g) * lin(hn, w.up)
+        out = h1 + lin(a, w.down)
         if trace is not None:
             trace.setdefault("attn", []).append(attn.float().clone())
             trace.setdefault("h1", []).append(h1.float().clone())

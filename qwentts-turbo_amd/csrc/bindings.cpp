@@ -180,6 +180,55 @@ class MegakernelTTSDecoder {
         sampling(do_sample, temperature, top_k, top_p, seed), (int)frame_step, false, out_token.data_ptr<int>(), skip);
   }
 
+  // Extended: prefill of the prompt embeddings [S, 1024] at positions position() .. position() + S - 1
+  // in one call (qtts_backbone_prefill: the transformers bf16 forward on MFMA, K/V straight into
+  // this decoder's cache). Returns the last token's final-norm hidden (f32 [1024] of bf16 values),
+  // also left in hidden_state_buffer(). With out_token, the first group-0 token is selected from
+  // the codec head (suppress mask, EOS removed when suppress_eos; generator.py:113-119). pos3:
+  // optional int32 [3, S] rotary (t, h, w) rows. The position advances by S.
+  torch::Tensor prefill(torch::Tensor embeds, c10::optional<torch::Tensor> out_token, int64_t eos_id, bool suppress_eos,
+                        bool do_sample, double temperature, int64_t top_k, double top_p, int64_t seed,
+                        c10::optional<torch::Tensor> pos3) {
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(dev_);
+    if (embeds.dim() == 3) embeds = embeds.squeeze(0);
+    TORCH_CHECK(embeds.dim() == 2 && embeds.size(1) == kHidden && embeds.size(0) >= 1, "embeds must be [S, 1024], got ",
+                embeds.sizes());
+    TORCH_CHECK(embeds.device() == dev_, "embeds must be on ", dev_);
+    auto e = embeds.to(torch::kBFloat16).contiguous();
+    const int S = (int)e.size(0);
+    TORCH_CHECK(position_ + S <= max_seq_len_, "prefill of ", S, " tokens at position ", position_, " exceeds max_seq_len ",
+                max_seq_len_);
+    const int* p3 = nullptr;
+    torch::Tensor p3t;
+    if (pos3.has_value()) {
+      p3t = pos3->to(dev_, torch::kInt32).contiguous();
+      TORCH_CHECK(p3t.dim() == 2 && p3t.size(0) == 3 && p3t.size(1) == S, "pos3 must be [3, S]");
+      p3 = p3t.data_ptr<int>();
+    }
+    int* tok = nullptr;
+    if (out_token.has_value()) {
+      TORCH_CHECK(out_token->is_cuda() && out_token->scalar_type() == torch::kInt32 && out_token->numel() >= 1,
+                  "out_token must be an int32 GPU tensor");
+      tok = out_token->data_ptr<int>();
+    }
+    const int vocab = (int)codec_head_weight_.size(0);
+    const size_t need = qtts_prefill_workspace_bytes(S, tok ? vocab : 0);
+    TORCH_CHECK(need > 0, "prefill workspace size query failed");
+    if (!pf_ws_.defined() || (size_t)pf_ws_.numel() < need)
+      pf_ws_ = torch::empty({(int64_t)need}, torch::dtype(torch::kUInt8).device(dev_));
+    QttsSampling samp = sampling(do_sample, temperature, top_k, top_p, seed);
+    hip_check(qtts_backbone_prefill(pf_ws_.data_ptr(), (size_t)pf_ws_.numel(),
+                                    reinterpret_cast<const TTSLayerWeights*>(d_layer_weights_.data_ptr()), num_layers_,
+                                    final_norm_weight_.data_ptr(), cos_table_.data_ptr(), sin_table_.data_ptr(),
+                                    k_cache_.data_ptr(), v_cache_.data_ptr(), max_seq_len_, position_, S, p3, e.data_ptr(),
+                                    g_normalized_.data_ptr<float>(), tok ? codec_head_weight_.data_ptr() : nullptr, vocab,
+                                    tok ? logits_.data_ptr<float>() : nullptr, tok, 1, (int)eos_id, suppress_eos ? 1 : 0,
+                                    &samp, 0, cur_stream()),
+              "qtts_backbone_prefill");
+    position_ += S;
+    return g_normalized_.clone();
+  }
+
   // Extended: decode_step_select for up to 8 independent decoders `decs` (sharing this decoder's
   // weights) in one launch, decoder s on XCD s, each at its own position with its own KV cache.
   // out_tokens[s] gets stream s's token and hidden_out[s] (f32 [n, 1024]) its final-norm hidden;
@@ -316,6 +365,7 @@ class MegakernelTTSDecoder {
   std::vector<torch::Tensor> layer_weights_tensors_;
   torch::Tensor k_cache_, v_cache_, hidden_buffer_, g_normalized_, logits_, token_, ws_;
   torch::Tensor ws_streams_;   // decode_steps_streams(): per-stream workspaces
+  torch::Tensor pf_ws_;        // prefill(): activations and split-K partials (grown on demand)
 };
 
 // ---------------------------------------------------------------------------------------
@@ -544,6 +594,10 @@ PYBIND11_MODULE(_qwentts_amd_C, m) {
       .def("hidden_state_buffer", &MegakernelTTSDecoder::hidden_state_buffer)
       .def("residual_buffer", &MegakernelTTSDecoder::residual_buffer)
       .def("logits_buffer", &MegakernelTTSDecoder::logits_buffer)
+      .def("prefill", &MegakernelTTSDecoder::prefill, py::arg("embeds"), py::arg("out_token") = py::none(),
+           py::arg("eos_id") = -1, py::arg("suppress_eos") = false, py::arg("do_sample") = false,
+           py::arg("temperature") = 1.0, py::arg("top_k") = 0, py::arg("top_p") = 1.0, py::arg("seed") = 0,
+           py::arg("pos3") = py::none())
       .def("decode_steps_streams", &MegakernelTTSDecoder::decode_steps_streams, py::arg("decoders"), py::arg("embeds"),
            py::arg("out_tokens"), py::arg("hidden_out"), py::arg("history"), py::arg("n_history"),
            py::arg("repetition_penalty"), py::arg("eos_id"), py::arg("suppress_eos"), py::arg("do_sample"),

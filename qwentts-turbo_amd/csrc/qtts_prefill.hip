@@ -1,0 +1,624 @@
+// Backbone prefill on MI355X (gfx950): the S prompt tokens through every layer at once, the
+// projections and both attention products on bf16 MFMA with f32 accumulation, K and V written
+// straight into the decode kernels' cache layout [layers, 8, max_seq, 128] bf16.
+//
+// What it replaces: the reference prefills with the qwen_tts PyTorch talker forward in bf16
+// (generator.py:209-225: transformers Qwen3DecoderLayer op order, TF/qwen3/modeling_qwen3.py
+// :50-64, :140-208, :211-324) and then copies that DynamicCache into the megakernel cache
+// (generator.py:245-257, megakernel_backbone.py:285-294); the first group-0 token comes from
+// the last position's hidden through the codec head (generator.py:113-117). Every value is
+// rounded where that bf16 forward rounds it:
+//   xn  = bf16(w * bf16(x * (1 / sqrt(mean(x^2) + eps))))              RMSNorm (:59-64)
+//   q,k,v = bf16(W xn); q,k per head through RMSNorm, then
+//   rope = bf16(bf16(q * cos) + bf16(rotate_half(q) * sin))            bf16 cos/sin tables
+//   s   = bf16(bf16(q . k) * scale), p = bf16(softmax_f32(s)), att = bf16(p V)   (:185-208)
+//   h1  = bf16(h + bf16(W_o att)); a = bf16(bf16(silu(bf16(W_g xn))) * bf16(W_u xn))
+//   h   = bf16(h1 + bf16(W_d a)); hidden = RMSNorm_final(h[S-1]); logits = bf16(W_head hidden)
+// The f32 sums run in MFMA order rather than the CPU's, so an f32 result can land on the other
+// side of a bf16 rounding boundary now and then; parity is a tolerance, not bit equality.
+//
+// Kernels (one launch each per layer; the host loop is in qtts_backbone_prefill below):
+//   rmsnorm_kernel   one wave per token
+//   gemm_kernel      C = A W^T, tile 128 x 64 x 64 (4 waves, each 32 rows x 2 MFMA 32x32x16
+//                    blocks), LDS double buffer, split-K over grid.z when the tile grid alone
+//                    would leave CUs idle (partials in f32, summed in a fixed order by
+//                    reduce_kernel); epilogues: store, residual add, SwiGLU (gate and up rows
+//                    interleaved by 32 in one tile)
+//   rope_kv_kernel   q/k RMSNorm + interleaved mRoPE, K/V cache write, one workgroup per token
+//   attn_kernel      causal GQA, one wave per (32-query block, query head): S^T = K Q^T on
+//                    MFMA (each lane then holds one query's scores, so the row max and sum
+//                    stay in the lane and its partner half-wave), two passes (row max / sum,
+//                    then p = bf16(e / l) and O^T = V^T P^T on MFMA with V^T staged in LDS)
+//   select_kernel    suppress mask + EOS suppression + the decode kernels' wave_select
+#include <hip/hip_runtime.h>
+#include <algorithm>
+#include <cstddef>
+#include <cstdint>
+#include "qwentts_amd.h"
+#include "qtts_common.h"
+#include "qtts_select.h"
+
+namespace qtts {
+namespace pf {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr float EPS = 1e-6f;                 // Qwen3RMSNorm eps (config rms_norm_eps)
+constexpr int BM = 128, BN = 64, BK = 64;    // GEMM tile
+constexpr int GT = 256;                      // GEMM threads (4 waves)
+constexpr int LROW = BK + 8;                 // LDS row (bf16): 144 B, 16-byte aligned, skewed banks
+constexpr int QKVW = 4096;                   // q | k | v row of one token
+constexpr int VTROW = 40;                    // LDS row of V^T (32 keys + pad, 8-byte aligned reads)
+constexpr int MAX_SPLIT = 16;
+
+enum WMode { W_DIRECT, W_QKV, W_O, W_GU, W_DOWN };
+enum Epi { E_STORE, E_RESID, E_SWIGLU };
+
+struct GemmArgs {
+  const bf16_t* A;                 // [M, K] activations, row stride lda
+  int lda;
+  const TTSLayerWeights* layers;   // device table (W_QKV .. W_DOWN)
+  int layer;
+  const bf16_t* B;                 // W_DIRECT: [N, K]
+  int M, N, K;                     // N: virtual columns (SwiGLU: gate/up interleaved by 32)
+  int kchunk;                      // K range per split (grid.z splits)
+  bf16_t* out;
+  int ldo;
+  const bf16_t* res;               // E_RESID: residual (may alias out)
+  int ldr;
+  float* part;                     // split-K partials [splits][M][N]
+};
+
+__device__ __forceinline__ bf16x8 as_bf8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ const bf16_t* tbl(const TTSLayerWeights* lw, int field) {
+  return reinterpret_cast<const bf16_t*>(ld_const(reinterpret_cast<const void* const*>(lw) + field));
+}
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+
+template <int EPI>
+__device__ __forceinline__ void epilogue(const GemmArgs& g, int m, int n, float v) {
+  if constexpr (EPI == E_STORE) {
+    g.out[(size_t)m * g.ldo + n] = f2bf(v);
+  } else if constexpr (EPI == E_RESID) {
+    const float r = bf2f(g.res[(size_t)m * g.ldr + n]);
+    g.out[(size_t)m * g.ldo + n] = f2bf(r + rbf(v));
+  }
+}
+
+// output column j of the SwiGLU GEMM from its gate and up sums
+__device__ __forceinline__ void epilogue_swiglu(const GemmArgs& g, int m, int j, float gs, float us) {
+  const float a = rbf(silu_f(rbf(gs)));
+  g.out[(size_t)m * g.ldo + j] = f2bf(a * rbf(us));
+}
+
+template <int WM, int EPI>
+__global__ void __launch_bounds__(GT) gemm_kernel(const GemmArgs g) {
+  __shared__ __attribute__((aligned(16))) bf16_t sa[2][BM * LROW];
+  __shared__ __attribute__((aligned(16))) bf16_t sb[2][BN * LROW];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int kbeg = blockIdx.z * g.kchunk, nk = g.kchunk / BK;
+  const int lr = t >> 3, lc = (t & 7) * 8;   // this thread's load row (within 32) and column
+
+  // weight rows this thread stages (virtual columns n0 + lr + 32 i)
+  const bf16_t* brow[2];
+  {
+    const TTSLayerWeights* lw = g.layers + g.layer;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int n = n0 + lr + 32 * i;
+      const bf16_t* p;
+      if constexpr (WM == W_DIRECT) {
+        p = g.B + (size_t)n * g.K;
+      } else if constexpr (WM == W_QKV) {
+        p = n < 2048 ? tbl(lw, 1) + (size_t)n * g.K
+                     : (n < 3072 ? tbl(lw, 2) + (size_t)(n - 2048) * g.K : tbl(lw, 3) + (size_t)(n - 3072) * g.K);
+      } else if constexpr (WM == W_O) {
+        p = tbl(lw, 6) + (size_t)n * g.K;
+      } else if constexpr (WM == W_GU) {
+        const int tt = n >> 6, r = n & 63;
+        p = r < 32 ? tbl(lw, 8) + (size_t)(32 * tt + r) * g.K : tbl(lw, 9) + (size_t)(32 * tt + r - 32) * g.K;
+      } else {
+        p = tbl(lw, 10) + (size_t)n * g.K;
+      }
+      brow[i] = p + kbeg + lc;
+    }
+  }
+  const bf16_t* arow[4];
+  bool aok[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + lr + 32 * i;
+    aok[i] = m < g.M;
+    arow[i] = g.A + (size_t)(aok[i] ? m : 0) * g.lda + kbeg + lc;
+  }
+
+  u32x4 ra[4], rb[2];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ra[i] = aok[i] ? ldw(arow[i] + k0) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) rb[i] = ldw(brow[i] + k0);
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(&sa[buf][(lr + 32 * i) * LROW + lc]) = ra[i];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) *reinterpret_cast<u32x4*>(&sb[buf][(lr + 32 * i) * LROW + lc]) = rb[i];
+  };
+
+  f32x16 acc[2];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[nb][r] = 0.0f;
+
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  const int arow_l = (32 * w + (lane & 31)) * LROW, brow_l = (lane & 31) * LROW, kh = 8 * (lane >> 5);
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) gload((kt + 1) * BK);
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      const int ko = 16 * kk + kh;
+      const bf16x8 av = as_bf8(*reinterpret_cast<const u32x4*>(&sa[buf][arow_l + ko]));
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const bf16x8 bv = as_bf8(*reinterpret_cast<const u32x4*>(&sb[buf][brow_l + 32 * nb * LROW + ko]));
+        acc[nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc[nb], 0, 0, 0);
+      }
+    }
+    if (kt + 1 < nk) sstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // D layout of a 32x32 block: lane column lane & 31; register r holds row
+  // 8 (r >> 2) + 4 (lane >> 5) + (r & 3)
+  const int col = lane & 31, hrow = 4 * (lane >> 5);
+  if (gridDim.z > 1) {
+    float* P = g.part + (size_t)blockIdx.z * g.M * g.N;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + 32 * w + 8 * (r >> 2) + hrow + (r & 3);
+        if (m < g.M) P[(size_t)m * g.N + n0 + 32 * nb + col] = acc[nb][r];
+      }
+    return;
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int m = m0 + 32 * w + 8 * (r >> 2) + hrow + (r & 3);
+    if (m >= g.M) continue;
+    if constexpr (EPI == E_SWIGLU) {
+      epilogue_swiglu(g, m, (n0 >> 1) + col, acc[0][r], acc[1][r]);
+    } else {
+      epilogue<EPI>(g, m, n0 + col, acc[0][r]);
+      epilogue<EPI>(g, m, n0 + 32 + col, acc[1][r]);
+    }
+  }
+}
+
+// Sum of the split-K partials in split order, then the GEMM's epilogue; one thread per output.
+template <int EPI>
+__global__ void __launch_bounds__(256) reduce_kernel(const GemmArgs g, int splits) {
+  const int nout = EPI == E_SWIGLU ? g.N / 2 : g.N;
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (long)g.M * nout) return;
+  const int m = (int)(idx / nout), j = (int)(idx % nout);
+  const size_t stride = (size_t)g.M * g.N;
+  const float* P = g.part + (size_t)m * g.N;
+  if constexpr (EPI == E_SWIGLU) {
+    const int nv = 64 * (j >> 5) + (j & 31);
+    float gs = 0.0f, us = 0.0f;
+    for (int z = 0; z < splits; ++z) {
+      gs += P[z * stride + nv];
+      us += P[z * stride + nv + 32];
+    }
+    epilogue_swiglu(g, m, j, gs, us);
+  } else {
+    float s = 0.0f;
+    for (int z = 0; z < splits; ++z) s += P[z * stride + j];
+    epilogue<EPI>(g, m, j, s);
+  }
+}
+
+// RMSNorm of M token rows (row stride ldx) into bf16 rows (stride ldo), one wave per token;
+// the gain comes from field `field` of layer `layer` of the device table, or `gain` when the
+// table is null. out_f32 (optional) receives the bf16 result widened to f32.
+__global__ void __launch_bounds__(256) rmsnorm_kernel(const bf16_t* x, int ldx, const TTSLayerWeights* layers,
+                                                      int layer, int field, const bf16_t* gain, bf16_t* out,
+                                                      int ldo, float* out_f32, int M) {
+  const int lane = threadIdx.x & 63;
+  const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= M) return;
+  const bf16_t* w = layers ? tbl(layers + layer, field) : gain;
+  const bf16_t* xr = x + (size_t)m * ldx;
+  u32x4 v[2];
+  float ss = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    v[k] = ldw(xr + 8 * (lane + 64 * k));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float a = bflo(v[k][e]), b = bfhi(v[k][e]);
+      ss += a * a + b * b;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  const float rs = 1.0f / sqrtf(ss / (float)HID + EPS);
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int e0 = 8 * (lane + 64 * k);
+    const u32x4 gw = ldw(w + e0);
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float a = rbf(bflo(gw[e]) * rbf(bflo(v[k][e]) * rs));
+      const float b = rbf(bfhi(gw[e]) * rbf(bfhi(v[k][e]) * rs));
+      o[e] = (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
+      if (out_f32) {
+        out_f32[e0 + 2 * e] = a;
+        out_f32[e0 + 2 * e + 1] = b;
+      }
+    }
+    if (out) *reinterpret_cast<u32x4*>(out + (size_t)m * ldo + e0) = o;
+  }
+}
+
+// Per token: q/k head RMSNorm (field 4 / 5 gains), interleaved mRoPE from the bf16 tables, q
+// written back in place, the rotated k and the v of every KV head written to the cache at
+// position p0 + s. Lane j of a wave handles channels j and j + 64 (the rotate_half pair).
+__global__ void __launch_bounds__(256) rope_kv_kernel(bf16_t* qkv, const TTSLayerWeights* layers, int layer,
+                                                      const bf16_t* cos_t, const bf16_t* sin_t, const int* pos3,
+                                                      int p0, int S, bf16_t* kc, bf16_t* vc, int max_seq) {
+  const int s = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int pos = p0 + s;
+  const int sec = (lane < 60 && lane % 3 == 1) ? 1 : ((lane < 60 && lane % 3 == 2) ? 2 : 0);
+  // table row of this channel's section (clamped into the table: a caller's out-of-range
+  // position must not read outside it)
+  const int row = pos3 ? min(max(pos3[sec * S + s], 0), max_seq - 1) : pos;
+  const float c0 = ldbf(cos_t + (size_t)row * HDIM + lane), c1 = ldbf(cos_t + (size_t)row * HDIM + lane + 64);
+  const float s0 = ldbf(sin_t + (size_t)row * HDIM + lane), s1 = ldbf(sin_t + (size_t)row * HDIM + lane + 64);
+  const TTSLayerWeights* lw = layers + layer;
+  const bf16_t* qn = tbl(lw, 4);
+  const bf16_t* kn = tbl(lw, 5);
+  bf16_t* src = qkv + (size_t)s * QKVW;
+  for (int hd = w; hd < NQH + NKVH; hd += 4) {
+    bf16_t* hp = src + hd * HDIM;
+    const float x0 = bf2f(hp[lane]), x1 = bf2f(hp[lane + 64]);
+    float ss = x0 * x0 + x1 * x1;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    const float rs = 1.0f / sqrtf(ss / (float)HDIM + EPS);
+    const bf16_t* gn = hd < NQH ? qn : kn;
+    const float y0 = rbf(ldbf(gn + lane) * rbf(x0 * rs));
+    const float y1 = rbf(ldbf(gn + lane + 64) * rbf(x1 * rs));
+    const bf16_t o0 = f2bf(rbf(y0 * c0) + rbf(-y1 * s0));
+    const bf16_t o1 = f2bf(rbf(y1 * c1) + rbf(y0 * s1));
+    if (hd < NQH) {
+      hp[lane] = o0;
+      hp[lane + 64] = o1;
+    } else {
+      bf16_t* dst = kc + (((size_t)layer * NKVH + (hd - NQH)) * max_seq + pos) * HDIM;
+      dst[lane] = o0;
+      dst[lane + 64] = o1;
+    }
+  }
+  // v: 8 heads x 128 = 1024 values, 4 per thread
+  const int i0 = 4 * threadIdx.x;
+  const int kvh = i0 >> 7, d = i0 & 127;
+  const u32x2 vv = *reinterpret_cast<const u32x2*>(src + 3072 + i0);
+  *reinterpret_cast<u32x2*>(vc + (((size_t)layer * NKVH + kvh) * max_seq + pos) * HDIM + d) = vv;
+}
+
+// Causal GQA attention of S queries (positions p0 .. p0 + S - 1) over cache positions
+// 0 .. p0 + S - 1, one wave per (32-query block, query head). MFMA 32x32x16 with A = K rows and
+// B = Q^T gives S^T: lane (half hf, column c) holds query 32 qb + c's scores for keys
+// 8 (r >> 2) + 4 hf + (r & 3), r < 16, of each 32-key block. O^T = V^T P^T reuses those score
+// registers as the B operand in place: k-index 8 hf + j of step kk2 is key
+// 16 kk2 + 8 (j >> 2) + 4 hf + (j & 3), and V^T (staged in LDS, [d][key]) is read in that order.
+__global__ void __launch_bounds__(64) attn_kernel(const bf16_t* qkv, const bf16_t* kc, const bf16_t* vc, int layer,
+                                                  int max_seq, int p0, int S, bf16_t* att, float scale) {
+  __shared__ __attribute__((aligned(16))) bf16_t vt[HDIM * VTROW];
+  const int lane = threadIdx.x, hf = lane >> 5, c = lane & 31;
+  const int qb = blockIdx.x, hq = blockIdx.y, kvh = hq >> 1;
+  const int i = 32 * qb + c;
+  const bool qok = i < S;
+  const int qpos = p0 + i;
+  const int last = p0 + min(S, 32 * qb + 32) - 1;   // last key any query of the block sees
+  const int nkb = last / 32 + 1;
+
+  u32x4 qr[8];
+  {
+    const bf16_t* qp = qkv + (size_t)(qok ? i : 0) * QKVW + hq * HDIM + 8 * hf;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) qr[kk] = qok ? ldw(qp + 16 * kk) : u32x4{0u, 0u, 0u, 0u};
+  }
+  const size_t hbase = ((size_t)layer * NKVH + kvh) * max_seq * HDIM;
+  const bf16_t* kb_ = kc + hbase;
+  const bf16_t* vb_ = vc + hbase;
+
+  auto scores = [&](int kb, float (&sc)[16]) {
+    const int key = 32 * kb + c;
+    const bool kok = key <= last;
+    const bf16_t* kp = kb_ + (size_t)(kok ? key : 0) * HDIM + 8 * hf;
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const u32x4 a = kok ? ldw(kp + 16 * kk) : u32x4{0u, 0u, 0u, 0u};
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(a), as_bf8(qr[kk]), acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kr = 32 * kb + 8 * (r >> 2) + 4 * hf + (r & 3);
+      const float v = rbf(rbf(acc[r]) * scale);
+      sc[r] = (qok && kr <= qpos) ? v : -INFINITY;
+    }
+  };
+
+  // pass 1: row maximum and softmax denominator (per lane over its keys, then the half-wave pair)
+  float m = -INFINITY, l = 0.0f;
+  for (int kb = 0; kb < nkb; ++kb) {
+    float sc[16];
+    scores(kb, sc);
+    float bm = sc[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) bm = fmaxf(bm, sc[r]);
+    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    // (no branch around the MFMAs: a fully masked block leaves m and l unchanged)
+    const float mn = fmaxf(m, bm);
+    float add = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) add += sc[r] == -INFINITY ? 0.0f : expf(sc[r] - mn);
+    l = m == -INFINITY ? add : l * expf(m - mn) + add;
+    m = mn;
+  }
+  l += __shfl_xor(l, 32, 64);
+
+  // pass 2: p = bf16(e / l), O^T += V^T P^T
+  f32x16 o[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[mb][r] = 0.0f;
+  const int kp2 = lane & 15, dg = 32 * (lane >> 4);
+  for (int kb = 0; kb < nkb; ++kb) {
+    float sc[16];
+    scores(kb, sc);
+    // stage V rows 2 kp2, 2 kp2 + 1 of the block, dims dg .. dg + 31, transposed into vt[d][key]
+    {
+      const int k0 = 32 * kb + 2 * kp2;
+      const bool ok0 = k0 <= last, ok1 = k0 + 1 <= last;
+      const bf16_t* v0 = vb_ + (size_t)(ok0 ? k0 : 0) * HDIM + dg;
+      const bf16_t* v1 = vb_ + (size_t)(ok1 ? k0 + 1 : 0) * HDIM + dg;
+#pragma unroll
+      for (int dd = 0; dd < 4; ++dd) {
+        const u32x4 a = ok0 ? ldw(v0 + 8 * dd) : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 b = ok1 ? ldw(v1 + 8 * dd) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int d = dg + 8 * dd + 2 * e;
+          *reinterpret_cast<uint32_t*>(&vt[d * VTROW + 2 * kp2]) = (a[e] & 0xffffu) | (b[e] << 16);
+          *reinterpret_cast<uint32_t*>(&vt[(d + 1) * VTROW + 2 * kp2]) = (a[e] >> 16) | (b[e] & 0xffff0000u);
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk2 = 0; kk2 < 2; ++kk2) {
+      u32x4 pb;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float e0 = sc[8 * kk2 + 2 * j] == -INFINITY ? 0.0f : expf(sc[8 * kk2 + 2 * j] - m) / l;
+        const float e1 = sc[8 * kk2 + 2 * j + 1] == -INFINITY ? 0.0f : expf(sc[8 * kk2 + 2 * j + 1] - m) / l;
+        pb[j] = (uint32_t)f2bf(e0) | ((uint32_t)f2bf(e1) << 16);
+      }
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        const bf16_t* vr = &vt[(32 * mb + c) * VTROW + 16 * kk2 + 4 * hf];
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(vr);
+        const u32x2 hi = *reinterpret_cast<const u32x2*>(vr + 8);
+        const u32x4 av = {lo[0], lo[1], hi[0], hi[1]};
+        o[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(av), as_bf8(pb), o[mb], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+  if (!qok) return;
+  // O^T layout: column = query c, register r of block mb = dim 32 mb + 8 (r >> 2) + 4 hf + (r & 3)
+  bf16_t* op = att + (size_t)i * (NQH * HDIM) + hq * HDIM;
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int rq = 0; rq < 4; ++rq) {
+      const int d0 = 32 * mb + 8 * rq + 4 * hf;
+      u32x2 pk;
+      pk[0] = (uint32_t)f2bf(o[mb][4 * rq]) | ((uint32_t)f2bf(o[mb][4 * rq + 1]) << 16);
+      pk[1] = (uint32_t)f2bf(o[mb][4 * rq + 2]) | ((uint32_t)f2bf(o[mb][4 * rq + 3]) << 16);
+      *reinterpret_cast<u32x2*>(op + d0) = pk;
+    }
+}
+
+// First group-0 token from bf16 logits: ids [n-1024, n) except EOS suppressed when mask_tail
+// (generator.py:71-75, :116), EOS suppressed when suppress_eos (min_new_tokens, :117-119), then
+// the decode kernels' selection (greedy argmax, or temperature / top-k / top-p / Gumbel-max).
+__global__ void __launch_bounds__(64) select_kernel(const bf16_t* logits, int n, int mask_tail, int eos_id,
+                                                    int suppress_eos, SelParams sp, float* out_logits,
+                                                    int* out_token) {
+  __shared__ float stage[MAXV];
+  __shared__ SelScratch sc;
+  const int lane = threadIdx.x;
+  for (int i = lane; i < n; i += 64) {
+    float v = bf2f(logits[i]);
+    if (out_logits) out_logits[i] = v;
+    if (mask_tail && i >= n - 1024 && i != eos_id) v = -INFINITY;
+    if (suppress_eos && i == eos_id) v = -INFINITY;
+    stage[i] = v;
+  }
+  __syncthreads();
+  const int tok = wave_select(stage, n, sp, &sc);
+  if (lane == 0) *out_token = tok;
+}
+
+// ---- host ----------------------------------------------------------------------------------
+
+struct Shape { int N, K; };
+constexpr Shape kQKV{4096, HID}, kO{HID, NQH * HDIM}, kGU{2 * INTER, HID}, kDown{HID, INTER};
+
+// split-K factor: double while the tile grid is below 256 workgroups and the K range still
+// splits into whole 64-wide steps
+int splits_for(int M, int N, int K) {
+  const int tiles = ((M + BM - 1) / BM) * (N / BN);
+  int ks = 1;
+  while (tiles * ks < 256 && ks < MAX_SPLIT && (K / BK) % (2 * ks) == 0) ks *= 2;
+  return ks;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct Layout {
+  size_t h, xn, qkv, att, act, hb, logits, part, total;
+};
+
+Layout layout(int S, int vocab) {
+  Layout L;
+  size_t o = 0;
+  auto take = [&](size_t bytes) { const size_t at = o; o = align256(o + bytes); return at; };
+  L.h = take((size_t)S * HID * 2);
+  L.xn = take((size_t)S * HID * 2);
+  L.qkv = take((size_t)S * QKVW * 2);
+  L.att = take((size_t)S * NQH * HDIM * 2);
+  L.act = take((size_t)S * INTER * 2);
+  L.hb = take(HID * 2);
+  L.logits = take((size_t)(vocab > 0 ? vocab : MAXV) * 2);
+  size_t pb = 0;
+  for (Shape sh : {kQKV, kO, kGU, kDown}) {
+    const int ks = splits_for(S, sh.N, sh.K);
+    if (ks > 1) pb = std::max(pb, (size_t)ks * S * sh.N * 4);
+  }
+  const int ksh = splits_for(1, vocab > 0 ? vocab : MAXV, HID);
+  if (ksh > 1) pb = std::max(pb, (size_t)ksh * (vocab > 0 ? vocab : MAXV) * 4);
+  L.part = take(pb);
+  L.total = o;
+  return L;
+}
+
+template <int WM, int EPI>
+hipError_t gemm(GemmArgs g, hipStream_t st) {
+  const int ks = splits_for(g.M, g.N, g.K);
+  g.kchunk = g.K / ks;
+  dim3 grid(g.N / BN, (g.M + BM - 1) / BM, ks);
+  hipLaunchKernelGGL((gemm_kernel<WM, EPI>), grid, dim3(GT), 0, st, g);
+  if (ks > 1) {
+    const long nout = (long)g.M * (EPI == E_SWIGLU ? g.N / 2 : g.N);
+    hipLaunchKernelGGL((reduce_kernel<EPI>), dim3((unsigned)((nout + 255) / 256)), dim3(256), 0, st, g, ks);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace pf
+}  // namespace qtts
+
+using namespace qtts;
+using namespace qtts::pf;
+
+extern "C" {
+
+size_t qtts_prefill_workspace_bytes(int n_tokens, int vocab) {
+  if (n_tokens < 1 || vocab < 0 || vocab > MAXV) return 0;
+  return layout(n_tokens, vocab).total;
+}
+
+hipError_t qtts_backbone_prefill(void* workspace, size_t workspace_bytes, const TTSLayerWeights* layer_weights,
+                                 int num_layers, const void* final_norm_weight, const void* cos_table,
+                                 const void* sin_table, void* k_cache, void* v_cache, int max_seq_len, int position,
+                                 int n_tokens, const int* pos3, const void* input_embeddings, float* out_hidden,
+                                 const void* codec_head, int vocab, float* out_logits, int* out_token, int mask_tail,
+                                 int eos_id, int suppress_eos, const QttsSampling* sampling, int frame_step,
+                                 hipStream_t stream) {
+  const int S = n_tokens;
+  if (workspace == nullptr || layer_weights == nullptr || final_norm_weight == nullptr || cos_table == nullptr ||
+      sin_table == nullptr || k_cache == nullptr || v_cache == nullptr || input_embeddings == nullptr)
+    return hipErrorInvalidValue;
+  if (num_layers < 1 || S < 1 || position < 0 || max_seq_len < 1 || position + S > max_seq_len)
+    return hipErrorInvalidValue;
+  if (codec_head != nullptr && (vocab < BN || vocab > MAXV || vocab % BN != 0 || out_token == nullptr))
+    return hipErrorInvalidValue;
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0 || (reinterpret_cast<uintptr_t>(input_embeddings) & 15u) != 0)
+    return hipErrorInvalidValue;
+  const Layout L = layout(S, codec_head ? vocab : 0);
+  if (workspace_bytes < L.total) return hipErrorInvalidValue;
+  char* ws = static_cast<char*>(workspace);
+  bf16_t* h = reinterpret_cast<bf16_t*>(ws + L.h);
+  bf16_t* xn = reinterpret_cast<bf16_t*>(ws + L.xn);
+  bf16_t* qkv = reinterpret_cast<bf16_t*>(ws + L.qkv);
+  bf16_t* att = reinterpret_cast<bf16_t*>(ws + L.att);
+  bf16_t* act = reinterpret_cast<bf16_t*>(ws + L.act);
+  bf16_t* hb = reinterpret_cast<bf16_t*>(ws + L.hb);
+  float* part = reinterpret_cast<float*>(ws + L.part);
+  auto* kc = static_cast<bf16_t*>(k_cache);
+  auto* vc = static_cast<bf16_t*>(v_cache);
+  const auto* cs = static_cast<const bf16_t*>(cos_table);
+  const auto* sn = static_cast<const bf16_t*>(sin_table);
+  const float scale = 1.0f / sqrtf((float)HDIM);
+  const unsigned norm_grid = (unsigned)((S + 3) / 4);
+
+  hipError_t e = hipMemcpyAsync(h, input_embeddings, (size_t)S * HID * 2, hipMemcpyDeviceToDevice, stream);
+  if (e != hipSuccess) return e;
+  for (int l = 0; l < num_layers; ++l) {
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(norm_grid), dim3(256), 0, stream, h, HID, layer_weights, l, 0,
+                       (const bf16_t*)nullptr, xn, HID, (float*)nullptr, S);
+    GemmArgs g{};
+    g.layers = layer_weights;
+    g.layer = l;
+    g.M = S;
+    g.part = part;
+    g.A = xn; g.lda = HID; g.N = kQKV.N; g.K = kQKV.K; g.out = qkv; g.ldo = QKVW;
+    if ((e = gemm<W_QKV, E_STORE>(g, stream)) != hipSuccess) return e;
+    hipLaunchKernelGGL(rope_kv_kernel, dim3(S), dim3(256), 0, stream, qkv, layer_weights, l, cs, sn, pos3, position, S,
+                       kc, vc, max_seq_len);
+    hipLaunchKernelGGL(attn_kernel, dim3((S + 31) / 32, NQH), dim3(64), 0, stream, qkv, kc, vc, l, max_seq_len,
+                       position, S, att, scale);
+    g.A = att; g.lda = NQH * HDIM; g.N = kO.N; g.K = kO.K; g.out = h; g.ldo = HID; g.res = h; g.ldr = HID;
+    if ((e = gemm<W_O, E_RESID>(g, stream)) != hipSuccess) return e;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(norm_grid), dim3(256), 0, stream, h, HID, layer_weights, l, 7,
+                       (const bf16_t*)nullptr, xn, HID, (float*)nullptr, S);
+    g.A = xn; g.lda = HID; g.N = kGU.N; g.K = kGU.K; g.out = act; g.ldo = INTER; g.res = nullptr;
+    if ((e = gemm<W_GU, E_SWIGLU>(g, stream)) != hipSuccess) return e;
+    g.A = act; g.lda = INTER; g.N = kDown.N; g.K = kDown.K; g.out = h; g.ldo = HID; g.res = h; g.ldr = HID;
+    if ((e = gemm<W_DOWN, E_RESID>(g, stream)) != hipSuccess) return e;
+  }
+  // final norm of the last token -> hidden (bf16 values; f32 copy for the caller)
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(256), 0, stream, h + (size_t)(S - 1) * HID, HID,
+                     (const TTSLayerWeights*)nullptr, 0, 0, static_cast<const bf16_t*>(final_norm_weight), hb, HID,
+                     out_hidden, 1);
+  if (codec_head != nullptr) {
+    bf16_t* lg = reinterpret_cast<bf16_t*>(ws + L.logits);
+    GemmArgs g{};
+    g.A = hb; g.lda = HID; g.B = static_cast<const bf16_t*>(codec_head); g.M = 1; g.N = vocab; g.K = HID;
+    g.out = lg; g.ldo = vocab; g.part = part;
+    if ((e = gemm<W_DIRECT, E_STORE>(g, stream)) != hipSuccess) return e;
+    SelParams sp{};
+    sp.do_sample = sampling ? sampling->do_sample : 0;
+    sp.temperature = sampling ? sampling->temperature : 1.0f;
+    sp.top_k = sampling ? sampling->top_k : 0;
+    sp.top_p = sampling ? sampling->top_p : 1.0f;
+    sp.seed = sampling ? sampling->seed : 0ull;
+    sp.frame_step = frame_step;
+    sp.group = 0;
+    hipLaunchKernelGGL(select_kernel, dim3(1), dim3(64), 0, stream, lg, vocab, mask_tail, eos_id, suppress_eos, sp,
+                       out_logits, out_token);
+  }
+  return hipGetLastError();
+}
+
+}  // extern "C"

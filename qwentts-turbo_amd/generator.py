@@ -13,8 +13,11 @@ The host enqueues frames without waiting and checks the EOS flag every ``sync_ev
 Differences (by design):
   * sampling draws with Gumbel-max over Philox-4x64-10 noise instead of torch.multinomial
     (same distribution; reproducible on device). Greedy decoding is unchanged.
-  * the prefill runs the backbone decode kernel token by token (kernel precision), not the
-    qwen_tts PyTorch forward; ``attention_mask`` must therefore be all ones.
+  * the prefill (:209-225) and the KV handoff (:245-257) are one ``qtts_backbone_prefill`` call:
+    the transformers bf16 forward of the whole prompt on MFMA, K/V written straight into the
+    decode cache, and the first group-0 token selected from its codec-head logits on device
+    (``prefill="mfma"``, default). ``prefill="steps"`` instead steps the decode kernel token by
+    token (kernel precision). ``attention_mask`` must be all ones (batch 1, no padding).
   * only the megakernel backends exist (``backend="pytorch"`` needs qwen_tts, which this
     build does not ship).
 """
@@ -76,8 +79,10 @@ class NativeTTSGenerator:
     def generate(self, talker_input_embeds, attention_mask, trailing_text_hidden, tts_pad_embed, max_tokens=500,
                  do_sample=False, temperature=0.9, top_k=50, top_p=1.0, cp_do_sample=False, cp_temperature=0.9,
                  cp_top_k=50, min_new_tokens=2, repetition_penalty=1.0, *, seed: int = 0,
-                 sync_every: int = 8) -> List[List[int]]:
+                 sync_every: int = 8, prefill: str = "mfma") -> List[List[int]]:
         """Run the generation loop; returns one [16] codec id list per frame (generator.py:77-176)."""
+        if prefill not in ("mfma", "steps"):
+            raise ValueError(f"prefill={prefill!r}: 'mfma' or 'steps'")
         dev = self.device
         bb, cp = self.backbone_mega.decoder, self.cp_mega.decoder
         emb = talker_input_embeds
@@ -101,11 +106,15 @@ class NativeTTSGenerator:
 
         # 1. prefill (positions 0..seq-1) and the first group-0 token
         bb.reset()
-        for i in range(seq - 1):
-            bb.decode_step_with_embedding(emb[i])
-        bb.decode_step_select(emb[seq - 1], g0, hist, 0, float(repetition_penalty), self.eos_token_id,
-                              min_new_tokens > 0, bool(do_sample), float(temperature), int(top_k), float(top_p),
-                              int(seed), 0)
+        if prefill == "mfma":
+            bb.prefill(emb, g0, self.eos_token_id, min_new_tokens > 0, bool(do_sample), float(temperature),
+                       int(top_k), float(top_p), int(seed))
+        else:
+            for i in range(seq - 1):
+                bb.decode_step_with_embedding(emb[i])
+            bb.decode_step_select(emb[seq - 1], g0, hist, 0, float(repetition_penalty), self.eos_token_id,
+                                  min_new_tokens > 0, bool(do_sample), float(temperature), int(top_k), float(top_p),
+                                  int(seed), 0)
         hidden = bb.hidden_state_buffer()
 
         # 2. frame loop, queued on the device; EOS checked every sync_every frames

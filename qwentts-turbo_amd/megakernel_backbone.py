@@ -86,6 +86,14 @@ class TTSMegakernelGenerator:
             return self.decoder.decode_step_with_embedding(input_embedding)
         return self.decoder.decode_step_3d(input_embedding, [int(p) for p in pos3])
 
+    def prefill(self, embeds: torch.Tensor, pos3=None) -> torch.Tensor:
+        """All prompt embeddings ([S, 1024] or [1, S, 1024]) in one call at positions
+        position .. position + S - 1: the transformers bf16 forward on MFMA with K/V written into
+        this decoder's cache (replaces generator.py:209-225 plus the KV handoff :245-257).
+        Returns the last token's final-norm hidden (f32 [1024]). ``pos3``: optional [3, S]
+        rotary (t, h, w) positions."""
+        return self.decoder.prefill(embeds, pos3=pos3)
+
     def reset(self):
         self.decoder.reset()
 

@@ -88,7 +88,9 @@ def test_c2_greedy_64_frames(c2_gen):
     fx = cases.load("c2_frames")
     prefill, trailing, pad = cases.c2_inputs()
     n = cases.C2_GREEDY_FRAMES
-    frames = c2_gen.generate(prefill, None, trailing, pad, max_tokens=n, min_new_tokens=n)
+    # the fixture pins the decode loop at kernel precision: the prompt is stepped through the
+    # decode kernel, as the oracle steps it
+    frames = c2_gen.generate(prefill, None, trailing, pad, max_tokens=n, min_new_tokens=n, prefill="steps")
     got = np.array(frames, dtype=np.int32)
     first_diff = next((i for i in range(min(len(got), len(fx["greedy"]))) if (got[i] != fx["greedy"][i]).any()), None)
     _print(f"c2 greedy: {len(frames)} frames, first differing frame {first_diff}")
@@ -102,7 +104,8 @@ def test_c2_sampled_frames(c2_gen):
     s = cases.C2_SAMPLING
     frames = c2_gen.generate(prefill, None, trailing, pad, max_tokens=n, do_sample=s["do_sample"],
                              temperature=s["temperature"], top_k=s["top_k"], top_p=s["top_p"],
-                             repetition_penalty=s["repetition_penalty"], min_new_tokens=n, seed=s["seed"])
+                             repetition_penalty=s["repetition_penalty"], min_new_tokens=n, seed=s["seed"],
+                             prefill="steps")
     got = np.array(frames, dtype=np.int32)
     first_diff = next((i for i in range(min(len(got), len(fx["sampled"]))) if (got[i] != fx["sampled"][i]).any()), None)
     _print(f"c2 sampled: {len(frames)} frames, first differing frame {first_diff}")
@@ -124,3 +127,20 @@ def test_c3_long_context_mrope(pkg):
     bb.check_error()
     _print(f"c3 L={cases.C3_KV + cases.C3_STEPS} mRoPE: worst hidden rel_l2 {worst:.2e}")
     assert worst < TOL
+
+
+def test_c2_generate_with_mfma_prefill(c2_gen):
+    """generate() with its default one-call MFMA prefill: the first frame's group 0 is the token
+    that prefill selects from the prompt (bf16 forward, suppress mask, EOS removed), every frame
+    holds 16 in-range ids, and the frame count is max_tokens while EOS stays suppressed."""
+    prefill, trailing, pad = cases.c2_inputs()
+    n = 6
+    frames = c2_gen.generate(prefill, None, trailing, pad, max_tokens=n, min_new_tokens=n)
+    assert len(frames) == n and all(len(f) == 16 for f in frames)
+    assert all(0 <= t < 3072 for f in frames for t in f)
+    bb = c2_gen.backbone_mega.decoder
+    bb.reset()
+    tok = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    bb.prefill(prefill[0].cuda(), tok, cases.EOS_ID, True)
+    _print(f"mfma prefill generate: first frame {frames[0][:4]}..., prefill token {int(tok.item())}")
+    assert frames[0][0] == int(tok.item())

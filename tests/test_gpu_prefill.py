@@ -1,0 +1,131 @@
+"""GPU parity of the MFMA prefill (qtts_backbone_prefill) against the oracle's transformers-bf16
+policy (``hf_bf16``, the reference's PyTorch prefill, generator.py:209-225) stepped token by token:
+the K/V cache entries of every prompt position and the last token's final-norm hidden.
+
+Tolerance: both sides store bf16 after every op; the GPU's f32 sums run in MFMA order, so a sum
+occasionally rounds to the neighbouring bf16 value, and each such flip perturbs the next op's
+sums and flips a few percent of its outputs. The spread therefore grows with depth. The bar is
+the north star's rel-L2 <= 1e-2 (TOL) for the 2-layer cases. For 28 layers the oracle's own
+spread between torch's f32 sums and f64 sums (same rounding points, ``hf_sums="f64"``) is
+already above 1e-2, so there the GPU is held to max(TOL, FLOOR_X x that spread): no further
+from the oracle than a second valid summation order is.
+"""
+import pytest
+import torch
+
+from oracle.qtts_oracle import DecoderOracle, TalkerWeights, rel_l2, suppress_mask
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+FLOOR_X = 2.0
+EOS = 2150
+
+
+def _print(*a):
+    print(*a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def small(pkg):
+    cfg = pkg.SyntheticConfig(n_bb_layers=2, n_cp_layers=1, n_groups=1)
+    sd = pkg.synthetic_state_dict(seed=21, cfg=cfg)
+    return {k: v.cuda() for k, v in sd.items()}, TalkerWeights.from_state_dict(sd, 2, 1)
+
+
+def _compare(bb, orc, p0, S, hidden, hidden_ref, label, bars=(TOL, TOL, TOL)):
+    L = p0 + S
+    ek = rel_l2(bb.get_k_cache()[:, :, p0:L].float().cpu(), orc.k[:, :, p0:L].float())
+    ev = rel_l2(bb.get_v_cache()[:, :, p0:L].float().cpu(), orc.v[:, :, p0:L].float())
+    eh = rel_l2(hidden.cpu(), hidden_ref)
+    _print(f"{label}: K rel_l2 {ek:.2e}, V {ev:.2e}, hidden {eh:.2e} (bars {bars[0]:.2e} {bars[1]:.2e} {bars[2]:.2e})")
+    assert ek < bars[0] and ev < bars[1] and eh < bars[2]
+    return eh
+
+
+@pytest.mark.parametrize("S", [1, 7, 64, 130, 333])
+def test_prefill_two_layers(pkg, small, S):
+    """Prompt lengths across the tile edges: one token, a partial 32-query block, exactly two
+    blocks, a partial 128-row GEMM tile, several tiles with a ragged last one."""
+    dsd, tw = small
+    bb = pkg.TTSMegakernelGenerator(model=dsd, max_seq_len=512)
+    orc = DecoderOracle(tw.bb_layers, tw.bb_norm, 512, "backbone", "hf_bf16")
+    x = torch.randn(S, 1024, generator=torch.Generator().manual_seed(100 + S)).to(torch.bfloat16)
+    _print(f"prefill 2 layers S={S}: launching")
+    h = bb.prefill(x.cuda())
+    torch.cuda.synchronize()
+    hr = None
+    for i in range(S):
+        hr, _ = orc.step(x[i], pos=i)
+    _compare(bb, orc, 0, S, h, hr, f"prefill 2 layers S={S}")
+    assert bb.position == S
+
+
+def test_prefill_after_prefix_and_distinct_mrope(pkg, small):
+    """A prompt continuing a cached prefix (positions 50..149 attend 0..149) with distinct
+    (t, h, w) rotary rows per token."""
+    dsd, tw = small
+    p0, S = 50, 100
+    bb = pkg.TTSMegakernelGenerator(model=dsd, max_seq_len=512)
+    orc = DecoderOracle(tw.bb_layers, tw.bb_norm, 512, "backbone", "hf_bf16")
+    g = torch.Generator().manual_seed(77)
+    k = torch.randn(2, 8, p0, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(2, 8, p0, 128, generator=g).to(torch.bfloat16)
+    bb.set_kv_cache(k.cuda(), v.cuda())
+    bb.set_position(p0)
+    orc.set_kv(k, v)
+    x = torch.randn(S, 1024, generator=g).to(torch.bfloat16)
+    pos = torch.arange(p0, p0 + S)
+    pos3 = torch.stack([pos, pos // 2 + 7, pos // 3 + 11]).to(torch.int32)
+    _print("prefill after a 50-position prefix, distinct mRoPE rows: launching")
+    h = bb.prefill(x.cuda(), pos3=pos3.cuda())
+    torch.cuda.synchronize()
+    hr = None
+    for i in range(S):
+        hr, _ = orc.step(x[i], pos=p0 + i, pos3=[int(pos3[j, i]) for j in range(3)])
+    _compare(bb, orc, p0, S, h, hr, "prefill after prefix, mRoPE")
+    assert bb.position == p0 + S
+
+
+def test_prefill_full_model_and_first_token(pkg):
+    """All 28 layers at a 40-token prompt, then the first group-0 token (greedy, suppress mask,
+    EOS removed) from the bf16 codec-head logits, as generate() uses it."""
+    sd = pkg.synthetic_state_dict(seed=1234)
+    dsd = {k: v.cuda() for k, v in sd.items()}
+    tw = TalkerWeights.from_state_dict(sd, 28, 5)
+    S = 40
+    bb = pkg.TTSMegakernelGenerator(model=dsd, max_seq_len=256)
+    orc = DecoderOracle(tw.bb_layers, tw.bb_norm, 256, "backbone", "hf_bf16")
+    x = torch.randn(S, 1024, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
+    tok = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    _print("prefill 28 layers S=40: launching")
+    h = bb.decoder.prefill(x.cuda(), tok, EOS, True)
+    torch.cuda.synchronize()
+    hr = None
+    for i in range(S):
+        hr, _ = orc.step(x[i], pos=i)
+    # the oracle's own summation-order spread over the same 28 layers
+    alt = DecoderOracle(tw.bb_layers, tw.bb_norm, 256, "backbone", "hf_bf16", hf_sums="f64")
+    ha = None
+    for i in range(S):
+        ha, _ = alt.step(x[i], pos=i)
+    fk = rel_l2(alt.k[:, :, :S].float(), orc.k[:, :, :S].float())
+    fv = rel_l2(alt.v[:, :, :S].float(), orc.v[:, :, :S].float())
+    fh = rel_l2(ha, hr)
+    _print(f"oracle f32-vs-f64 sums spread: K {fk:.2e}, V {fv:.2e}, hidden {fh:.2e}")
+    bars = tuple(max(TOL, FLOOR_X * f) for f in (fk, fv, fh))
+    _compare(bb, orc, 0, S, h, hr, "prefill 28 layers S=40", bars)
+    # logits: bf16(W_head . bf16 hidden) (generator.py:116), against the oracle's hidden
+    lref = torch.nn.functional.linear(hr.to(torch.bfloat16), tw.codec_head.to(torch.bfloat16)).float()
+    lg = bb.decoder.logits_buffer().cpu()
+    el = rel_l2(lg, lref)
+    _print(f"logits rel_l2 {el:.2e}")
+    assert el < bars[2]
+    # selection on the GPU's logits: suppress mask (generator.py:71-75) and EOS removed (:117),
+    # greedy argmax with the lowest index on ties -- exact
+    m = lg.clone()
+    m[suppress_mask(m.numel(), EOS)] = -float("inf")
+    m[EOS] = -float("inf")
+    t = int(tok.item())
+    _print(f"first token {t} (argmax of the masked GPU logits {int(m.argmax())})")
+    assert t == int(m.argmax())
