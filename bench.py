@@ -99,6 +99,47 @@ def cpu_baseline(sample_seconds: float = 15.0) -> dict:
                       f"PyTorch oracle) in {el:.1f} s"}
 
 
+def prefill_flops(S: int) -> int:
+    """Algorithmic flops of the MFMA prefill of S tokens: 2 per weight element per token for the
+    28 layers' projections, plus the causal attention products Q K^T and P V (S (S + 1) / 2
+    query-key pairs x 128 dims x 2 products x 2 flops, 16 heads), plus the codec head of the
+    last token."""
+    proj = 2 * 15_728_640 * 28 * S
+    attn = 2 * 2 * 128 * 16 * 28 * (S * (S + 1) // 2)
+    return proj + attn + 2 * 3072 * 1024
+
+
+def prefill_figures(bbg, reps: int = 5) -> dict:
+    """The MFMA prefill (qtts_backbone_prefill, prompt through all 28 layers + first-token
+    selection) at S = 128 (config 0's prompt) and S = 2048, timed with HIP events; roofline
+    against HBM (weights read once: 887 MB + the KV written) at S = 128 and against dense bf16
+    MFMA (2.5 PFLOP/s) at S = 2048."""
+    import torch
+    out = {}
+    tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    g = torch.Generator(device="cuda").manual_seed(11)
+    for S in (128, 2048):
+        x = torch.randn(S, 1024, generator=g, device="cuda").to(torch.bfloat16)
+        for _ in range(2):
+            bbg.decoder.set_position(0)
+            bbg.decoder.prefill(x, tok, -1, False)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            bbg.decoder.set_position(0)
+            bbg.decoder.prefill(x, tok, -1, False)
+        e1.record()
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) / reps * 1e-3
+        bytes_ = W_BB + KV_BB * S
+        fl = prefill_flops(S)
+        out[f"S{S}"] = {"ms": round(t * 1e3, 3), "tokens_per_s": round(S / t, 1),
+                        "hbm_gbs": round(bytes_ / t / 1e9, 1), "hbm_frac": round(bytes_ / t / 1e9 / HBM_PEAK_GBS, 4),
+                        "tflops": round(fl / t / 1e12, 1), "mfma_frac": round(fl / t / 1e12 / 2500.0, 4)}
+    bbg.decoder.check_error()
+    return out
+
+
 def batched_c4(pkg, sd, frames: int = 10) -> dict:
     """Config 4: 8 independent streams with ragged attended lengths in [128, 1024]; one frame =
     per stream one backbone step (head + greedy g0) and one code-predictor frame."""
@@ -142,6 +183,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-batched", action="store_true", help="skip the batch-8 ragged-context figure")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the MFMA prefill figures")
+    ap.add_argument("--prefill-only", action="store_true", help="only the MFMA prefill figures (one JSON line)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device-to-device copies of MIB MiB (the reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes) and exit")
@@ -169,6 +212,9 @@ def main():
 
     sd = pkg.synthetic_state_dict(seed=1234, device="cuda")
     bbg = pkg.TTSMegakernelGenerator(model=sd, max_seq_len=4096)
+    if args.prefill_only:
+        print(json.dumps({"prefill": prefill_figures(bbg)}), flush=True)
+        return
     cpg = pkg.CodePredictorMegakernelGenerator(model=sd, max_seq_len=32)
     bb, cp = bbg.decoder, cpg.decoder
     g = torch.Generator(device="cuda").manual_seed(5)
@@ -252,6 +298,8 @@ def main():
     }
     if not args.no_batched:
         out["batched_c4"] = batched_c4(pkg, sd)
+    if not args.no_prefill:
+        out["prefill"] = prefill_figures(bbg)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)

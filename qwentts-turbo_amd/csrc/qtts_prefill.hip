@@ -25,10 +25,11 @@
 //                    reduce_kernel); epilogues: store, residual add, SwiGLU (gate and up rows
 //                    interleaved by 32 in one tile)
 //   rope_kv_kernel   q/k RMSNorm + interleaved mRoPE, K/V cache write, one workgroup per token
-//   attn_kernel      causal GQA, one wave per (32-query block, query head): S^T = K Q^T on
-//                    MFMA (each lane then holds one query's scores, so the row max and sum
-//                    stay in the lane and its partner half-wave), two passes (row max / sum,
-//                    then p = bf16(e / l) and O^T = V^T P^T on MFMA with V^T staged in LDS)
+//   attn_kernel      causal GQA, 4 waves per (32-query block, query head) splitting the key
+//                    blocks: S^T = K Q^T on MFMA (each lane then holds one query's scores, so
+//                    the row max and sum stay in the lane and its partner half-wave), two passes
+//                    (row max / sum, then p = bf16(e * (1 / l)) and O^T = V^T P^T on MFMA with V^T
+//                    staged in LDS), partials merged in wave order
 //   select_kernel    suppress mask + EOS suppression + the decode kernels' wave_select
 #include <hip/hip_runtime.h>
 #include <algorithm>
@@ -136,18 +137,20 @@ __global__ void __launch_bounds__(GT) gemm_kernel(const GemmArgs g) {
     arow[i] = g.A + (size_t)(aok[i] ? m : 0) * g.lda + kbeg + lc;
   }
 
-  u32x4 ra[4], rb[2];
-  auto gload = [&](int k0) {
+  // register stages two tiles ahead of the MFMAs (tile kt + 2 loads while tile kt computes and
+  // tile kt + 1 moves to LDS): twice the weight bytes in flight of a plain double buffer
+  u32x4 ra[2][4], rb[2][2];
+  auto gload = [&](int k0, u32x4 (&a)[4], u32x4 (&b)[2]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ra[i] = aok[i] ? ldw(arow[i] + k0) : u32x4{0u, 0u, 0u, 0u};
+    for (int i = 0; i < 4; ++i) a[i] = aok[i] ? ldw(arow[i] + k0) : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int i = 0; i < 2; ++i) rb[i] = ldw(brow[i] + k0);
+    for (int i = 0; i < 2; ++i) b[i] = ldw(brow[i] + k0);
   };
-  auto sstore = [&](int buf) {
+  auto sstore = [&](int buf, const u32x4 (&a)[4], const u32x4 (&b)[2]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(&sa[buf][(lr + 32 * i) * LROW + lc]) = ra[i];
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(&sa[buf][(lr + 32 * i) * LROW + lc]) = a[i];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) *reinterpret_cast<u32x4*>(&sb[buf][(lr + 32 * i) * LROW + lc]) = rb[i];
+    for (int i = 0; i < 2; ++i) *reinterpret_cast<u32x4*>(&sb[buf][(lr + 32 * i) * LROW + lc]) = b[i];
   };
 
   f32x16 acc[2];
@@ -156,13 +159,8 @@ __global__ void __launch_bounds__(GT) gemm_kernel(const GemmArgs g) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[nb][r] = 0.0f;
 
-  gload(0);
-  sstore(0);
-  __syncthreads();
   const int arow_l = (32 * w + (lane & 31)) * LROW, brow_l = (lane & 31) * LROW, kh = 8 * (lane >> 5);
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) gload((kt + 1) * BK);
+  auto compute = [&](int buf) {
 #pragma unroll
     for (int kk = 0; kk < BK / 16; ++kk) {
       const int ko = 16 * kk + kh;
@@ -173,8 +171,22 @@ __global__ void __launch_bounds__(GT) gemm_kernel(const GemmArgs g) {
         acc[nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc[nb], 0, 0, 0);
       }
     }
-    if (kt + 1 < nk) sstore(buf ^ 1);
+  };
+  // one step: tile kt in LDS buffer kt & 1, tile kt + 1 in register stage S1, stage S0 free
+  auto step = [&](int kt, u32x4 (&a0)[4], u32x4 (&b0)[2], const u32x4 (&a1)[4], const u32x4 (&b1)[2]) {
+    if (kt + 2 < nk) gload((kt + 2) * BK, a0, b0);
+    compute(kt & 1);
+    if (kt + 1 < nk) sstore((kt + 1) & 1, a1, b1);
     __syncthreads();
+  };
+
+  gload(0, ra[0], rb[0]);
+  if (nk > 1) gload(BK, ra[1], rb[1]);
+  sstore(0, ra[0], rb[0]);
+  __syncthreads();
+  for (int kt = 0; kt < nk; kt += 2) {
+    step(kt, ra[0], rb[0], ra[1], rb[1]);
+    if (kt + 1 < nk) step(kt + 1, ra[1], rb[1], ra[0], rb[0]);
   }
 
   // D layout of a 32x32 block: lane column lane & 31; register r holds row
@@ -319,21 +331,31 @@ __global__ void __launch_bounds__(256) rope_kv_kernel(bf16_t* qkv, const TTSLaye
 }
 
 // Causal GQA attention of S queries (positions p0 .. p0 + S - 1) over cache positions
-// 0 .. p0 + S - 1, one wave per (32-query block, query head). MFMA 32x32x16 with A = K rows and
-// B = Q^T gives S^T: lane (half hf, column c) holds query 32 qb + c's scores for keys
-// 8 (r >> 2) + 4 hf + (r & 3), r < 16, of each 32-key block. O^T = V^T P^T reuses those score
-// registers as the B operand in place: k-index 8 hf + j of step kk2 is key
-// 16 kk2 + 8 (j >> 2) + 4 hf + (j & 3), and V^T (staged in LDS, [d][key]) is read in that order.
-__global__ void __launch_bounds__(64) attn_kernel(const bf16_t* qkv, const bf16_t* kc, const bf16_t* vc, int layer,
-                                                  int max_seq, int p0, int S, bf16_t* att, float scale) {
-  __shared__ __attribute__((aligned(16))) bf16_t vt[HDIM * VTROW];
-  const int lane = threadIdx.x, hf = lane >> 5, c = lane & 31;
-  const int qb = blockIdx.x, hq = blockIdx.y, kvh = hq >> 1;
+// 0 .. p0 + S - 1, one workgroup of AW waves per (32-query block, query head); wave w takes the
+// 32-key blocks kb = w, w + AW, ... MFMA 32x32x16 with A = K rows and B = Q^T gives S^T: lane
+// (half hf, column c) holds query 32 qb + c's scores for keys 8 (r >> 2) + 4 hf + (r & 3), r < 16,
+// of each block, so a query's row max and sum stay in the lane and its partner half-wave. The
+// waves' (max, sum) pairs merge through LDS in wave order; pass 2 forms p = bf16(e * (1 / l)) and
+// O^T = V^T P^T, reusing the score registers as the B operand in place (k-index 8 hf + j of step
+// kk2 is key 16 kk2 + 8 (j >> 2) + 4 hf + (j & 3); each wave's V^T block is staged in its own LDS
+// rows [d][key] and read in that order). The AW partial O^T are added in wave order by wave 0.
+// Query blocks are issued last-first: the longest rows start earliest.
+constexpr int AW = 4;
+constexpr int ATT_SMEM = std::max(AW * HDIM * VTROW * 2, (AW - 1) * HDIM * 32 * 4);
+
+__global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, const bf16_t* kc, const bf16_t* vc,
+                                                       int layer, int max_seq, int p0, int S, bf16_t* att,
+                                                       float scale) {
+  __shared__ __attribute__((aligned(16))) char smem[ATT_SMEM];
+  __shared__ float sml[AW][2][32];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hf = lane >> 5, c = lane & 31;
+  const int qb = gridDim.x - 1 - blockIdx.x, hq = blockIdx.y, kvh = hq >> 1;
   const int i = 32 * qb + c;
   const bool qok = i < S;
   const int qpos = p0 + i;
   const int last = p0 + min(S, 32 * qb + 32) - 1;   // last key any query of the block sees
   const int nkb = last / 32 + 1;
+  bf16_t* vt = reinterpret_cast<bf16_t*>(smem) + w * HDIM * VTROW;
 
   u32x4 qr[8];
   {
@@ -365,9 +387,9 @@ __global__ void __launch_bounds__(64) attn_kernel(const bf16_t* qkv, const bf16_
     }
   };
 
-  // pass 1: row maximum and softmax denominator (per lane over its keys, then the half-wave pair)
+  // pass 1: this wave's row maximum and softmax denominator
   float m = -INFINITY, l = 0.0f;
-  for (int kb = 0; kb < nkb; ++kb) {
+  for (int kb = w; kb < nkb; kb += AW) {
     float sc[16];
     scores(kb, sc);
     float bm = sc[0];
@@ -378,20 +400,39 @@ __global__ void __launch_bounds__(64) attn_kernel(const bf16_t* qkv, const bf16_
     const float mn = fmaxf(m, bm);
     float add = 0.0f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) add += sc[r] == -INFINITY ? 0.0f : expf(sc[r] - mn);
-    l = m == -INFINITY ? add : l * expf(m - mn) + add;
+    for (int r = 0; r < 16; ++r) add += sc[r] == -INFINITY ? 0.0f : __expf(sc[r] - mn);
+    l = m == -INFINITY ? add : l * __expf(m - mn) + add;
     m = mn;
   }
   l += __shfl_xor(l, 32, 64);
+  if (hf == 0) {
+    sml[w][0][c] = m;
+    sml[w][1][c] = l;
+  }
+  __syncthreads();
+  {
+    float M = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < AW; ++v) M = fmaxf(M, sml[v][0][c]);
+    float L = 0.0f;
+#pragma unroll
+    for (int v = 0; v < AW; ++v) {
+      const float mv = sml[v][0][c];
+      L += mv == -INFINITY ? 0.0f : sml[v][1][c] * __expf(mv - M);
+    }
+    m = M;
+    l = L;
+  }
+  const float rl = l > 0.0f ? 1.0f / l : 0.0f;   // softmax scale (torch multiplies by 1 / sum too)
 
-  // pass 2: p = bf16(e / l), O^T += V^T P^T
+  // pass 2: p = bf16(e * (1 / l)), O^T += V^T P^T over this wave's blocks
   f32x16 o[4];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[mb][r] = 0.0f;
   const int kp2 = lane & 15, dg = 32 * (lane >> 4);
-  for (int kb = 0; kb < nkb; ++kb) {
+  for (int kb = w; kb < nkb; kb += AW) {
     float sc[16];
     scores(kb, sc);
     // stage V rows 2 kp2, 2 kp2 + 1 of the block, dims dg .. dg + 31, transposed into vt[d][key]
@@ -412,14 +453,15 @@ __global__ void __launch_bounds__(64) attn_kernel(const bf16_t* qkv, const bf16_
         }
       }
     }
-    __syncthreads();
+    // the rows are this wave's own: order the writes before the reads within the wave
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
 #pragma unroll
     for (int kk2 = 0; kk2 < 2; ++kk2) {
       u32x4 pb;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float e0 = sc[8 * kk2 + 2 * j] == -INFINITY ? 0.0f : expf(sc[8 * kk2 + 2 * j] - m) / l;
-        const float e1 = sc[8 * kk2 + 2 * j + 1] == -INFINITY ? 0.0f : expf(sc[8 * kk2 + 2 * j + 1] - m) / l;
+        const float e0 = sc[8 * kk2 + 2 * j] == -INFINITY ? 0.0f : __expf(sc[8 * kk2 + 2 * j] - m) * rl;
+        const float e1 = sc[8 * kk2 + 2 * j + 1] == -INFINITY ? 0.0f : __expf(sc[8 * kk2 + 2 * j + 1] - m) * rl;
         pb[j] = (uint32_t)f2bf(e0) | ((uint32_t)f2bf(e1) << 16);
       }
 #pragma unroll
@@ -431,9 +473,25 @@ __global__ void __launch_bounds__(64) attn_kernel(const bf16_t* qkv, const bf16_
         o[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(av), as_bf8(pb), o[mb], 0, 0, 0);
       }
     }
-    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   }
-  if (!qok) return;
+  // partial O^T of waves 1.. to LDS (the V^T rows are dead), added in wave order by wave 0
+  __syncthreads();
+  float* ob = reinterpret_cast<float*>(smem);
+  if (w > 0) {
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) ob[((w - 1) * 64 + mb * 16 + r) * 64 + lane] = o[mb][r];
+  }
+  __syncthreads();
+  if (w > 0 || !qok) return;
+#pragma unroll 1
+  for (int v = 1; v < AW; ++v)
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[mb][r] += ob[((v - 1) * 64 + mb * 16 + r) * 64 + lane];
   // O^T layout: column = query c, register r of block mb = dim 32 mb + 8 (r >> 2) + 4 hf + (r & 3)
   bf16_t* op = att + (size_t)i * (NQH * HDIM) + hq * HDIM;
 #pragma unroll
@@ -474,12 +532,14 @@ __global__ void __launch_bounds__(64) select_kernel(const bf16_t* logits, int n,
 struct Shape { int N, K; };
 constexpr Shape kQKV{4096, HID}, kO{HID, NQH * HDIM}, kGU{2 * INTER, HID}, kDown{HID, INTER};
 
-// split-K factor: double while the tile grid is below 256 workgroups and the K range still
-// splits into whole 64-wide steps
+// split-K factor: double while the tile grid is below one workgroup per CU (two per CU from 512
+// rows on, where each split still runs a long K loop) and the K range still splits into whole
+// 64-wide steps
 int splits_for(int M, int N, int K) {
   const int tiles = ((M + BM - 1) / BM) * (N / BN);
+  const int target = M >= 512 ? 512 : 256;
   int ks = 1;
-  while (tiles * ks < 256 && ks < MAX_SPLIT && (K / BK) % (2 * ks) == 0) ks *= 2;
+  while (tiles * ks < target && ks < MAX_SPLIT && (K / BK) % (2 * ks) == 0) ks *= 2;
   return ks;
 }
 
@@ -586,7 +646,7 @@ hipError_t qtts_backbone_prefill(void* workspace, size_t workspace_bytes, const 
     if ((e = gemm<W_QKV, E_STORE>(g, stream)) != hipSuccess) return e;
     hipLaunchKernelGGL(rope_kv_kernel, dim3(S), dim3(256), 0, stream, qkv, layer_weights, l, cs, sn, pos3, position, S,
                        kc, vc, max_seq_len);
-    hipLaunchKernelGGL(attn_kernel, dim3((S + 31) / 32, NQH), dim3(64), 0, stream, qkv, kc, vc, l, max_seq_len,
+    hipLaunchKernelGGL(attn_kernel, dim3((S + 31) / 32, NQH), dim3(64 * AW), 0, stream, qkv, kc, vc, l, max_seq_len,
                        position, S, att, scale);
     g.A = att; g.lda = NQH * HDIM; g.N = kO.N; g.K = kO.K; g.out = h; g.ldo = HID; g.res = h; g.ldr = HID;
     if ((e = gemm<W_O, E_RESID>(g, stream)) != hipSuccess) return e;
