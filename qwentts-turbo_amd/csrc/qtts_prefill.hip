@@ -19,8 +19,9 @@
 //
 // Kernels (one launch each per layer; the host loop is in qtts_backbone_prefill below):
 //   rmsnorm_kernel   one wave per token
-//   gemm_kernel      C = A W^T, tile 128 x 64 x 64 (4 waves, each 32 rows x 2 MFMA 32x32x16
-//                    blocks), LDS double buffer, split-K over grid.z when the tile grid alone
+//   gemm_kernel      C = A W^T, tile 128 x 64 (4 waves, each 32 rows x 2 MFMA 32x32x16 blocks)
+//                    or, from 256 rows on, 128 x 128 (2 x 2 waves of 64 x 64), K steps of 64,
+//                    LDS double buffer + register stages, split-K over grid.z when the tile grid alone
 //                    would leave CUs idle (partials in f32, summed in a fixed order by
 //                    reduce_kernel); epilogues: store, residual add, SwiGLU (gate and up rows
 //                    interleaved by 32 in one tile)
@@ -46,7 +47,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr float EPS = 1e-6f;                 // Qwen3RMSNorm eps (config rms_norm_eps)
-constexpr int BM = 128, BN = 64, BK = 64;    // GEMM tile
+constexpr int BM = 128, BK = 64;             // GEMM tile rows and K step (columns: 64 or 128)
 constexpr int GT = 256;                      // GEMM threads (4 waves)
 constexpr int LROW = BK + 8;                 // LDS row (bf16): 144 B, 16-byte aligned, skewed banks
 constexpr int QKVW = 4096;                   // q | k | v row of one token
@@ -73,6 +74,15 @@ struct GemmArgs {
 
 __device__ __forceinline__ bf16x8 as_bf8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
+// bf16 rounding (round to nearest even) with gfx950's conversion instruction
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float rbh(float x) { return (float)(__bf16)x; }
+__device__ __forceinline__ bf16_t f2bh(float x) { return __builtin_bit_cast(bf16_t, (__bf16)x); }
+__device__ __forceinline__ uint32_t pack_bh(float lo, float hi) {
+  const bf16x2 v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 __device__ __forceinline__ const bf16_t* tbl(const TTSLayerWeights* lw, int field) {
   return reinterpret_cast<const bf16_t*>(ld_const(reinterpret_cast<const void* const*>(lw) + field));
 }
@@ -82,34 +92,57 @@ __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x));
 template <int EPI>
 __device__ __forceinline__ void epilogue(const GemmArgs& g, int m, int n, float v) {
   if constexpr (EPI == E_STORE) {
-    g.out[(size_t)m * g.ldo + n] = f2bf(v);
+    g.out[(size_t)m * g.ldo + n] = f2bh(v);
   } else if constexpr (EPI == E_RESID) {
     const float r = bf2f(g.res[(size_t)m * g.ldr + n]);
-    g.out[(size_t)m * g.ldo + n] = f2bf(r + rbf(v));
+    g.out[(size_t)m * g.ldo + n] = f2bh(r + rbh(v));
   }
 }
 
 // output column j of the SwiGLU GEMM from its gate and up sums
 __device__ __forceinline__ void epilogue_swiglu(const GemmArgs& g, int m, int j, float gs, float us) {
-  const float a = rbf(silu_f(rbf(gs)));
-  g.out[(size_t)m * g.ldo + j] = f2bf(a * rbf(us));
+  const float a = rbh(silu_f(rbh(gs)));
+  g.out[(size_t)m * g.ldo + j] = f2bh(a * rbh(us));
 }
 
-template <int WM, int EPI>
-__global__ void __launch_bounds__(GT) gemm_kernel(const GemmArgs g) {
+// SwiGLU tiles of TN virtual columns hold TN / 2 outputs: rows [64 q, 64 q + 32) of the tile are
+// gate rows and [64 q + 32, 64 q + 64) the up rows of the same 32 outputs, so each wave's two
+// 32-column MFMA blocks are a (gate, up) pair in the same lanes. Virtual column n -> weight row:
+template <int TN>
+__device__ __forceinline__ int swiglu_row(int n, bool& up) {
+  const int tt = n / TN, r = n % TN;
+  up = ((r >> 5) & 1) != 0;
+  return (TN / 2) * tt + 32 * (r >> 6) + (r & 31);
+}
+// ... and output column j -> its gate virtual column (the up column is 32 further)
+template <int TN>
+__device__ __forceinline__ int swiglu_gate_col(int j) {
+  const int tt = j / (TN / 2), r = j % (TN / 2);
+  return TN * tt + 64 * (r >> 5) + (r & 31);
+}
+
+// C = A W^T on a BM x TN tile. TN = 64: wave w owns rows 32 w .. 32 w + 31 and both 32-column
+// blocks. TN = 128: waves form 2 x 2, wave w owns rows 64 (w & 1) .. + 63 (two 32-row blocks)
+// and columns 64 (w >> 1) .. + 63 (two 32-column blocks): one LDS operand read per MFMA.
+template <int WM, int EPI, int TN>
+__global__ void __launch_bounds__(GT, 2) gemm_kernel(const GemmArgs g) {
+  constexpr int MBW = TN == 128 ? 2 : 1;          // 32-row blocks per wave
+  constexpr int NBR = TN / 32;                     // B rows staged per thread
   __shared__ __attribute__((aligned(16))) bf16_t sa[2][BM * LROW];
-  __shared__ __attribute__((aligned(16))) bf16_t sb[2][BN * LROW];
+  __shared__ __attribute__((aligned(16))) bf16_t sb[2][TN * LROW];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * TN;
   const int kbeg = blockIdx.z * g.kchunk, nk = g.kchunk / BK;
   const int lr = t >> 3, lc = (t & 7) * 8;   // this thread's load row (within 32) and column
+  const int wr0 = TN == 128 ? 64 * (w & 1) : 32 * w;   // wave's first tile row
+  const int wc0 = TN == 128 ? 64 * (w >> 1) : 0;       // wave's first tile column
 
   // weight rows this thread stages (virtual columns n0 + lr + 32 i)
-  const bf16_t* brow[2];
+  const bf16_t* brow[NBR];
   {
     const TTSLayerWeights* lw = g.layers + g.layer;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < NBR; ++i) {
       const int n = n0 + lr + 32 * i;
       const bf16_t* p;
       if constexpr (WM == W_DIRECT) {
@@ -120,8 +153,9 @@ __global__ void __launch_bounds__(GT) gemm_kernel(const GemmArgs g) {
       } else if constexpr (WM == W_O) {
         p = tbl(lw, 6) + (size_t)n * g.K;
       } else if constexpr (WM == W_GU) {
-        const int tt = n >> 6, r = n & 63;
-        p = r < 32 ? tbl(lw, 8) + (size_t)(32 * tt + r) * g.K : tbl(lw, 9) + (size_t)(32 * tt + r - 32) * g.K;
+        bool up;
+        const int row = swiglu_row<TN>(n, up);
+        p = (up ? tbl(lw, 9) : tbl(lw, 8)) + (size_t)row * g.K;
       } else {
         p = tbl(lw, 10) + (size_t)n * g.K;
       }
@@ -139,41 +173,49 @@ __global__ void __launch_bounds__(GT) gemm_kernel(const GemmArgs g) {
 
   // register stages two tiles ahead of the MFMAs (tile kt + 2 loads while tile kt computes and
   // tile kt + 1 moves to LDS): twice the weight bytes in flight of a plain double buffer
-  u32x4 ra[2][4], rb[2][2];
-  auto gload = [&](int k0, u32x4 (&a)[4], u32x4 (&b)[2]) {
+  u32x4 ra[2][4], rb[2][NBR];
+  auto gload = [&](int k0, u32x4 (&a)[4], u32x4 (&b)[NBR]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) a[i] = aok[i] ? ldw(arow[i] + k0) : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int i = 0; i < 2; ++i) b[i] = ldw(brow[i] + k0);
+    for (int i = 0; i < NBR; ++i) b[i] = ldw(brow[i] + k0);
   };
-  auto sstore = [&](int buf, const u32x4 (&a)[4], const u32x4 (&b)[2]) {
+  auto sstore = [&](int buf, const u32x4 (&a)[4], const u32x4 (&b)[NBR]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(&sa[buf][(lr + 32 * i) * LROW + lc]) = a[i];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) *reinterpret_cast<u32x4*>(&sb[buf][(lr + 32 * i) * LROW + lc]) = b[i];
+    for (int i = 0; i < NBR; ++i) *reinterpret_cast<u32x4*>(&sb[buf][(lr + 32 * i) * LROW + lc]) = b[i];
   };
 
-  f32x16 acc[2];
+  f32x16 acc[MBW][2];
 #pragma unroll
-  for (int nb = 0; nb < 2; ++nb)
+  for (int mb = 0; mb < MBW; ++mb)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[nb][r] = 0.0f;
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mb][nb][r] = 0.0f;
 
-  const int arow_l = (32 * w + (lane & 31)) * LROW, brow_l = (lane & 31) * LROW, kh = 8 * (lane >> 5);
+  const int arow_l = (wr0 + (lane & 31)) * LROW, brow_l = (wc0 + (lane & 31)) * LROW, kh = 8 * (lane >> 5);
   auto compute = [&](int buf) {
 #pragma unroll
     for (int kk = 0; kk < BK / 16; ++kk) {
       const int ko = 16 * kk + kh;
-      const bf16x8 av = as_bf8(*reinterpret_cast<const u32x4*>(&sa[buf][arow_l + ko]));
+      bf16x8 av[MBW], bv[2];
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        const bf16x8 bv = as_bf8(*reinterpret_cast<const u32x4*>(&sb[buf][brow_l + 32 * nb * LROW + ko]));
-        acc[nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc[nb], 0, 0, 0);
-      }
+      for (int mb = 0; mb < MBW; ++mb)
+        av[mb] = as_bf8(*reinterpret_cast<const u32x4*>(&sa[buf][arow_l + 32 * mb * LROW + ko]));
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+        bv[nb] = as_bf8(*reinterpret_cast<const u32x4*>(&sb[buf][brow_l + 32 * nb * LROW + ko]));
+#pragma unroll
+      for (int mb = 0; mb < MBW; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+          acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[mb], bv[nb], acc[mb][nb], 0, 0, 0);
     }
   };
   // one step: tile kt in LDS buffer kt & 1, tile kt + 1 in register stage S1, stage S0 free
-  auto step = [&](int kt, u32x4 (&a0)[4], u32x4 (&b0)[2], const u32x4 (&a1)[4], const u32x4 (&b1)[2]) {
+  auto step = [&](int kt, u32x4 (&a0)[4], u32x4 (&b0)[NBR], const u32x4 (&a1)[4], const u32x4 (&b1)[NBR]) {
     if (kt + 2 < nk) gload((kt + 2) * BK, a0, b0);
     compute(kt & 1);
     if (kt + 1 < nk) sstore((kt + 1) & 1, a1, b1);
@@ -195,29 +237,33 @@ __global__ void __launch_bounds__(GT) gemm_kernel(const GemmArgs g) {
   if (gridDim.z > 1) {
     float* P = g.part + (size_t)blockIdx.z * g.M * g.N;
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
+    for (int mb = 0; mb < MBW; ++mb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = m0 + 32 * w + 8 * (r >> 2) + hrow + (r & 3);
-        if (m < g.M) P[(size_t)m * g.N + n0 + 32 * nb + col] = acc[nb][r];
-      }
+      for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + wr0 + 32 * mb + 8 * (r >> 2) + hrow + (r & 3);
+          if (m < g.M) P[(size_t)m * g.N + n0 + wc0 + 32 * nb + col] = acc[mb][nb][r];
+        }
     return;
   }
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int m = m0 + 32 * w + 8 * (r >> 2) + hrow + (r & 3);
-    if (m >= g.M) continue;
-    if constexpr (EPI == E_SWIGLU) {
-      epilogue_swiglu(g, m, (n0 >> 1) + col, acc[0][r], acc[1][r]);
-    } else {
-      epilogue<EPI>(g, m, n0 + col, acc[0][r]);
-      epilogue<EPI>(g, m, n0 + 32 + col, acc[1][r]);
+  for (int mb = 0; mb < MBW; ++mb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = m0 + wr0 + 32 * mb + 8 * (r >> 2) + hrow + (r & 3);
+      if (m >= g.M) continue;
+      if constexpr (EPI == E_SWIGLU) {
+        epilogue_swiglu(g, m, n0 / 2 + wc0 / 2 + col, acc[mb][0][r], acc[mb][1][r]);
+      } else {
+        epilogue<EPI>(g, m, n0 + wc0 + col, acc[mb][0][r]);
+        epilogue<EPI>(g, m, n0 + wc0 + 32 + col, acc[mb][1][r]);
+      }
     }
-  }
 }
 
 // Sum of the split-K partials in split order, then the GEMM's epilogue; one thread per output.
-template <int EPI>
+template <int EPI, int TN>
 __global__ void __launch_bounds__(256) reduce_kernel(const GemmArgs g, int splits) {
   const int nout = EPI == E_SWIGLU ? g.N / 2 : g.N;
   const long idx = (long)blockIdx.x * 256 + threadIdx.x;
@@ -226,7 +272,7 @@ __global__ void __launch_bounds__(256) reduce_kernel(const GemmArgs g, int split
   const size_t stride = (size_t)g.M * g.N;
   const float* P = g.part + (size_t)m * g.N;
   if constexpr (EPI == E_SWIGLU) {
-    const int nv = 64 * (j >> 5) + (j & 31);
+    const int nv = swiglu_gate_col<TN>(j);
     float gs = 0.0f, us = 0.0f;
     for (int z = 0; z < splits; ++z) {
       gs += P[z * stride + nv];
@@ -382,7 +428,7 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int kr = 32 * kb + 8 * (r >> 2) + 4 * hf + (r & 3);
-      const float v = rbf(rbf(acc[r]) * scale);
+      const float v = rbh(rbh(acc[r]) * scale);
       sc[r] = (qok && kr <= qpos) ? v : -INFINITY;
     }
   };
@@ -396,11 +442,13 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
 #pragma unroll
     for (int r = 1; r < 16; ++r) bm = fmaxf(bm, sc[r]);
     bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-    // (no branch around the MFMAs: a fully masked block leaves m and l unchanged)
+    // (no branch around the MFMAs: a fully masked block leaves m and l unchanged; masked scores
+    // are -inf, whose exp is 0, and a still fully masked row subtracts 0 instead of -inf)
     const float mn = fmaxf(m, bm);
+    const float mr = mn == -INFINITY ? 0.0f : mn;
     float add = 0.0f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) add += sc[r] == -INFINITY ? 0.0f : __expf(sc[r] - mn);
+    for (int r = 0; r < 16; ++r) add += __expf(sc[r] - mr);
     l = m == -INFINITY ? add : l * __expf(m - mn) + add;
     m = mn;
   }
@@ -424,6 +472,7 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
     l = L;
   }
   const float rl = l > 0.0f ? 1.0f / l : 0.0f;   // softmax scale (torch multiplies by 1 / sum too)
+  const float mr = m == -INFINITY ? 0.0f : m;
 
   // pass 2: p = bf16(e * (1 / l)), O^T += V^T P^T over this wave's blocks
   f32x16 o[4];
@@ -459,11 +508,8 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
     for (int kk2 = 0; kk2 < 2; ++kk2) {
       u32x4 pb;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float e0 = sc[8 * kk2 + 2 * j] == -INFINITY ? 0.0f : __expf(sc[8 * kk2 + 2 * j] - m) * rl;
-        const float e1 = sc[8 * kk2 + 2 * j + 1] == -INFINITY ? 0.0f : __expf(sc[8 * kk2 + 2 * j + 1] - m) * rl;
-        pb[j] = (uint32_t)f2bf(e0) | ((uint32_t)f2bf(e1) << 16);
-      }
+      for (int j = 0; j < 4; ++j)
+        pb[j] = pack_bh(__expf(sc[8 * kk2 + 2 * j] - mr) * rl, __expf(sc[8 * kk2 + 2 * j + 1] - mr) * rl);
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
         const bf16_t* vr = &vt[(32 * mb + c) * VTROW + 16 * kk2 + 4 * hf];
@@ -500,8 +546,8 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
     for (int rq = 0; rq < 4; ++rq) {
       const int d0 = 32 * mb + 8 * rq + 4 * hf;
       u32x2 pk;
-      pk[0] = (uint32_t)f2bf(o[mb][4 * rq]) | ((uint32_t)f2bf(o[mb][4 * rq + 1]) << 16);
-      pk[1] = (uint32_t)f2bf(o[mb][4 * rq + 2]) | ((uint32_t)f2bf(o[mb][4 * rq + 3]) << 16);
+      pk[0] = pack_bh(o[mb][4 * rq], o[mb][4 * rq + 1]);
+      pk[1] = pack_bh(o[mb][4 * rq + 2], o[mb][4 * rq + 3]);
       *reinterpret_cast<u32x2*>(op + d0) = pk;
     }
 }
@@ -532,12 +578,16 @@ __global__ void __launch_bounds__(64) select_kernel(const bf16_t* logits, int n,
 struct Shape { int N, K; };
 constexpr Shape kQKV{4096, HID}, kO{HID, NQH * HDIM}, kGU{2 * INTER, HID}, kDown{HID, INTER};
 
+// tile width: 128 columns from 256 rows on (one LDS read per MFMA), 64 below (more tiles for
+// the weight-streaming small-M case)
+int tile_n(int M) { return M >= 256 ? 128 : 64; }
+
 // split-K factor: double while the tile grid is below one workgroup per CU (two per CU from 512
 // rows on, where each split still runs a long K loop) and the K range still splits into whole
 // 64-wide steps
 int splits_for(int M, int N, int K) {
-  const int tiles = ((M + BM - 1) / BM) * (N / BN);
-  const int target = M >= 512 ? 512 : 256;
+  const int tiles = ((M + BM - 1) / BM) * (N / tile_n(M));
+  const int target = M >= 512 ? 512 : (M >= 256 ? 256 : 128);
   int ks = 1;
   while (tiles * ks < target && ks < MAX_SPLIT && (K / BK) % (2 * ks) == 0) ks *= 2;
   return ks;
@@ -572,16 +622,22 @@ Layout layout(int S, int vocab) {
   return L;
 }
 
+template <int WM, int EPI, int TN>
+void gemm_launch(const GemmArgs& g, int ks, hipStream_t st) {
+  dim3 grid(g.N / TN, (g.M + BM - 1) / BM, ks);
+  hipLaunchKernelGGL((gemm_kernel<WM, EPI, TN>), grid, dim3(GT), 0, st, g);
+  if (ks > 1) {
+    const long nout = (long)g.M * (EPI == E_SWIGLU ? g.N / 2 : g.N);
+    hipLaunchKernelGGL((reduce_kernel<EPI, TN>), dim3((unsigned)((nout + 255) / 256)), dim3(256), 0, st, g, ks);
+  }
+}
+
 template <int WM, int EPI>
 hipError_t gemm(GemmArgs g, hipStream_t st) {
   const int ks = splits_for(g.M, g.N, g.K);
   g.kchunk = g.K / ks;
-  dim3 grid(g.N / BN, (g.M + BM - 1) / BM, ks);
-  hipLaunchKernelGGL((gemm_kernel<WM, EPI>), grid, dim3(GT), 0, st, g);
-  if (ks > 1) {
-    const long nout = (long)g.M * (EPI == E_SWIGLU ? g.N / 2 : g.N);
-    hipLaunchKernelGGL((reduce_kernel<EPI>), dim3((unsigned)((nout + 255) / 256)), dim3(256), 0, st, g, ks);
-  }
+  if (tile_n(g.M) == 128) gemm_launch<WM, EPI, 128>(g, ks, st);
+  else gemm_launch<WM, EPI, 64>(g, ks, st);
   return hipGetLastError();
 }
 
@@ -611,7 +667,7 @@ hipError_t qtts_backbone_prefill(void* workspace, size_t workspace_bytes, const 
     return hipErrorInvalidValue;
   if (num_layers < 1 || S < 1 || position < 0 || max_seq_len < 1 || position + S > max_seq_len)
     return hipErrorInvalidValue;
-  if (codec_head != nullptr && (vocab < BN || vocab > MAXV || vocab % BN != 0 || out_token == nullptr))
+  if (codec_head != nullptr && (vocab < 128 || vocab > MAXV || vocab % 128 != 0 || out_token == nullptr))
     return hipErrorInvalidValue;
   if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0 || (reinterpret_cast<uintptr_t>(input_embeddings) & 15u) != 0)
     return hipErrorInvalidValue;

@@ -109,3 +109,28 @@ def test_backbone_streams_match_batch1(pkg, lengths, sample):
     ref.check_error()
     assert xl.positions() == ref.positions() == lengths
     print(f"backbone streams {lengths}: tokens {tok.tolist()}", flush=True)
+
+
+def test_backbone_streams_reject_bad_arguments(pkg):
+    """decode_steps_streams validates before launching: more than 8 decoders, a decoder listed
+    twice, a decoder over other weight tensors, a full KV cache; positions stay unchanged."""
+    cfg = pkg.SyntheticConfig(n_bb_layers=1, n_cp_layers=1, n_groups=1)
+    dsd = {k: v.cuda() for k, v in pkg.synthetic_state_dict(seed=5, cfg=cfg).items()}
+    bd = pkg.BatchedTTSDecoder(dsd, 2, max_seq_len=16)
+    lead, other = bd.streams[0].decoder, bd.streams[1].decoder
+    i32 = dict(dtype=torch.int32, device="cuda")
+    x2 = torch.zeros(2, 1024, dtype=torch.bfloat16, device="cuda")
+    h2 = torch.empty(2, 1024, device="cuda")
+    args = (None, [], 1.0, -1, False, False, 1.0, 0, 1.0, 0, 0)
+    with pytest.raises(RuntimeError, match="1..8"):
+        lead.decode_steps_streams([lead] * 9, torch.zeros(9, 1024, dtype=torch.bfloat16, device="cuda"),
+                                  torch.zeros(9, **i32), torch.empty(9, 1024, device="cuda"), *args)
+    with pytest.raises(RuntimeError, match="twice"):
+        lead.decode_steps_streams([lead, lead], x2, torch.zeros(2, **i32), h2, *args)
+    alien = pkg.TTSMegakernelGenerator(model=dsd, max_seq_len=16).decoder   # its own weight copy
+    with pytest.raises(RuntimeError, match="share"):
+        lead.decode_steps_streams([lead, alien], x2, torch.zeros(2, **i32), h2, *args)
+    other.set_position(16)
+    with pytest.raises(RuntimeError, match="KV cache full"):
+        lead.decode_steps_streams([lead, other], x2, torch.zeros(2, **i32), h2, *args)
+    assert lead.position() == 0 and other.position() == 16

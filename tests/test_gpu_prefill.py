@@ -129,3 +129,19 @@ def test_prefill_full_model_and_first_token(pkg):
     t = int(tok.item())
     _print(f"first token {t} (argmax of the masked GPU logits {int(m.argmax())})")
     assert t == int(m.argmax())
+
+
+def test_prefill_rejects_bad_arguments(pkg, small):
+    """Host-side validation before any launch: a prompt past max_seq_len, a wrong embedding
+    width, a pos3 of the wrong shape; the decoder's position is left unchanged."""
+    dsd, _ = small
+    bb = pkg.TTSMegakernelGenerator(model=dsd, max_seq_len=64)
+    bb.set_position(60)
+    with pytest.raises(RuntimeError, match="max_seq_len"):
+        bb.prefill(torch.zeros(5, 1024, dtype=torch.bfloat16, device="cuda"))
+    with pytest.raises(RuntimeError, match="embeds"):
+        bb.prefill(torch.zeros(2, 512, dtype=torch.bfloat16, device="cuda"))
+    with pytest.raises(RuntimeError, match="pos3"):
+        bb.prefill(torch.zeros(2, 1024, dtype=torch.bfloat16, device="cuda"),
+                   pos3=torch.zeros(3, 3, dtype=torch.int32, device="cuda"))
+    assert bb.position == 60
