@@ -26,6 +26,8 @@
 //                    reduce_kernel); epilogues: store, residual add, SwiGLU (gate and up rows
 //                    interleaved by 32 in one tile)
 //   rope_kv_kernel   q/k RMSNorm + interleaved mRoPE, K/V cache write, one workgroup per token
+//                    (fused into the split-K reduction of QKV when split: reduce_rope_kernel)
+//   reduce_resid_norm_kernel  split-K O / down: sums, residual add and the next RMSNorm per token
 //   attn_kernel      causal GQA, 4 waves per (32-query block, query head) splitting the key
 //                    blocks: S^T = K Q^T on MFMA (each lane then holds one query's scores, so
 //                    the row max and sum stay in the lane and its partner half-wave), two passes
@@ -262,27 +264,39 @@ __global__ void __launch_bounds__(GT, 2) gemm_kernel(const GemmArgs g) {
     }
 }
 
-// Sum of the split-K partials in split order, then the GEMM's epilogue; one thread per output.
+// Sum of the split-K partials in split order, then the GEMM's epilogue; four consecutive
+// outputs per thread (16-byte partial loads; a SwiGLU group of four lies in one 32-column block).
 template <int EPI, int TN>
 __global__ void __launch_bounds__(256) reduce_kernel(const GemmArgs g, int splits) {
   const int nout = EPI == E_SWIGLU ? g.N / 2 : g.N;
-  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  const long idx = ((long)blockIdx.x * 256 + threadIdx.x) * 4;
   if (idx >= (long)g.M * nout) return;
   const int m = (int)(idx / nout), j = (int)(idx % nout);
   const size_t stride = (size_t)g.M * g.N;
   const float* P = g.part + (size_t)m * g.N;
   if constexpr (EPI == E_SWIGLU) {
     const int nv = swiglu_gate_col<TN>(j);
-    float gs = 0.0f, us = 0.0f;
+    float4 gs = {0.0f, 0.0f, 0.0f, 0.0f}, us = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int z = 0; z < splits; ++z) {
-      gs += P[z * stride + nv];
-      us += P[z * stride + nv + 32];
+      const float4 a = *reinterpret_cast<const float4*>(P + z * stride + nv);
+      const float4 b = *reinterpret_cast<const float4*>(P + z * stride + nv + 32);
+      gs.x += a.x; gs.y += a.y; gs.z += a.z; gs.w += a.w;
+      us.x += b.x; us.y += b.y; us.z += b.z; us.w += b.w;
     }
-    epilogue_swiglu(g, m, j, gs, us);
+    epilogue_swiglu(g, m, j, gs.x, us.x);
+    epilogue_swiglu(g, m, j + 1, gs.y, us.y);
+    epilogue_swiglu(g, m, j + 2, gs.z, us.z);
+    epilogue_swiglu(g, m, j + 3, gs.w, us.w);
   } else {
-    float s = 0.0f;
-    for (int z = 0; z < splits; ++z) s += P[z * stride + j];
-    epilogue<EPI>(g, m, j, s);
+    float4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int z = 0; z < splits; ++z) {
+      const float4 a = *reinterpret_cast<const float4*>(P + z * stride + j);
+      v.x += a.x; v.y += a.y; v.z += a.z; v.w += a.w;
+    }
+    epilogue<EPI>(g, m, j, v.x);
+    epilogue<EPI>(g, m, j + 1, v.y);
+    epilogue<EPI>(g, m, j + 2, v.z);
+    epilogue<EPI>(g, m, j + 3, v.w);
   }
 }
 
@@ -332,11 +346,12 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const bf16_t* x, int ldx, 
 
 // Per token: q/k head RMSNorm (field 4 / 5 gains), interleaved mRoPE from the bf16 tables, q
 // written back in place, the rotated k and the v of every KV head written to the cache at
-// position p0 + s. Lane j of a wave handles channels j and j + 64 (the rotate_half pair).
-__global__ void __launch_bounds__(256) rope_kv_kernel(bf16_t* qkv, const TTSLayerWeights* layers, int layer,
-                                                      const bf16_t* cos_t, const bf16_t* sin_t, const int* pos3,
-                                                      int p0, int S, bf16_t* kc, bf16_t* vc, int max_seq) {
-  const int s = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+// position p0 + s. Lane j of a wave handles channels j and j + 64 (the rotate_half pair). Run by
+// a whole 256-thread workgroup on token s's q | k | v row `src`.
+__device__ __forceinline__ void rope_kv_row(bf16_t* src, int s, const TTSLayerWeights* layers, int layer,
+                                            const bf16_t* cos_t, const bf16_t* sin_t, const int* pos3, int p0, int S,
+                                            bf16_t* kc, bf16_t* vc, int max_seq) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int pos = p0 + s;
   const int sec = (lane < 60 && lane % 3 == 1) ? 1 : ((lane < 60 && lane % 3 == 2) ? 2 : 0);
   // table row of this channel's section (clamped into the table: a caller's out-of-range
@@ -344,36 +359,124 @@ __global__ void __launch_bounds__(256) rope_kv_kernel(bf16_t* qkv, const TTSLaye
   const int row = pos3 ? min(max(pos3[sec * S + s], 0), max_seq - 1) : pos;
   const float c0 = ldbf(cos_t + (size_t)row * HDIM + lane), c1 = ldbf(cos_t + (size_t)row * HDIM + lane + 64);
   const float s0 = ldbf(sin_t + (size_t)row * HDIM + lane), s1 = ldbf(sin_t + (size_t)row * HDIM + lane + 64);
+  // wave w takes heads w + 4 k (k < 6): q heads for k < 4, k heads 16 + w, 20 + w for k = 4, 5;
+  // every load is issued before the first reduction, the six reductions interleave
+  constexpr int HPW = (NQH + NKVH) / 4;
   const TTSLayerWeights* lw = layers + layer;
   const bf16_t* qn = tbl(lw, 4);
   const bf16_t* kn = tbl(lw, 5);
-  bf16_t* src = qkv + (size_t)s * QKVW;
-  for (int hd = w; hd < NQH + NKVH; hd += 4) {
-    bf16_t* hp = src + hd * HDIM;
-    const float x0 = bf2f(hp[lane]), x1 = bf2f(hp[lane + 64]);
-    float ss = x0 * x0 + x1 * x1;
+  float x0[HPW], x1[HPW], ss[HPW];
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
-    const float rs = 1.0f / sqrtf(ss / (float)HDIM + EPS);
-    const bf16_t* gn = hd < NQH ? qn : kn;
-    const float y0 = rbf(ldbf(gn + lane) * rbf(x0 * rs));
-    const float y1 = rbf(ldbf(gn + lane + 64) * rbf(x1 * rs));
-    const bf16_t o0 = f2bf(rbf(y0 * c0) + rbf(-y1 * s0));
-    const bf16_t o1 = f2bf(rbf(y1 * c1) + rbf(y0 * s1));
-    if (hd < NQH) {
-      hp[lane] = o0;
-      hp[lane + 64] = o1;
-    } else {
-      bf16_t* dst = kc + (((size_t)layer * NKVH + (hd - NQH)) * max_seq + pos) * HDIM;
-      dst[lane] = o0;
-      dst[lane + 64] = o1;
-    }
+  for (int k = 0; k < HPW; ++k) {
+    const bf16_t* hp = src + (w + 4 * k) * HDIM;
+    x0[k] = bf2f(hp[lane]);
+    x1[k] = bf2f(hp[lane + 64]);
+  }
+  const float gq0 = ldbf(qn + lane), gq1 = ldbf(qn + lane + 64);
+  const float gk0 = ldbf(kn + lane), gk1 = ldbf(kn + lane + 64);
+#pragma unroll
+  for (int k = 0; k < HPW; ++k) ss[k] = x0[k] * x0[k] + x1[k] * x1[k];
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1)
+#pragma unroll
+    for (int k = 0; k < HPW; ++k) ss[k] += __shfl_xor(ss[k], o, 64);
+#pragma unroll
+  for (int k = 0; k < HPW; ++k) {
+    const float rs = 1.0f / sqrtf(ss[k] / (float)HDIM + EPS);
+    const float y0 = rbh((k < 4 ? gq0 : gk0) * rbh(x0[k] * rs));
+    const float y1 = rbh((k < 4 ? gq1 : gk1) * rbh(x1[k] * rs));
+    const bf16_t o0 = f2bh(rbh(y0 * c0) + rbh(-y1 * s0));
+    const bf16_t o1 = f2bh(rbh(y1 * c1) + rbh(y0 * s1));
+    bf16_t* dst = k < 4 ? src + (w + 4 * k) * HDIM
+                        : kc + (((size_t)layer * NKVH + (w + 4 * (k - 4))) * max_seq + pos) * HDIM;
+    dst[lane] = o0;
+    dst[lane + 64] = o1;
   }
   // v: 8 heads x 128 = 1024 values, 4 per thread
   const int i0 = 4 * threadIdx.x;
   const int kvh = i0 >> 7, d = i0 & 127;
   const u32x2 vv = *reinterpret_cast<const u32x2*>(src + 3072 + i0);
   *reinterpret_cast<u32x2*>(vc + (((size_t)layer * NKVH + kvh) * max_seq + pos) * HDIM + d) = vv;
+}
+
+__global__ void __launch_bounds__(256) rope_kv_kernel(bf16_t* qkv, const TTSLayerWeights* layers, int layer,
+                                                      const bf16_t* cos_t, const bf16_t* sin_t, const int* pos3,
+                                                      int p0, int S, bf16_t* kc, bf16_t* vc, int max_seq) {
+  rope_kv_row(qkv + (size_t)blockIdx.x * QKVW, blockIdx.x, layers, layer, cos_t, sin_t, pos3, p0, S, kc, vc, max_seq);
+}
+
+// Split-K QKV: token m's 4096 sums in split order -> bf16 q | k | v row, then rope_kv_row on it
+// (one launch instead of a reduction and a rope pass).
+__global__ void __launch_bounds__(256) reduce_rope_kernel(const GemmArgs g, int splits, const bf16_t* cos_t,
+                                                          const bf16_t* sin_t, const int* pos3, int p0, bf16_t* kc,
+                                                          bf16_t* vc, int max_seq) {
+  const int m = blockIdx.x;
+  const size_t stride = (size_t)g.M * g.N;
+  const float* P = g.part + (size_t)m * g.N;
+  bf16_t* row = g.out + (size_t)m * g.ldo;
+  // thread t: elements 16 t .. 16 t + 15, in 16-byte loads
+  const int n0 = 16 * threadIdx.x;
+  float v[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) v[i] = 0.0f;
+  for (int z = 0; z < splits; ++z) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 p = *reinterpret_cast<const float4*>(P + z * stride + n0 + 4 * q);
+      v[4 * q] += p.x; v[4 * q + 1] += p.y; v[4 * q + 2] += p.z; v[4 * q + 3] += p.w;
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = pack_bh(v[8 * q + 2 * e], v[8 * q + 2 * e + 1]);
+    *reinterpret_cast<u32x4*>(row + n0 + 8 * q) = o;
+  }
+  __syncthreads();   // the row is read back by other threads of the workgroup
+  rope_kv_row(row, m, g.layers, g.layer, cos_t, sin_t, pos3, p0, g.M, kc, vc, max_seq);
+}
+
+// Split-K O or down projection of token m: sums in split order, residual add in place
+// (h = bf16(h + bf16(sum))), then the RMSNorm of the new row with gain field `field` of layer
+// `nlayer` into xn (skipped when nlayer < 0): one launch instead of a reduction and a norm.
+__global__ void __launch_bounds__(256) reduce_resid_norm_kernel(const GemmArgs g, int splits, int nlayer, int field,
+                                                                bf16_t* xn) {
+  __shared__ float red[4];
+  const int m = blockIdx.x, t = threadIdx.x, lane = t & 63;
+  const size_t stride = (size_t)g.M * g.N;
+  const float* P = g.part + (size_t)m * g.N + 4 * t;
+  bf16_t* hr = g.out + (size_t)m * g.ldo + 4 * t;
+  const u32x2 rv = *reinterpret_cast<const u32x2*>(g.res + (size_t)m * g.ldr + 4 * t);
+  float hv[4];
+  {
+    float sv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int z = 0; z < splits; ++z) {
+      const float4 p = *reinterpret_cast<const float4*>(P + z * stride);
+      sv[0] += p.x; sv[1] += p.y; sv[2] += p.z; sv[3] += p.w;
+    }
+    hv[0] = rbh(bflo(rv[0]) + rbh(sv[0]));
+    hv[1] = rbh(bfhi(rv[0]) + rbh(sv[1]));
+    hv[2] = rbh(bflo(rv[1]) + rbh(sv[2]));
+    hv[3] = rbh(bfhi(rv[1]) + rbh(sv[3]));
+  }
+  u32x2 hp;
+  hp[0] = pack_bh(hv[0], hv[1]);
+  hp[1] = pack_bh(hv[2], hv[3]);
+  *reinterpret_cast<u32x2*>(hr) = hp;
+  if (nlayer < 0) return;
+  float ss = hv[0] * hv[0] + hv[1] * hv[1] + hv[2] * hv[2] + hv[3] * hv[3];
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  if (lane == 0) red[t >> 6] = ss;
+  __syncthreads();
+  ss = (red[0] + red[1]) + (red[2] + red[3]);
+  const float rs = 1.0f / sqrtf(ss / (float)HID + EPS);
+  const u32x2 gw = *reinterpret_cast<const u32x2*>(tbl(g.layers + nlayer, field) + 4 * t);
+  u32x2 o;
+  o[0] = pack_bh(bflo(gw[0]) * rbh(hv[0] * rs), bfhi(gw[0]) * rbh(hv[1] * rs));
+  o[1] = pack_bh(bflo(gw[1]) * rbh(hv[2] * rs), bfhi(gw[1]) * rbh(hv[3] * rs));
+  *reinterpret_cast<u32x2*>(xn + (size_t)m * HID + 4 * t) = o;
 }
 
 // Causal GQA attention of S queries (positions p0 .. p0 + S - 1) over cache positions
@@ -623,22 +726,24 @@ Layout layout(int S, int vocab) {
 }
 
 template <int WM, int EPI, int TN>
-void gemm_launch(const GemmArgs& g, int ks, hipStream_t st) {
+void gemm_launch(const GemmArgs& g, int ks, bool reduce, hipStream_t st) {
   dim3 grid(g.N / TN, (g.M + BM - 1) / BM, ks);
   hipLaunchKernelGGL((gemm_kernel<WM, EPI, TN>), grid, dim3(GT), 0, st, g);
-  if (ks > 1) {
-    const long nout = (long)g.M * (EPI == E_SWIGLU ? g.N / 2 : g.N);
+  if (ks > 1 && reduce) {
+    const long nout = (long)g.M * (EPI == E_SWIGLU ? g.N / 2 : g.N) / 4;
     hipLaunchKernelGGL((reduce_kernel<EPI, TN>), dim3((unsigned)((nout + 255) / 256)), dim3(256), 0, st, g, ks);
   }
 }
 
+// Launches the GEMM; with split-K the partial sums are left in g.part for a fused consumer when
+// `reduce` is false, else reduced here. Returns the split count (0 on a launch error).
 template <int WM, int EPI>
-hipError_t gemm(GemmArgs g, hipStream_t st) {
+int gemm(GemmArgs& g, hipStream_t st, bool reduce = true) {
   const int ks = splits_for(g.M, g.N, g.K);
   g.kchunk = g.K / ks;
-  if (tile_n(g.M) == 128) gemm_launch<WM, EPI, 128>(g, ks, st);
-  else gemm_launch<WM, EPI, 64>(g, ks, st);
-  return hipGetLastError();
+  if (tile_n(g.M) == 128) gemm_launch<WM, EPI, 128>(g, ks, reduce, st);
+  else gemm_launch<WM, EPI, 64>(g, ks, reduce, st);
+  return hipGetLastError() == hipSuccess ? ks : 0;
 }
 
 }  // namespace pf
@@ -690,28 +795,47 @@ hipError_t qtts_backbone_prefill(void* workspace, size_t workspace_bytes, const 
 
   hipError_t e = hipMemcpyAsync(h, input_embeddings, (size_t)S * HID * 2, hipMemcpyDeviceToDevice, stream);
   if (e != hipSuccess) return e;
+  // layer 0's input norm; later input norms come with the previous layer's down projection
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(norm_grid), dim3(256), 0, stream, h, HID, layer_weights, 0, 0,
+                     (const bf16_t*)nullptr, xn, HID, (float*)nullptr, S);
+  const unsigned rows = (unsigned)S;
   for (int l = 0; l < num_layers; ++l) {
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(norm_grid), dim3(256), 0, stream, h, HID, layer_weights, l, 0,
-                       (const bf16_t*)nullptr, xn, HID, (float*)nullptr, S);
     GemmArgs g{};
     g.layers = layer_weights;
     g.layer = l;
     g.M = S;
     g.part = part;
+    int ks;
+    // QKV, then q/k-norm + RoPE + K/V write (fused with the split-K reduction)
     g.A = xn; g.lda = HID; g.N = kQKV.N; g.K = kQKV.K; g.out = qkv; g.ldo = QKVW;
-    if ((e = gemm<W_QKV, E_STORE>(g, stream)) != hipSuccess) return e;
-    hipLaunchKernelGGL(rope_kv_kernel, dim3(S), dim3(256), 0, stream, qkv, layer_weights, l, cs, sn, pos3, position, S,
-                       kc, vc, max_seq_len);
+    if ((ks = gemm<W_QKV, E_STORE>(g, stream, false)) == 0) return hipGetLastError();
+    if (ks > 1)
+      hipLaunchKernelGGL(reduce_rope_kernel, dim3(rows), dim3(256), 0, stream, g, ks, cs, sn, pos3, position, kc, vc,
+                         max_seq_len);
+    else
+      hipLaunchKernelGGL(rope_kv_kernel, dim3(rows), dim3(256), 0, stream, qkv, layer_weights, l, cs, sn, pos3, position,
+                         S, kc, vc, max_seq_len);
     hipLaunchKernelGGL(attn_kernel, dim3((S + 31) / 32, NQH), dim3(64 * AW), 0, stream, qkv, kc, vc, l, max_seq_len,
                        position, S, att, scale);
+    // O + residual, then the post-attention norm (fused with the split-K reduction)
     g.A = att; g.lda = NQH * HDIM; g.N = kO.N; g.K = kO.K; g.out = h; g.ldo = HID; g.res = h; g.ldr = HID;
-    if ((e = gemm<W_O, E_RESID>(g, stream)) != hipSuccess) return e;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(norm_grid), dim3(256), 0, stream, h, HID, layer_weights, l, 7,
-                       (const bf16_t*)nullptr, xn, HID, (float*)nullptr, S);
+    if ((ks = gemm<W_O, E_RESID>(g, stream, false)) == 0) return hipGetLastError();
+    if (ks > 1)
+      hipLaunchKernelGGL(reduce_resid_norm_kernel, dim3(rows), dim3(256), 0, stream, g, ks, l, 7, xn);
+    else
+      hipLaunchKernelGGL(rmsnorm_kernel, dim3(norm_grid), dim3(256), 0, stream, h, HID, layer_weights, l, 7,
+                         (const bf16_t*)nullptr, xn, HID, (float*)nullptr, S);
     g.A = xn; g.lda = HID; g.N = kGU.N; g.K = kGU.K; g.out = act; g.ldo = INTER; g.res = nullptr;
-    if ((e = gemm<W_GU, E_SWIGLU>(g, stream)) != hipSuccess) return e;
+    if (gemm<W_GU, E_SWIGLU>(g, stream) == 0) return hipGetLastError();
+    // down + residual, then the next layer's input norm (fused with the split-K reduction)
+    const int nl = l + 1 < num_layers ? l + 1 : -1;
     g.A = act; g.lda = INTER; g.N = kDown.N; g.K = kDown.K; g.out = h; g.ldo = HID; g.res = h; g.ldr = HID;
-    if ((e = gemm<W_DOWN, E_RESID>(g, stream)) != hipSuccess) return e;
+    if ((ks = gemm<W_DOWN, E_RESID>(g, stream, false)) == 0) return hipGetLastError();
+    if (ks > 1)
+      hipLaunchKernelGGL(reduce_resid_norm_kernel, dim3(rows), dim3(256), 0, stream, g, ks, nl, 0, xn);
+    else if (nl >= 0)
+      hipLaunchKernelGGL(rmsnorm_kernel, dim3(norm_grid), dim3(256), 0, stream, h, HID, layer_weights, nl, 0,
+                         (const bf16_t*)nullptr, xn, HID, (float*)nullptr, S);
   }
   // final norm of the last token -> hidden (bf16 values; f32 copy for the caller)
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(256), 0, stream, h + (size_t)(S - 1) * HID, HID,
@@ -722,7 +846,7 @@ hipError_t qtts_backbone_prefill(void* workspace, size_t workspace_bytes, const 
     GemmArgs g{};
     g.A = hb; g.lda = HID; g.B = static_cast<const bf16_t*>(codec_head); g.M = 1; g.N = vocab; g.K = HID;
     g.out = lg; g.ldo = vocab; g.part = part;
-    if ((e = gemm<W_DIRECT, E_STORE>(g, stream)) != hipSuccess) return e;
+    if (gemm<W_DIRECT, E_STORE>(g, stream) == 0) return hipGetLastError();
     SelParams sp{};
     sp.do_sample = sampling ? sampling->do_sample : 0;
     sp.temperature = sampling ? sampling->temperature : 1.0f;
