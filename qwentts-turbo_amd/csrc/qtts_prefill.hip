@@ -17,7 +17,7 @@
 // The f32 sums run in MFMA order rather than the CPU's, so an f32 result can land on the other
 // side of a bf16 rounding boundary now and then; parity is a tolerance, not bit equality.
 //
-// Kernels (one launch each per layer; the host loop is in qtts_backbone_prefill below):
+// Kernels (the host loop over layers is in qtts_backbone_prefill below):
 //   rmsnorm_kernel   one wave per token
 //   gemm_kernel      C = A W^T, tile 128 x 64 (4 waves, each 32 rows x 2 MFMA 32x32x16 blocks)
 //                    or, from 256 rows on, 128 x 128 (2 x 2 waves of 64 x 64), K steps of 64,
@@ -685,9 +685,10 @@ constexpr Shape kQKV{4096, HID}, kO{HID, NQH * HDIM}, kGU{2 * INTER, HID}, kDown
 // the weight-streaming small-M case)
 int tile_n(int M) { return M >= 256 ? 128 : 64; }
 
-// split-K factor: double while the tile grid is below one workgroup per CU (two per CU from 512
-// rows on, where each split still runs a long K loop) and the K range still splits into whole
-// 64-wide steps
+// split-K factor: double while the tile grid is below its target and the K range still splits
+// into whole 64-wide steps. Targets: 128 workgroups below 256 rows (every split writes a full
+// f32 partial tile, which at 128 rows outweighs the weights it streams), one per CU from 256
+// rows, two per CU from 512 rows (where each split still runs a long K loop)
 int splits_for(int M, int N, int K) {
   const int tiles = ((M + BM - 1) / BM) * (N / tile_n(M));
   const int target = M >= 512 ? 512 : (M >= 256 ? 256 : 128);
