@@ -4,6 +4,9 @@ the reference's Python side would bind them, checked against the CPU oracle.
 launch_tts_decode_with_embedding  <- fused_decode_tts.cu:834-857
 launch_tts_decode                 <- fused_decode_tts.cu:664-688 (token-id gather)
 launch_cp_decode_with_embedding   <- fused_decode_code_predictor.cu:674-697
+
+and the extended entry points (no reference counterpart): qtts_backbone_step_streams (several
+streams in one launch) and qtts_backbone_prefill (the prompt prefill, generator.py:209-225).
 """
 import ctypes
 import struct
@@ -135,3 +138,104 @@ def test_launch_cp_decode_with_embedding(lib, model):
     print(f"launch_cp_decode_with_embedding, 16 steps: worst rel_l2 {worst:.2e}", flush=True)
     assert worst < TOL
     assert rel_l2(kc[:, :, :16].cpu(), orc.k[:, :, :16]) == 0.0
+
+
+# ---- the extended entry points, bound the same way ------------------------------------------
+
+class QttsBackboneStream(ctypes.Structure):
+    """include/qwentts_amd.h QttsBackboneStream."""
+    _fields_ = [("k_cache", P), ("v_cache", P), ("position", I), ("pos3", I * 3), ("input_embedding", P),
+                ("out_hidden", P), ("out_residual", P), ("out_logits", P), ("out_token", P), ("history", P),
+                ("n_history", I), ("seed", ctypes.c_ulonglong)]
+
+
+def test_qtts_backbone_step_streams(lib, model):
+    """Three streams at positions 0, 9 and 40 of their own caches in one launch, each against the
+    oracle stepping that stream alone (kernel policy, f64 sums: rel-L2 < 1e-5)."""
+    sd, tw = model
+    layers = [[t.cuda().contiguous() for t in lw] for lw in tw.bb_layers]
+    table = _layer_table(layers)
+    norm = tw.bb_norm.cuda()
+    max_seq = 64
+    cos, sin = (t.cuda() for t in rope_tables(max_seq, 128, 1e6))
+    lib.qtts_workspace_bytes.restype = ctypes.c_size_t
+    wsb = lib.qtts_workspace_bytes()
+    ws = torch.zeros(3 * wsb, dtype=torch.uint8, device="cuda")
+    lib.qtts_workspace_init.argtypes = [P, I]
+    lib.qtts_workspace_init.restype = I
+    assert lib.qtts_workspace_init(_ptr(ws), torch.cuda.current_device()) == 0
+    fn = lib.qtts_backbone_step_streams
+    fn.argtypes = [I, P, P, I, P, P, P, I, ctypes.POINTER(QttsBackboneStream), P, I, I, F, I, I, P, I, P]
+    fn.restype = I
+    g = torch.Generator().manual_seed(8)
+    positions = [0, 9, 40]
+    bufs, orcs, xs = [], [], []
+    arr = (QttsBackboneStream * 3)()
+    for s, pos in enumerate(positions):
+        kc = torch.zeros(2, 8, max_seq, 128, dtype=torch.bfloat16)
+        vc = torch.zeros_like(kc)
+        kc[:, :, :pos] = torch.randn(2, 8, pos, 128, generator=g).to(torch.bfloat16)
+        vc[:, :, :pos] = torch.randn(2, 8, pos, 128, generator=g).to(torch.bfloat16)
+        orc = DecoderOracle(tw.bb_layers, tw.bb_norm, max_seq, "backbone", "kernel")
+        orc.set_kv(kc[:, :, :pos], vc[:, :, :pos])
+        x = torch.randn(1024, generator=g).to(torch.bfloat16)
+        b = dict(kc=kc.cuda(), vc=vc.cuda(), x=x.cuda(), hid=torch.empty(1024, device="cuda"),
+                 res=torch.empty(1024, dtype=torch.bfloat16, device="cuda"))
+        bufs.append(b); orcs.append(orc); xs.append(x)
+        st = arr[s]
+        st.k_cache, st.v_cache, st.position = b["kc"].data_ptr(), b["vc"].data_ptr(), pos
+        st.pos3[0] = st.pos3[1] = st.pos3[2] = pos
+        st.input_embedding, st.out_hidden, st.out_residual = b["x"].data_ptr(), b["hid"].data_ptr(), b["res"].data_ptr()
+    assert fn(3, _ptr(ws), _ptr(table), 2, _ptr(norm), _ptr(cos), _ptr(sin), max_seq, arr, None, 0, 0, 1.0, -1, 0,
+              None, 0, _stream()) == 0
+    torch.cuda.synchronize()
+    worst = 0.0
+    for s, pos in enumerate(positions):
+        hr, outs = orcs[s].step(xs[s], pos=pos)
+        worst = max(worst, rel_l2(bufs[s]["hid"].cpu(), hr), rel_l2(bufs[s]["res"].float().cpu(), outs[-1]))
+        assert rel_l2(bufs[s]["kc"][:, :, pos].float().cpu(), orcs[s].k[:, :, pos].float()) < TOL
+    print(f"qtts_backbone_step_streams, 3 streams: worst rel_l2 {worst:.2e}", flush=True)
+    assert worst < TOL
+    # a stream position outside the cache is rejected before any launch
+    arr[2].position = max_seq
+    assert fn(3, _ptr(ws), _ptr(table), 2, _ptr(norm), _ptr(cos), _ptr(sin), max_seq, arr, None, 0, 0, 1.0, -1, 0,
+              None, 0, _stream()) != 0
+
+
+def test_qtts_backbone_prefill(lib, model):
+    """A 20-token prompt in one call, K/V straight into the cache, against the oracle's
+    transformers-bf16 policy stepped token by token (2 layers: rel-L2 <= 1e-2)."""
+    sd, tw = model
+    layers = [[t.cuda().contiguous() for t in lw] for lw in tw.bb_layers]
+    table = _layer_table(layers)
+    norm = tw.bb_norm.cuda()
+    max_seq, S = 64, 20
+    cos, sin = (t.cuda() for t in rope_tables(max_seq, 128, 1e6))
+    lib.qtts_prefill_workspace_bytes.argtypes = [I, I]
+    lib.qtts_prefill_workspace_bytes.restype = ctypes.c_size_t
+    wsb = lib.qtts_prefill_workspace_bytes(S, 0)
+    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    fn = lib.qtts_backbone_prefill
+    fn.argtypes = [P, ctypes.c_size_t, P, I, P, P, P, P, P, I, I, I, P, P, P, P, I, P, P, I, I, I, P, I, P]
+    fn.restype = I
+    kc = torch.zeros(2, 8, max_seq, 128, dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros_like(kc)
+    x = torch.randn(S, 1024, generator=torch.Generator().manual_seed(12)).to(torch.bfloat16)
+    xd = x.cuda()
+    hid = torch.empty(1024, device="cuda")
+    assert fn(_ptr(ws), wsb, _ptr(table), 2, _ptr(norm), _ptr(cos), _ptr(sin), _ptr(kc), _ptr(vc), max_seq, 0, S,
+              None, _ptr(xd), _ptr(hid), None, 0, None, None, 0, -1, 0, None, 0, _stream()) == 0
+    torch.cuda.synchronize()
+    orc = DecoderOracle(tw.bb_layers, tw.bb_norm, max_seq, "backbone", "hf_bf16")
+    hr = None
+    for i in range(S):
+        hr, _ = orc.step(x[i], pos=i)
+    e = (rel_l2(hid.cpu(), hr), rel_l2(kc[:, :, :S].float().cpu(), orc.k[:, :, :S].float()),
+         rel_l2(vc[:, :, :S].float().cpu(), orc.v[:, :, :S].float()))
+    print(f"qtts_backbone_prefill S={S}: hidden / K / V rel_l2 {e[0]:.2e} {e[1]:.2e} {e[2]:.2e}", flush=True)
+    assert max(e) < 1e-2
+    # too small a workspace, or a prompt past the cache, is rejected before any launch
+    assert fn(_ptr(ws), wsb - 256, _ptr(table), 2, _ptr(norm), _ptr(cos), _ptr(sin), _ptr(kc), _ptr(vc), max_seq, 0,
+              S, None, _ptr(xd), _ptr(hid), None, 0, None, None, 0, -1, 0, None, 0, _stream()) != 0
+    assert fn(_ptr(ws), wsb, _ptr(table), 2, _ptr(norm), _ptr(cos), _ptr(sin), _ptr(kc), _ptr(vc), max_seq, 50, S,
+              None, _ptr(xd), _ptr(hid), None, 0, None, None, 0, -1, 0, None, 0, _stream()) != 0
