@@ -174,11 +174,16 @@ __global__ void __launch_bounds__(GT, 2) gemm_kernel(const GemmArgs g) {
   }
 
   // register stages two tiles ahead of the MFMAs (tile kt + 2 loads while tile kt computes and
-  // tile kt + 1 moves to LDS): twice the weight bytes in flight of a plain double buffer
+  // tile kt + 1 moves to LDS): twice the weight bytes in flight of a plain double buffer. Every
+  // load is issued unconditionally (rows past M read row 0 and are zeroed afterwards): a load
+  // under a branch makes the compiler wait for all outstanding loads instead of just the old ones.
   u32x4 ra[2][4], rb[2][NBR];
   auto gload = [&](int k0, u32x4 (&a)[4], u32x4 (&b)[NBR]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) a[i] = aok[i] ? ldw(arow[i] + k0) : u32x4{0u, 0u, 0u, 0u};
+    for (int i = 0; i < 4; ++i) {
+      const u32x4 v = ldw(arow[i] + k0);
+      a[i] = aok[i] ? v : u32x4{0u, 0u, 0u, 0u};
+    }
 #pragma unroll
     for (int i = 0; i < NBR; ++i) b[i] = ldw(brow[i] + k0);
   };
@@ -510,37 +515,60 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
   {
     const bf16_t* qp = qkv + (size_t)(qok ? i : 0) * QKVW + hq * HDIM + 8 * hf;
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) qr[kk] = qok ? ldw(qp + 16 * kk) : u32x4{0u, 0u, 0u, 0u};
+    for (int kk = 0; kk < 8; ++kk) {
+      const u32x4 v = ldw(qp + 16 * kk);   // unconditional (clamped row): see loadk
+      qr[kk] = qok ? v : u32x4{0u, 0u, 0u, 0u};
+    }
   }
   const size_t hbase = ((size_t)layer * NKVH + kvh) * max_seq * HDIM;
   const bf16_t* kb_ = kc + hbase;
   const bf16_t* vb_ = vc + hbase;
 
-  auto scores = [&](int kb, float (&sc)[16]) {
+  // K rows of block kb for this lane (key 32 kb + c, dims 16 kk + 8 hf ..), issued a block ahead.
+  // Loads are unconditional from a clamped row and zeroed afterwards: a load under a branch
+  // would make the compiler wait for every outstanding load, the prefetch included.
+  auto loadk = [&](int kb, u32x4 (&kr)[8]) {
     const int key = 32 * kb + c;
-    const bool kok = key <= last;
+    const bool kok = kb < nkb && key <= last;
     const bf16_t* kp = kb_ + (size_t)(kok ? key : 0) * HDIM + 8 * hf;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const u32x4 v = ldw(kp + 16 * kk);
+      kr[kk] = kok ? v : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto scores = [&](int kb, const u32x4 (&kr)[8], float (&sc)[16]) {
     f32x16 acc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      const u32x4 a = kok ? ldw(kp + 16 * kk) : u32x4{0u, 0u, 0u, 0u};
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(a), as_bf8(qr[kk]), acc, 0, 0, 0);
-    }
+    for (int kk = 0; kk < 8; ++kk)
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(kr[kk]), as_bf8(qr[kk]), acc, 0, 0, 0);
+    // blocks that every query of the block sees whole (the wave-uniform common case) skip the mask
+    if (32 * kb + 31 <= p0 + 32 * qb && 32 * qb + 31 < S) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int kr = 32 * kb + 8 * (r >> 2) + 4 * hf + (r & 3);
-      const float v = rbh(rbh(acc[r]) * scale);
-      sc[r] = (qok && kr <= qpos) ? v : -INFINITY;
+      for (int r = 0; r < 16; ++r) sc[r] = rbh(rbh(acc[r]) * scale);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kr = 32 * kb + 8 * (r >> 2) + 4 * hf + (r & 3);
+        const float v = rbh(rbh(acc[r]) * scale);
+        sc[r] = (qok && kr <= qpos) ? v : -INFINITY;
+      }
     }
   };
+  // e^(s - m) as 2^(s log2 e - m log2 e): one fma into the hardware exp2
+  constexpr float L2E = 1.4426950408889634f;
+  auto ex = [](float s, float nm) { return __builtin_amdgcn_exp2f(fmaf(s, L2E, nm)); };
 
   // pass 1: this wave's row maximum and softmax denominator
   float m = -INFINITY, l = 0.0f;
-  for (int kb = w; kb < nkb; kb += AW) {
+  u32x4 kq[2][8];
+  loadk(w, kq[0]);
+  auto pass1 = [&](int kb, const u32x4 (&kr)[8], u32x4 (&kn)[8]) {
+    loadk(kb + AW, kn);
     float sc[16];
-    scores(kb, sc);
+    scores(kb, kr, sc);
     float bm = sc[0];
 #pragma unroll
     for (int r = 1; r < 16; ++r) bm = fmaxf(bm, sc[r]);
@@ -548,12 +576,16 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
     // (no branch around the MFMAs: a fully masked block leaves m and l unchanged; masked scores
     // are -inf, whose exp is 0, and a still fully masked row subtracts 0 instead of -inf)
     const float mn = fmaxf(m, bm);
-    const float mr = mn == -INFINITY ? 0.0f : mn;
+    const float nm = mn == -INFINITY ? 0.0f : -mn * L2E;
     float add = 0.0f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) add += __expf(sc[r] - mr);
+    for (int r = 0; r < 16; ++r) add += ex(sc[r], nm);
     l = m == -INFINITY ? add : l * __expf(m - mn) + add;
     m = mn;
+  };
+  for (int kb = w; kb < nkb; kb += 2 * AW) {
+    pass1(kb, kq[0], kq[1]);
+    if (kb + AW < nkb) pass1(kb + AW, kq[1], kq[0]);
   }
   l += __shfl_xor(l, 32, 64);
   if (hf == 0) {
@@ -575,7 +607,7 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
     l = L;
   }
   const float rl = l > 0.0f ? 1.0f / l : 0.0f;   // softmax scale (torch multiplies by 1 / sum too)
-  const float mr = m == -INFINITY ? 0.0f : m;
+  const float nm = m == -INFINITY ? 0.0f : -m * L2E;
 
   // pass 2: p = bf16(e * (1 / l)), O^T += V^T P^T over this wave's blocks
   f32x16 o[4];
@@ -584,19 +616,27 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[mb][r] = 0.0f;
   const int kp2 = lane & 15, dg = 32 * (lane >> 4);
-  for (int kb = w; kb < nkb; kb += AW) {
+  loadk(w, kq[0]);
+  auto pass2 = [&](int kb, const u32x4 (&kr)[8], u32x4 (&kn)[8]) {
+    loadk(kb + AW, kn);
     float sc[16];
-    scores(kb, sc);
+    scores(kb, kr, sc);
     // stage V rows 2 kp2, 2 kp2 + 1 of the block, dims dg .. dg + 31, transposed into vt[d][key]
     {
       const int k0 = 32 * kb + 2 * kp2;
       const bool ok0 = k0 <= last, ok1 = k0 + 1 <= last;
       const bf16_t* v0 = vb_ + (size_t)(ok0 ? k0 : 0) * HDIM + dg;
       const bf16_t* v1 = vb_ + (size_t)(ok1 ? k0 + 1 : 0) * HDIM + dg;
+      u32x4 va[4], vb[4];
 #pragma unroll
       for (int dd = 0; dd < 4; ++dd) {
-        const u32x4 a = ok0 ? ldw(v0 + 8 * dd) : u32x4{0u, 0u, 0u, 0u};
-        const u32x4 b = ok1 ? ldw(v1 + 8 * dd) : u32x4{0u, 0u, 0u, 0u};
+        va[dd] = ldw(v0 + 8 * dd);   // unconditional (clamped rows): see loadk
+        vb[dd] = ldw(v1 + 8 * dd);
+      }
+#pragma unroll
+      for (int dd = 0; dd < 4; ++dd) {
+        const u32x4 a = ok0 ? va[dd] : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 b = ok1 ? vb[dd] : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int d = dg + 8 * dd + 2 * e;
@@ -612,7 +652,7 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
       u32x4 pb;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        pb[j] = pack_bh(__expf(sc[8 * kk2 + 2 * j] - mr) * rl, __expf(sc[8 * kk2 + 2 * j + 1] - mr) * rl);
+        pb[j] = pack_bh(ex(sc[8 * kk2 + 2 * j], nm) * rl, ex(sc[8 * kk2 + 2 * j + 1], nm) * rl);
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
         const bf16_t* vr = &vt[(32 * mb + c) * VTROW + 16 * kk2 + 4 * hf];
@@ -623,6 +663,10 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  };
+  for (int kb = w; kb < nkb; kb += 2 * AW) {
+    pass2(kb, kq[0], kq[1]);
+    if (kb + AW < nkb) pass2(kb + AW, kq[1], kq[0]);
   }
   // partial O^T of waves 1.. to LDS (the V^T rows are dead), added in wave order by wave 0
   __syncthreads();
