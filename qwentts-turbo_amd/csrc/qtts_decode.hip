@@ -1402,17 +1402,22 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       // Each tile is loaded one step ahead of its use, right after the step's own compute,
       // so at most the tile in use and the next one are live.
       // XL: a GEMV stage runs the workgroup's 8 row groups; each group's tile is issued one group
-      // ahead into the second register set (the first group's a step ahead, as in batch 1)
+      // ahead into the second register set (the first group's a step ahead, as in batch 1). The
+      // last pair is peeled off the loop so that no tile load sits under a branch: the compiler
+      // then waits only for the tile in use, not for the one in flight behind it.
       auto qkv_stage = [&](int layer_) {
         if constexpr (XL) {
           TileQKV t1;
 #pragma unroll 1
-          for (int sub = 0; sub < NSUB; sub += 2) {
+          for (int sub = 0; sub < NSUB - 2; sub += 2) {
             load_qkv<BB>(t1, LW, layer_, xcd, li + sub + 1, mw, lane);
             math_qkv(lp, li + sub, tq);
-            if (sub + 2 < NSUB) load_qkv<BB>(tq, LW, layer_, xcd, li + sub + 2, mw, lane);
+            load_qkv<BB>(tq, LW, layer_, xcd, li + sub + 2, mw, lane);
             math_qkv(lp, li + sub + 1, t1);
           }
+          load_qkv<BB>(t1, LW, layer_, xcd, li + NSUB - 1, mw, lane);
+          math_qkv(lp, li + NSUB - 2, tq);
+          math_qkv(lp, li + NSUB - 1, t1);
         } else {
           math_qkv(lp, li, tq);
         }
@@ -1421,12 +1426,15 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
         if constexpr (XL) {
           TileO t1;
 #pragma unroll 1
-          for (int sub = 0; sub < NSUB; sub += 2) {
+          for (int sub = 0; sub < NSUB - 2; sub += 2) {
             load_o<BB>(t1, LW, layer_, xcd, li + sub + 1, mw, lane);
             math_o(lp, li + sub, to);
-            if (sub + 2 < NSUB) load_o<BB>(to, LW, layer_, xcd, li + sub + 2, mw, lane);
+            load_o<BB>(to, LW, layer_, xcd, li + sub + 2, mw, lane);
             math_o(lp, li + sub + 1, t1);
           }
+          load_o<BB>(t1, LW, layer_, xcd, li + NSUB - 1, mw, lane);
+          math_o(lp, li + NSUB - 2, to);
+          math_o(lp, li + NSUB - 1, t1);
         } else {
           math_o(lp, li, to);
         }
@@ -1435,12 +1443,15 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
         if constexpr (XL) {
           TileGU t1;
 #pragma unroll 1
-          for (int sub = 0; sub < NSUB; sub += 2) {
+          for (int sub = 0; sub < NSUB - 2; sub += 2) {
             load_gu<BB>(t1, LW, layer_, xcd, li + sub + 1, mw, lane);
             math_gu(lp, li + sub, tgu);
-            if (sub + 2 < NSUB) load_gu<BB>(tgu, LW, layer_, xcd, li + sub + 2, mw, lane);
+            load_gu<BB>(tgu, LW, layer_, xcd, li + sub + 2, mw, lane);
             math_gu(lp, li + sub + 1, t1);
           }
+          load_gu<BB>(t1, LW, layer_, xcd, li + NSUB - 1, mw, lane);
+          math_gu(lp, li + NSUB - 2, tgu);
+          math_gu(lp, li + NSUB - 1, t1);
         } else {
           math_gu(lp, li, tgu);
         }
@@ -1449,12 +1460,15 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
         if constexpr (XL) {
           TileD t1;
 #pragma unroll 1
-          for (int sub = 0; sub < NSUB; sub += 2) {
+          for (int sub = 0; sub < NSUB - 2; sub += 2) {
             load_d<BB>(t1, LW, layer_, xcd, li + sub + 1, mw, lane);
             math_down(lp, li + sub, td);
-            if (sub + 2 < NSUB) load_d<BB>(td, LW, layer_, xcd, li + sub + 2, mw, lane);
+            load_d<BB>(td, LW, layer_, xcd, li + sub + 2, mw, lane);
             math_down(lp, li + sub + 1, t1);
           }
+          load_d<BB>(t1, LW, layer_, xcd, li + NSUB - 1, mw, lane);
+          math_down(lp, li + NSUB - 2, td);
+          math_down(lp, li + NSUB - 1, t1);
         } else {
           math_down(lp, li, td);
         }
@@ -1466,16 +1480,18 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           TileQKV t1;
           int row0, nrows;
 #pragma unroll 1
-          for (int sub = 0; sub < NSUB; sub += 2) {
+          for (int sub = 0; sub < NSUB - 2; sub += 2) {
             head_rows(sub + 1, row0, nrows);
             load_head<BB>(t1, head_weights(pi), row0, nrows, lane);
             head_group(pi, sub, tq, bv, bi);
-            if (sub + 2 < NSUB) {
-              head_rows(sub + 2, row0, nrows);
-              load_head<BB>(tq, head_weights(pi), row0, nrows, lane);
-            }
+            head_rows(sub + 2, row0, nrows);
+            load_head<BB>(tq, head_weights(pi), row0, nrows, lane);
             head_group(pi, sub + 1, t1, bv, bi);
           }
+          head_rows(NSUB - 1, row0, nrows);
+          load_head<BB>(t1, head_weights(pi), row0, nrows, lane);
+          head_group(pi, NSUB - 2, tq, bv, bi);
+          head_group(pi, NSUB - 1, t1, bv, bi);
         } else {
           head_group(pi, 0, tq, bv, bi);
         }
