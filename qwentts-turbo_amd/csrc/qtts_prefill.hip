@@ -493,7 +493,8 @@ __global__ void __launch_bounds__(256) reduce_resid_norm_kernel(const GemmArgs g
 // O^T = V^T P^T, reusing the score registers as the B operand in place (k-index 8 hf + j of step
 // kk2 is key 16 kk2 + 8 (j >> 2) + 4 hf + (j & 3); each wave's V^T block is staged in its own LDS
 // rows [d][key] and read in that order). The AW partial O^T are added in wave order by wave 0.
-// Query blocks are issued last-first: the longest rows start earliest.
+// Grid: 16 x (query blocks) workgroups, KV head = linear id mod 8 (one head per XCD's L2), the
+// longest query blocks first.
 constexpr int AW = 4;
 constexpr int ATT_SMEM = std::max(AW * HDIM * VTROW * 2, (AW - 1) * HDIM * 32 * 4);
 
@@ -503,7 +504,11 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
   __shared__ __attribute__((aligned(16))) char smem[ATT_SMEM];
   __shared__ float sml[AW][2][32];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hf = lane >> 5, c = lane & 31;
-  const int qb = gridDim.x - 1 - blockIdx.x, hq = blockIdx.y, kvh = hq >> 1;
+  // XCD-aware order: workgroups go to the XCDs round-robin by linear id, so id & 7 picks the KV
+  // head and each XCD's L2 holds one head's K and V; within it, the longest query blocks first
+  const int nqb = (S + 31) / 32, id = blockIdx.x;
+  const int kvh = id & 7, rest = id >> 3;
+  const int hq = 2 * kvh + (rest & 1), qb = nqb - 1 - (rest >> 1);
   const int i = 32 * qb + c;
   const bool qok = i < S;
   const int qpos = p0 + i;
@@ -538,12 +543,17 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
     }
   };
   auto scores = [&](int kb, const u32x4 (&kr)[8], float (&sc)[16]) {
-    f32x16 acc;
+    // two independent 4-step MFMA chains (even and odd 16-dim steps), added at the end
+    f32x16 acc, acc2;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    for (int r = 0; r < 16; ++r) acc[r] = acc2[r] = 0.0f;
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
+    for (int kk = 0; kk < 8; kk += 2) {
       acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(kr[kk]), as_bf8(qr[kk]), acc, 0, 0, 0);
+      acc2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(kr[kk + 1]), as_bf8(qr[kk + 1]), acc2, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] += acc2[r];
     // blocks that every query of the block sees whole (the wave-uniform common case) skip the mask
     if (32 * kb + 31 <= p0 + 32 * qb && 32 * qb + 31 < S) {
 #pragma unroll
@@ -860,7 +870,7 @@ hipError_t qtts_backbone_prefill(void* workspace, size_t workspace_bytes, const 
     else
       hipLaunchKernelGGL(rope_kv_kernel, dim3(rows), dim3(256), 0, stream, qkv, layer_weights, l, cs, sn, pos3, position,
                          S, kc, vc, max_seq_len);
-    hipLaunchKernelGGL(attn_kernel, dim3((S + 31) / 32, NQH), dim3(64 * AW), 0, stream, qkv, kc, vc, l, max_seq_len,
+    hipLaunchKernelGGL(attn_kernel, dim3((S + 31) / 32 * NQH), dim3(64 * AW), 0, stream, qkv, kc, vc, l, max_seq_len,
                        position, S, att, scale);
     // O + residual, then the post-attention norm (fused with the split-K reduction)
     g.A = att; g.lda = NQH * HDIM; g.N = kO.N; g.K = kO.K; g.out = h; g.ldo = HID; g.res = h; g.ldr = HID;
