@@ -49,9 +49,11 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr float EPS = 1e-6f;                 // Qwen3RMSNorm eps (config rms_norm_eps)
-constexpr int BM = 128, BK = 64;             // GEMM tile rows and K step (columns: 64 or 128)
+constexpr int BM = 128;                      // GEMM tile rows (columns TN: 64 or 128)
 constexpr int GT = 256;                      // GEMM threads (4 waves)
-constexpr int LROW = BK + 8;                 // LDS row (bf16): 144 B, 16-byte aligned, skewed banks
+// K step of a TN-column tile: 128 for the 64-column (small-M, latency-bound) tiles, whose short
+// K loops then take half the load round trips; 64 for the 128-column tiles
+template <int TN> constexpr int bk_of() { return TN == 64 ? 128 : 64; }
 constexpr int QKVW = 4096;                   // q | k | v row of one token
 constexpr int VTROW = 40;                    // LDS row of V^T (32 keys + pad, 8-byte aligned reads)
 constexpr int MAX_SPLIT = 16;
@@ -128,14 +130,19 @@ __device__ __forceinline__ int swiglu_gate_col(int j) {
 // and columns 64 (w >> 1) .. + 63 (two 32-column blocks): one LDS operand read per MFMA.
 template <int WM, int EPI, int TN>
 __global__ void __launch_bounds__(GT, 2) gemm_kernel(const GemmArgs g) {
+  constexpr int BK = bk_of<TN>();
+  constexpr int LROW = BK + 8;                     // LDS row (bf16): 16-byte aligned, skewed banks
+  constexpr int CPR = BK / 8;                      // 16-byte chunks per tile row
+  constexpr int RPP = GT / CPR;                    // tile rows one pass of the workgroup loads
+  constexpr int NAR = BM / RPP;                    // A chunks per thread
+  constexpr int NBR = TN / RPP;                    // B chunks per thread
   constexpr int MBW = TN == 128 ? 2 : 1;          // 32-row blocks per wave
-  constexpr int NBR = TN / 32;                     // B rows staged per thread
   __shared__ __attribute__((aligned(16))) bf16_t sa[2][BM * LROW];
   __shared__ __attribute__((aligned(16))) bf16_t sb[2][TN * LROW];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * TN;
   const int kbeg = blockIdx.z * g.kchunk, nk = g.kchunk / BK;
-  const int lr = t >> 3, lc = (t & 7) * 8;   // this thread's load row (within 32) and column
+  const int lr = t / CPR, lc = (t % CPR) * 8;   // this thread's load row (within RPP) and column
   const int wr0 = TN == 128 ? 64 * (w & 1) : 32 * w;   // wave's first tile row
   const int wc0 = TN == 128 ? 64 * (w >> 1) : 0;       // wave's first tile column
 
@@ -145,7 +152,7 @@ __global__ void __launch_bounds__(GT, 2) gemm_kernel(const GemmArgs g) {
     const TTSLayerWeights* lw = g.layers + g.layer;
 #pragma unroll
     for (int i = 0; i < NBR; ++i) {
-      const int n = n0 + lr + 32 * i;
+      const int n = n0 + lr + RPP * i;
       const bf16_t* p;
       if constexpr (WM == W_DIRECT) {
         p = g.B + (size_t)n * g.K;
@@ -164,11 +171,11 @@ __global__ void __launch_bounds__(GT, 2) gemm_kernel(const GemmArgs g) {
       brow[i] = p + kbeg + lc;
     }
   }
-  const bf16_t* arow[4];
-  bool aok[4];
+  const bf16_t* arow[NAR];
+  bool aok[NAR];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int m = m0 + lr + 32 * i;
+  for (int i = 0; i < NAR; ++i) {
+    const int m = m0 + lr + RPP * i;
     aok[i] = m < g.M;
     arow[i] = g.A + (size_t)(aok[i] ? m : 0) * g.lda + kbeg + lc;
   }
@@ -177,21 +184,21 @@ __global__ void __launch_bounds__(GT, 2) gemm_kernel(const GemmArgs g) {
   // tile kt + 1 moves to LDS): twice the weight bytes in flight of a plain double buffer. Every
   // load is issued unconditionally (rows past M read row 0 and are zeroed afterwards): a load
   // under a branch makes the compiler wait for all outstanding loads instead of just the old ones.
-  u32x4 ra[2][4], rb[2][NBR];
-  auto gload = [&](int k0, u32x4 (&a)[4], u32x4 (&b)[NBR]) {
+  u32x4 ra[2][NAR], rb[2][NBR];
+  auto gload = [&](int k0, u32x4 (&a)[NAR], u32x4 (&b)[NBR]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NAR; ++i) {
       const u32x4 v = ldw(arow[i] + k0);
       a[i] = aok[i] ? v : u32x4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
     for (int i = 0; i < NBR; ++i) b[i] = ldw(brow[i] + k0);
   };
-  auto sstore = [&](int buf, const u32x4 (&a)[4], const u32x4 (&b)[NBR]) {
+  auto sstore = [&](int buf, const u32x4 (&a)[NAR], const u32x4 (&b)[NBR]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(&sa[buf][(lr + 32 * i) * LROW + lc]) = a[i];
+    for (int i = 0; i < NAR; ++i) *reinterpret_cast<u32x4*>(&sa[buf][(lr + RPP * i) * LROW + lc]) = a[i];
 #pragma unroll
-    for (int i = 0; i < NBR; ++i) *reinterpret_cast<u32x4*>(&sb[buf][(lr + 32 * i) * LROW + lc]) = b[i];
+    for (int i = 0; i < NBR; ++i) *reinterpret_cast<u32x4*>(&sb[buf][(lr + RPP * i) * LROW + lc]) = b[i];
   };
 
   f32x16 acc[MBW][2];
@@ -222,7 +229,7 @@ __global__ void __launch_bounds__(GT, 2) gemm_kernel(const GemmArgs g) {
     }
   };
   // one step: tile kt in LDS buffer kt & 1, tile kt + 1 in register stage S1, stage S0 free
-  auto step = [&](int kt, u32x4 (&a0)[4], u32x4 (&b0)[NBR], const u32x4 (&a1)[4], const u32x4 (&b1)[NBR]) {
+  auto step = [&](int kt, u32x4 (&a0)[NAR], u32x4 (&b0)[NBR], const u32x4 (&a1)[NAR], const u32x4 (&b1)[NBR]) {
     if (kt + 2 < nk) gload((kt + 2) * BK, a0, b0);
     compute(kt & 1);
     if (kt + 1 < nk) sstore((kt + 1) & 1, a1, b1);
@@ -744,10 +751,11 @@ int tile_n(int M) { return M >= 256 ? 128 : 64; }
 // f32 partial tile, which at 128 rows outweighs the weights it streams), one per CU from 256
 // rows, two per CU from 512 rows (where each split still runs a long K loop)
 int splits_for(int M, int N, int K) {
-  const int tiles = ((M + BM - 1) / BM) * (N / tile_n(M));
+  const int tn = tile_n(M), bk = tn == 64 ? bk_of<64>() : bk_of<128>();
+  const int tiles = ((M + BM - 1) / BM) * (N / tn);
   const int target = M >= 512 ? 512 : (M >= 256 ? 256 : 128);
   int ks = 1;
-  while (tiles * ks < target && ks < MAX_SPLIT && (K / BK) % (2 * ks) == 0) ks *= 2;
+  while (tiles * ks < target && ks < MAX_SPLIT && (K / bk) % (2 * ks) == 0) ks *= 2;
   return ks;
 }
 
