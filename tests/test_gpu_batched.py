@@ -134,3 +134,35 @@ def test_backbone_streams_reject_bad_arguments(pkg):
     with pytest.raises(RuntimeError, match="KV cache full"):
         lead.decode_steps_streams([lead, other], x2, torch.zeros(2, **i32), h2, *args)
     assert lead.position() == 0 and other.position() == 16
+
+
+@pytest.mark.parametrize("n,sample", [(3, False), (9, True)], ids=["greedy3", "sampled9"])
+def test_cp_frames_streams_match_batch1(pkg, n, sample):
+    """Code-predictor frames of n streams through BatchedTTSDecoder.cp_frames (up to 8 per launch,
+    stream s on XCD s) against the batch-1 frame() of each stream with the same key (seed + s):
+    the 15 group ids and the combined next input bit-identical; 9 streams take two launches; the
+    sampled case draws every group with temperature and top-k."""
+    cfg = pkg.SyntheticConfig(n_bb_layers=1, n_cp_layers=2, n_groups=15)
+    dsd = {k: v.cuda() for k, v in pkg.synthetic_state_dict(seed=40 + n, cfg=cfg).items()}
+    dec = pkg.BatchedTTSDecoder(dsd, n, max_seq_len=16)
+    g = torch.Generator().manual_seed(n)
+    hid = torch.randn(n, 1024, generator=g).cuda()
+    i32 = dict(dtype=torch.int32, device="cuda")
+    g0 = torch.randint(0, 2048, (n,), generator=g, dtype=torch.int32).cuda()
+    text = torch.randn(n, 1024, generator=g).to(torch.bfloat16).cuda()
+    toks = torch.full((n, 16), -1, **i32)
+    comb = torch.empty(n, 1024, dtype=torch.bfloat16, device="cuda")
+    kw = dict(do_sample=sample, temperature=0.8, top_k=30, seed=11, frame_step=5)
+    print(f"cp frames {n} streams sample={sample}: launching", flush=True)
+    dec.cp_frames(hid, g0, text, toks, comb, **kw)
+    cp = dec.cp.decoder
+    for s in range(n):
+        t1 = torch.full((16,), -1, **i32)
+        c1 = torch.empty(1024, dtype=torch.bfloat16, device="cuda")
+        cp.frame(hid[s].contiguous(), g0[s:s + 1], text[s].contiguous(), t1, c1, -1, torch.zeros(1, **i32), sample,
+                 kw["temperature"], kw["top_k"], 1.0, kw["seed"] + s, kw["frame_step"])
+        torch.cuda.synchronize()
+        assert torch.equal(toks[s], t1), f"stream {s}: {toks[s].tolist()} vs {t1.tolist()}"
+        assert torch.equal(comb[s], c1), f"stream {s}: combined input differs"
+    dec.check_error()
+    print(f"cp frames {n} streams: first stream groups {toks[0, 1:6].tolist()}...", flush=True)
