@@ -129,7 +129,7 @@ __device__ __forceinline__ int swiglu_gate_col(int j) {
 // blocks. TN = 128: waves form 2 x 2, wave w owns rows 64 (w & 1) .. + 63 (two 32-row blocks)
 // and columns 64 (w >> 1) .. + 63 (two 32-column blocks): one LDS operand read per MFMA.
 template <int WM, int EPI, int TN>
-__global__ void __launch_bounds__(GT, 2) gemm_kernel(const GemmArgs g) {
+__global__ void __launch_bounds__(GT, TN == 128 ? 2 : 1) gemm_kernel(const GemmArgs g) {
   constexpr int BK = bk_of<TN>();
   constexpr int LROW = BK + 8;                     // LDS row (bf16): 16-byte aligned, skewed banks
   constexpr int CPR = BK / 8;                      // 16-byte chunks per tile row
