@@ -11,7 +11,8 @@ Prints one JSON line (see the repository's bench contract) with:
   roofline      algorithmic bytes / kernel time for the dominant kernel, timed with HIP events
                 on the launch stream, against MI355X's 8 TB/s
   cpu_baseline  the same frame through the CPU oracle's HF-bf16 path (eager PyTorch, bf16
-                weights) on this host, timed on a bounded sample of frames
+                weights) on this host, timed on a bounded sample of frames; also split into
+                backbone steps/s (config 0's unit) and code-predictor steps/s (config 1's)
 """
 from __future__ import annotations
 
@@ -73,7 +74,10 @@ def cpu_baseline(sample_seconds: float = 15.0) -> dict:
     hidden = torch.randn(1024, generator=g)
     x = torch.randn(1024, generator=g).to(torch.bfloat16)
 
+    t_parts = [0.0, 0.0]   # code predictor, backbone
+
     def frame(hidden, x):
+        t = time.perf_counter()
         cp.reset()
         cp.step(rb(hidden).to(torch.bfloat16), pos=0)
         h, _ = cp.step(tw.codec_embedding[5].to(torch.bfloat16), pos=1)
@@ -82,11 +86,15 @@ def cpu_baseline(sample_seconds: float = 15.0) -> dict:
             if gi:
                 h, _ = cp.step(embs[gi - 1][toks[-1]], pos=gi + 1)
             toks.append(int(torch.argmax(torch.mv(heads[gi], h.to(torch.bfloat16)).float())))
+        t1 = time.perf_counter()
         hb, _ = bb.step(x, pos=511)
         lg = torch.mv(codec_head, hb.to(torch.bfloat16)).float()
+        t_parts[0] += t1 - t
+        t_parts[1] += time.perf_counter() - t1
         return hb, int(torch.argmax(lg))
 
     frame(hidden, x)  # warm-up
+    t_parts[0] = t_parts[1] = 0.0
     n, t0 = 0, time.perf_counter()
     while True:
         frame(hidden, x)
@@ -95,6 +103,7 @@ def cpu_baseline(sample_seconds: float = 15.0) -> dict:
         if el >= sample_seconds or n >= 500:
             break
     return {"value": n / el, "unit": "frames/s", "cores": threads, "kind": "port",
+            "backbone_steps_per_s": round(n / t_parts[1], 2), "cp_steps_per_s": round(15 * n / t_parts[0], 2),
             "sample": f"{n} frames (1 backbone step at 512 context + 16 code-predictor steps, HF-bf16 eager "
                       f"PyTorch oracle) in {el:.1f} s"}
 
