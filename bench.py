@@ -12,7 +12,8 @@ Prints one JSON line (see the repository's bench contract) with:
                 on the launch stream, against MI355X's 8 TB/s
   cpu_baseline  the same frame through the CPU oracle's HF-bf16 path (eager PyTorch, bf16
                 weights) on this host, timed on a bounded sample of frames; also split into
-                backbone steps/s (config 0's unit) and code-predictor steps/s (config 1's)
+                backbone steps/s (config 0's unit) and code-predictor steps/s (config 1's), plus
+                the prefill's tokens/s (the oracle's bf16 policy, the reference's prefill arithmetic)
 """
 from __future__ import annotations
 
@@ -102,8 +103,21 @@ def cpu_baseline(sample_seconds: float = 15.0) -> dict:
         el = time.perf_counter() - t0
         if el >= sample_seconds or n >= 500:
             break
+    # the prefill (scope row f3): the oracle's bf16 policy over a prompt from position 0, on a
+    # bounded sample of tokens (about 3 s)
+    pf = DecoderOracle(tw.bb_layers, tw.bb_norm, 520, "backbone", "hf_bf16")
+    xs = torch.randn(64, 1024, generator=g).to(torch.bfloat16)
+    pf.step(xs[0], pos=0)
+    npf, tp0 = 0, time.perf_counter()
+    while npf < 63:
+        pf.step(xs[npf + 1], pos=npf + 1)
+        npf += 1
+        if time.perf_counter() - tp0 >= 3.0:
+            break
+    pf_rate = npf / (time.perf_counter() - tp0)
     return {"value": n / el, "unit": "frames/s", "cores": threads, "kind": "port",
             "backbone_steps_per_s": round(n / t_parts[1], 2), "cp_steps_per_s": round(15 * n / t_parts[0], 2),
+            "prefill_tokens_per_s": round(pf_rate, 2),
             "sample": f"{n} frames (1 backbone step at 512 context + 16 code-predictor steps, HF-bf16 eager "
                       f"PyTorch oracle) in {el:.1f} s"}
 
