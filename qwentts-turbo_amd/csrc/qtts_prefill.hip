@@ -55,7 +55,8 @@ constexpr int GT = 256;                      // GEMM threads (4 waves)
 // K loops then take half the load round trips; 64 for the 128-column tiles
 template <int TN> constexpr int bk_of() { return TN == 64 ? 128 : 64; }
 constexpr int QKVW = 4096;                   // q | k | v row of one token
-constexpr int VTROW = 40;                    // LDS row of V^T (32 keys + pad, 8-byte aligned reads)
+constexpr int VTROW = 36;                    // LDS row of V^T: 32 keys + pad; 72 B keeps the 8-byte
+                                             // reads aligned and puts rows 8 apart 16 banks apart
 constexpr int MAX_SPLIT = 16;
 
 enum WMode { W_DIRECT, W_QKV, W_O, W_GU, W_DOWN };
@@ -632,7 +633,9 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
   for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[mb][r] = 0.0f;
-  const int kp2 = lane & 15, dg = 32 * (lane >> 4);
+  // staging: lane (group dgr = lane >> 4, pair kp2 = lane & 15) moves keys 2 kp2, 2 kp2 + 1 of dims
+  // 32 dd + 8 dgr + 0..7: the four groups write rows 8 apart, i.e. different banks
+  const int kp2 = lane & 15, dgr = lane >> 4;
   loadk(w, kq[0]);
   auto pass2 = [&](int kb, const u32x4 (&kr)[8], u32x4 (&kn)[8]) {
     loadk(kb + AW, kn);
@@ -642,13 +645,13 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
     {
       const int k0 = 32 * kb + 2 * kp2;
       const bool ok0 = k0 <= last, ok1 = k0 + 1 <= last;
-      const bf16_t* v0 = vb_ + (size_t)(ok0 ? k0 : 0) * HDIM + dg;
-      const bf16_t* v1 = vb_ + (size_t)(ok1 ? k0 + 1 : 0) * HDIM + dg;
+      const bf16_t* v0 = vb_ + (size_t)(ok0 ? k0 : 0) * HDIM + 8 * dgr;
+      const bf16_t* v1 = vb_ + (size_t)(ok1 ? k0 + 1 : 0) * HDIM + 8 * dgr;
       u32x4 va[4], vb[4];
 #pragma unroll
       for (int dd = 0; dd < 4; ++dd) {
-        va[dd] = ldw(v0 + 8 * dd);   // unconditional (clamped rows): see loadk
-        vb[dd] = ldw(v1 + 8 * dd);
+        va[dd] = ldw(v0 + 32 * dd);   // unconditional (clamped rows): see loadk
+        vb[dd] = ldw(v1 + 32 * dd);
       }
 #pragma unroll
       for (int dd = 0; dd < 4; ++dd) {
@@ -656,7 +659,7 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
         const u32x4 b = ok1 ? vb[dd] : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int d = dg + 8 * dd + 2 * e;
+          const int d = 32 * dd + 8 * dgr + 2 * e;
           *reinterpret_cast<uint32_t*>(&vt[d * VTROW + 2 * kp2]) = (a[e] & 0xffffu) | (b[e] << 16);
           *reinterpret_cast<uint32_t*>(&vt[(d + 1) * VTROW + 2 * kp2]) = (a[e] >> 16) | (b[e] & 0xffff0000u);
         }
