@@ -145,3 +145,32 @@ def test_prefill_rejects_bad_arguments(pkg, small):
         bb.prefill(torch.zeros(2, 1024, dtype=torch.bfloat16, device="cuda"),
                    pos3=torch.zeros(3, 3, dtype=torch.int32, device="cuda"))
     assert bb.position == 60
+
+
+def test_prefill_then_decode_handoff(pkg, small):
+    """The decode kernel continues from the cache the prefill wrote (generator.py:104-119 then
+    :152-172): a 100-token prompt, then 3 backbone decode steps with the codec head. The oracle
+    does the same, prefilling with its bf16 policy and handing that KV to its kernel policy. The
+    decode hidden states agree within the prefill's tolerance, since the two caches differ only
+    at bf16 rounding level."""
+    dsd, tw = small
+    S = 100
+    bb = pkg.TTSMegakernelGenerator(model=dsd, max_seq_len=256)
+    pf = DecoderOracle(tw.bb_layers, tw.bb_norm, 256, "backbone", "hf_bf16")
+    g = torch.Generator().manual_seed(31)
+    x = torch.randn(S + 3, 1024, generator=g).to(torch.bfloat16)
+    print("prefill + decode handoff: launching", flush=True)
+    bb.prefill(x[:S].cuda())
+    for i in range(S):
+        pf.step(x[i], pos=i)
+    dec = DecoderOracle(tw.bb_layers, tw.bb_norm, 256, "backbone", "kernel")
+    dec.set_kv(pf.k[:, :, :S], pf.v[:, :, :S])
+    worst = 0.0
+    for j in range(3):
+        h = bb.decode_step_with_embedding(x[S + j].cuda())
+        hr, _ = dec.step(x[S + j], pos=S + j)
+        worst = max(worst, rel_l2(h.cpu(), hr))
+    bb.check_error()
+    print(f"prefill + decode handoff: worst decode hidden rel_l2 {worst:.2e}", flush=True)
+    assert worst < TOL
+    assert bb.position == S + 3
