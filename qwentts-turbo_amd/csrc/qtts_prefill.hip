@@ -55,6 +55,7 @@ constexpr int GT = 256;                      // GEMM threads (4 waves)
 // K loops then take half the load round trips; 64 for the 128-column tiles
 template <int TN> constexpr int bk_of() { return TN == 64 ? 128 : 64; }
 constexpr int QKVW = 4096;                   // q | k | v row of one token
+constexpr int QROW = 136;                    // LDS row of the query block: 128 dims + 16-byte pad
 constexpr int VTROW = 36;                    // LDS row of V^T: 32 keys + pad; 72 B keeps the 8-byte
                                              // reads aligned and puts rows 8 apart 16 banks apart
 constexpr int MAX_SPLIT = 16;
@@ -494,7 +495,8 @@ __global__ void __launch_bounds__(256) reduce_resid_norm_kernel(const GemmArgs g
 
 // Causal GQA attention of S queries (positions p0 .. p0 + S - 1) over cache positions
 // 0 .. p0 + S - 1, one workgroup of AW waves per (32-query block, query head); wave w takes the
-// 32-key blocks kb = w, w + AW, ... MFMA 32x32x16 with A = K rows and B = Q^T gives S^T: lane
+// 32-key blocks kb = w, w + AW, ... The block's queries sit in LDS; each wave stages its K
+// block in its own LDS rows from coalesced loads. MFMA 32x32x16 with A = K rows and B = Q^T gives S^T: lane
 // (half hf, column c) holds query 32 qb + c's scores for keys 8 (r >> 2) + 4 hf + (r & 3), r < 16,
 // of each block, so a query's row max and sum stay in the lane and its partner half-wave. The
 // waves' (max, sum) pairs merge through LDS in wave order; pass 2 forms p = bf16(e * (1 / l)) and
@@ -505,12 +507,14 @@ __global__ void __launch_bounds__(256) reduce_resid_norm_kernel(const GemmArgs g
 // longest query blocks first.
 constexpr int AW = 4;
 constexpr int ATT_SMEM = std::max(AW * HDIM * VTROW * 2, (AW - 1) * HDIM * 32 * 4);
+static_assert(32 * QROW <= HDIM * VTROW, "a wave's LDS region holds its staged K block");
 
 __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, const bf16_t* kc, const bf16_t* vc,
                                                        int layer, int max_seq, int p0, int S, bf16_t* att,
                                                        float scale) {
   __shared__ __attribute__((aligned(16))) char smem[ATT_SMEM];
   __shared__ float sml[AW][2][32];
+  __shared__ __attribute__((aligned(16))) bf16_t sq[32 * QROW];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hf = lane >> 5, c = lane & 31;
   // XCD-aware order: workgroups go to the XCDs round-robin by linear id, so id & 7 picks the KV
   // head and each XCD's L2 holds one head's K and V; within it, the longest query blocks first
@@ -524,41 +528,62 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
   const int nkb = last / 32 + 1;
   bf16_t* vt = reinterpret_cast<bf16_t*>(smem) + w * HDIM * VTROW;
 
-  u32x4 qr[8];
-  {
-    const bf16_t* qp = qkv + (size_t)(qok ? i : 0) * QKVW + hq * HDIM + 8 * hf;
+  // the block's 32 query rows go to LDS once (two 16-byte chunks per thread); every wave reads
+  // its B operands from there, which keeps 32 VGPRs free for the V prefetch
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      const u32x4 v = ldw(qp + 16 * kk);   // unconditional (clamped row): see loadk
-      qr[kk] = qok ? v : u32x4{0u, 0u, 0u, 0u};
-    }
+  for (int j = 0; j < 2; ++j) {
+    const int ch = threadIdx.x + 64 * AW * j, qrow = ch >> 4, qcol = 8 * (ch & 15);
+    const int qi = 32 * qb + qrow;
+    const u32x4 v = ldw(qkv + (size_t)(qi < S ? qi : 0) * QKVW + hq * HDIM + qcol);   // clamped row
+    *reinterpret_cast<u32x4*>(&sq[qrow * QROW + qcol]) = qi < S ? v : u32x4{0u, 0u, 0u, 0u};
   }
+  __syncthreads();
   const size_t hbase = ((size_t)layer * NKVH + kvh) * max_seq * HDIM;
   const bf16_t* kb_ = kc + hbase;
   const bf16_t* vb_ = vc + hbase;
 
-  // K rows of block kb for this lane (key 32 kb + c, dims 16 kk + 8 hf ..), issued a block ahead.
-  // Loads are unconditional from a clamped row and zeroed afterwards: a load under a branch
-  // would make the compiler wait for every outstanding load, the prefetch included.
+  // K block kb (32 keys x 128 dims) in 8 coalesced 1 KB rounds, issued a block ahead: round i,
+  // lane j loads key 32 kb + 4 i + (j >> 4), dims 8 (j & 15) .. + 7 (four whole rows per
+  // instruction; a row-per-lane load touches 32 cache lines per instruction and kept the address
+  // unit busy). Loads are unconditional from a clamped row and zeroed when staged: a load under a
+  // branch would make the compiler wait for every outstanding load, the prefetch included.
+  bf16_t* kt = vt;   // the wave's LDS region holds the K block, then (pass 2) the V^T block
   auto loadk = [&](int kb, u32x4 (&kr)[8]) {
-    const int key = 32 * kb + c;
-    const bool kok = kb < nkb && key <= last;
-    const bf16_t* kp = kb_ + (size_t)(kok ? key : 0) * HDIM + 8 * hf;
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      const u32x4 v = ldw(kp + 16 * kk);
-      kr[kk] = kok ? v : u32x4{0u, 0u, 0u, 0u};
+    for (int r = 0; r < 8; ++r) {
+      const int key = 32 * kb + 4 * r + (lane >> 4);
+      kr[r] = ldw(kb_ + (size_t)(key <= last ? key : 0) * HDIM + 8 * (lane & 15));
     }
   };
-  auto scores = [&](int kb, const u32x4 (&kr)[8], float (&sc)[16]) {
+  auto stagek = [&](int kb, const u32x4 (&kr)[8]) {
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int row = 4 * r + (lane >> 4);
+      *reinterpret_cast<u32x4*>(&kt[row * QROW + 8 * (lane & 15)]) =
+          32 * kb + row <= last ? kr[r] : u32x4{0u, 0u, 0u, 0u};
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  };
+  auto scores = [&](int kb, float (&sc)[16]) {
     // two independent 4-step MFMA chains (even and odd 16-dim steps), added at the end
     f32x16 acc, acc2;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = acc2[r] = 0.0f;
+    // Q^T operand (query c, dims 16 kk + 8 hf ..) from LDS; the offset is made opaque so the
+    // reads stay in the loop instead of being hoisted into 32 live registers
+    // and the K operand (key c, the same dims) from the staged block; both row pitches are QROW
+    int qo = c * QROW + 8 * hf;
+    asm volatile("" : "+v"(qo));
+    const bf16_t* qp = &sq[qo];
+    const bf16_t* kp = &kt[qo];
 #pragma unroll
     for (int kk = 0; kk < 8; kk += 2) {
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(kr[kk]), as_bf8(qr[kk]), acc, 0, 0, 0);
-      acc2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(kr[kk + 1]), as_bf8(qr[kk + 1]), acc2, 0, 0, 0);
+      const u32x4 q0 = *reinterpret_cast<const u32x4*>(qp + 16 * kk);
+      const u32x4 q1 = *reinterpret_cast<const u32x4*>(qp + 16 * kk + 16);
+      const u32x4 k0 = *reinterpret_cast<const u32x4*>(kp + 16 * kk);
+      const u32x4 k1 = *reinterpret_cast<const u32x4*>(kp + 16 * kk + 16);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(k0), as_bf8(q0), acc, 0, 0, 0);
+      acc2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(k1), as_bf8(q1), acc2, 0, 0, 0);
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] += acc2[r];
@@ -581,12 +606,14 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
 
   // pass 1: this wave's row maximum and softmax denominator
   float m = -INFINITY, l = 0.0f;
-  u32x4 kq[2][8];
-  loadk(w, kq[0]);
-  auto pass1 = [&](int kb, const u32x4 (&kr)[8], u32x4 (&kn)[8]) {
-    loadk(kb + AW, kn);
+  u32x4 kq[8];
+  loadk(w, kq);
+  auto pass1 = [&](int kb) {
+    stagek(kb, kq);
+    loadk(kb + AW, kq);
     float sc[16];
-    scores(kb, kr, sc);
+    scores(kb, sc);
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");   // K reads before the next staging
     float bm = sc[0];
 #pragma unroll
     for (int r = 1; r < 16; ++r) bm = fmaxf(bm, sc[r]);
@@ -601,10 +628,7 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
     l = m == -INFINITY ? add : l * __expf(m - mn) + add;
     m = mn;
   };
-  for (int kb = w; kb < nkb; kb += 2 * AW) {
-    pass1(kb, kq[0], kq[1]);
-    if (kb + AW < nkb) pass1(kb + AW, kq[1], kq[0]);
-  }
+  for (int kb = w; kb < nkb; kb += AW) pass1(kb);
   l += __shfl_xor(l, 32, 64);
   if (hf == 0) {
     sml[w][0][c] = m;
@@ -636,27 +660,35 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
   // staging: lane (group dgr = lane >> 4, pair kp2 = lane & 15) moves keys 2 kp2, 2 kp2 + 1 of dims
   // 32 dd + 8 dgr + 0..7: the four groups write rows 8 apart, i.e. different banks
   const int kp2 = lane & 15, dgr = lane >> 4;
-  loadk(w, kq[0]);
-  auto pass2 = [&](int kb, const u32x4 (&kr)[8], u32x4 (&kn)[8]) {
-    loadk(kb + AW, kn);
+  // V rows 2 kp2, 2 kp2 + 1 of block kb, dims 32 dd + 8 dgr .. + 7, issued a block ahead into vr
+  // (unconditional loads from clamped rows, zeroed when staged: see loadk)
+  u32x4 vr[8];
+  auto loadv = [&](int kb) {
+    const int k0 = 32 * kb + 2 * kp2;
+    const bf16_t* v0 = vb_ + (size_t)(k0 <= last ? k0 : 0) * HDIM + 8 * dgr;
+    const bf16_t* v1 = vb_ + (size_t)(k0 + 1 <= last ? k0 + 1 : 0) * HDIM + 8 * dgr;
+#pragma unroll
+    for (int dd = 0; dd < 4; ++dd) {
+      vr[dd] = ldw(v0 + 32 * dd);
+      vr[4 + dd] = ldw(v1 + 32 * dd);
+    }
+  };
+  loadk(w, kq);
+  loadv(w);
+  auto pass2 = [&](int kb) {
+    stagek(kb, kq);
+    loadk(kb + AW, kq);
     float sc[16];
-    scores(kb, kr, sc);
-    // stage V rows 2 kp2, 2 kp2 + 1 of the block, dims dg .. dg + 31, transposed into vt[d][key]
+    scores(kb, sc);
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");   // K reads before the V^T staging
+    // stage the prefetched V rows of this block transposed into vt[d][key], then issue the next
     {
       const int k0 = 32 * kb + 2 * kp2;
       const bool ok0 = k0 <= last, ok1 = k0 + 1 <= last;
-      const bf16_t* v0 = vb_ + (size_t)(ok0 ? k0 : 0) * HDIM + 8 * dgr;
-      const bf16_t* v1 = vb_ + (size_t)(ok1 ? k0 + 1 : 0) * HDIM + 8 * dgr;
-      u32x4 va[4], vb[4];
 #pragma unroll
       for (int dd = 0; dd < 4; ++dd) {
-        va[dd] = ldw(v0 + 32 * dd);   // unconditional (clamped rows): see loadk
-        vb[dd] = ldw(v1 + 32 * dd);
-      }
-#pragma unroll
-      for (int dd = 0; dd < 4; ++dd) {
-        const u32x4 a = ok0 ? va[dd] : u32x4{0u, 0u, 0u, 0u};
-        const u32x4 b = ok1 ? vb[dd] : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 a = ok0 ? vr[dd] : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 b = ok1 ? vr[4 + dd] : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int d = 32 * dd + 8 * dgr + 2 * e;
@@ -665,6 +697,7 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
         }
       }
     }
+    loadv(kb + AW);
     // the rows are this wave's own: order the writes before the reads within the wave
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
 #pragma unroll
@@ -684,10 +717,7 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
     }
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   };
-  for (int kb = w; kb < nkb; kb += 2 * AW) {
-    pass2(kb, kq[0], kq[1]);
-    if (kb + AW < nkb) pass2(kb + AW, kq[1], kq[0]);
-  }
+  for (int kb = w; kb < nkb; kb += AW) pass2(kb);
   // partial O^T of waves 1.. to LDS (the V^T rows are dead), added in wave order by wave 0
   __syncthreads();
   float* ob = reinterpret_cast<float*>(smem);
