@@ -556,11 +556,17 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
     }
   };
   auto stagek = [&](int kb, const u32x4 (&kr)[8]) {
+    if (32 * kb + 31 <= last) {   // wave-uniform: a whole block needs no zeroing
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      const int row = 4 * r + (lane >> 4);
-      *reinterpret_cast<u32x4*>(&kt[row * QROW + 8 * (lane & 15)]) =
-          32 * kb + row <= last ? kr[r] : u32x4{0u, 0u, 0u, 0u};
+      for (int r = 0; r < 8; ++r)
+        *reinterpret_cast<u32x4*>(&kt[(4 * r + (lane >> 4)) * QROW + 8 * (lane & 15)]) = kr[r];
+    } else {
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const int row = 4 * r + (lane >> 4);
+        *reinterpret_cast<u32x4*>(&kt[row * QROW + 8 * (lane & 15)]) =
+            32 * kb + row <= last ? kr[r] : u32x4{0u, 0u, 0u, 0u};
+      }
     }
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   };
@@ -684,7 +690,8 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
     // stage the prefetched V rows of this block transposed into vt[d][key], then issue the next
     {
       const int k0 = 32 * kb + 2 * kp2;
-      const bool ok0 = k0 <= last, ok1 = k0 + 1 <= last;
+      const bool whole = 32 * kb + 31 <= last;   // wave-uniform: a whole block needs no zeroing
+      const bool ok0 = whole || k0 <= last, ok1 = whole || k0 + 1 <= last;
 #pragma unroll
       for (int dd = 0; dd < 4; ++dd) {
         const u32x4 a = ok0 ? vr[dd] : u32x4{0u, 0u, 0u, 0u};

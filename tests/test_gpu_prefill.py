@@ -43,13 +43,15 @@ def _compare(bb, orc, p0, S, hidden, hidden_ref, label, bars=(TOL, TOL, TOL)):
     return eh
 
 
-@pytest.mark.parametrize("S", [1, 7, 64, 130, 333])
+@pytest.mark.parametrize("S", [1, 7, 64, 130, 333, 1100])
 def test_prefill_two_layers(pkg, small, S):
     """Prompt lengths across the tile edges: one token, a partial 32-query block, exactly two
-    blocks, a partial 128-row GEMM tile, several tiles with a ragged last one."""
+    blocks, a partial 128-row GEMM tile, several tiles with a ragged last one, and a long prompt
+    (the widest split-K target, 35 query blocks, a ragged last block)."""
     dsd, tw = small
-    bb = pkg.TTSMegakernelGenerator(model=dsd, max_seq_len=512)
-    orc = DecoderOracle(tw.bb_layers, tw.bb_norm, 512, "backbone", "hf_bf16")
+    ms = 512 if S <= 512 else 2048
+    bb = pkg.TTSMegakernelGenerator(model=dsd, max_seq_len=ms)
+    orc = DecoderOracle(tw.bb_layers, tw.bb_norm, ms, "backbone", "hf_bf16")
     x = torch.randn(S, 1024, generator=torch.Generator().manual_seed(100 + S)).to(torch.bfloat16)
     _print(f"prefill 2 layers S={S}: launching")
     h = bb.prefill(x.cuda())
