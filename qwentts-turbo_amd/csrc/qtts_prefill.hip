@@ -21,7 +21,8 @@
 //   rmsnorm_kernel   one wave per token
 //   gemm_kernel      C = A W^T, tile 128 x 64 (4 waves, each 32 rows x 2 MFMA 32x32x16 blocks)
 //                    or, from 256 rows on, 128 x 128 (2 x 2 waves of 64 x 64), K steps of 64,
-//                    LDS double buffer + register stages, split-K over grid.z when the tile grid alone
+//                    LDS double buffer + 2 (3 for 128 x 128) register stages of branch-free
+//                    loads, split-K over grid.z when the tile grid alone
 //                    would leave CUs idle (partials in f32, summed in a fixed order by
 //                    reduce_kernel); epilogues: store, residual add, SwiGLU (gate and up rows
 //                    interleaved by 32 in one tile)
@@ -182,11 +183,12 @@ __global__ void __launch_bounds__(GT, TN == 128 ? 2 : 1) gemm_kernel(const GemmA
     arow[i] = g.A + (size_t)(aok[i] ? m : 0) * g.lda + kbeg + lc;
   }
 
-  // register stages two tiles ahead of the MFMAs (tile kt + 2 loads while tile kt computes and
-  // tile kt + 1 moves to LDS): twice the weight bytes in flight of a plain double buffer. Every
-  // load is issued unconditionally (rows past M read row 0 and are zeroed afterwards): a load
-  // under a branch makes the compiler wait for all outstanding loads instead of just the old ones.
-  u32x4 ra[2][NAR], rb[2][NBR];
+  // NST register stages ahead of the MFMAs (tile kt + NST loads while tile kt computes and tile
+  // kt + 1 moves to LDS). Every load is issued unconditionally (rows past M read row 0 and are
+  // zeroed afterwards; K steps past the end reload the last one): a load under a branch makes the
+  // compiler wait for all outstanding loads instead of just the old ones.
+  constexpr int NST = TN == 128 ? 3 : 2;
+  u32x4 ra[NST][NAR], rb[NST][NBR];
   auto gload = [&](int k0, u32x4 (&a)[NAR], u32x4 (&b)[NBR]) {
 #pragma unroll
     for (int i = 0; i < NAR; ++i) {
@@ -230,21 +232,25 @@ __global__ void __launch_bounds__(GT, TN == 128 ? 2 : 1) gemm_kernel(const GemmA
           acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[mb], bv[nb], acc[mb][nb], 0, 0, 0);
     }
   };
-  // one step: tile kt in LDS buffer kt & 1, tile kt + 1 in register stage S1, stage S0 free
+  // one step: tile kt in LDS buffer kt & 1, tile kt + 1 in register stage (kt + 1) % NST, stage
+  // kt % NST free (its tile went to LDS in the previous step)
   auto step = [&](int kt, u32x4 (&a0)[NAR], u32x4 (&b0)[NBR], const u32x4 (&a1)[NAR], const u32x4 (&b1)[NBR]) {
-    if (kt + 2 < nk) gload((kt + 2) * BK, a0, b0);
+    gload(min(kt + NST, nk - 1) * BK, a0, b0);
     compute(kt & 1);
     if (kt + 1 < nk) sstore((kt + 1) & 1, a1, b1);
     __syncthreads();
   };
 
-  gload(0, ra[0], rb[0]);
-  if (nk > 1) gload(BK, ra[1], rb[1]);
+#pragma unroll
+  for (int st = 0; st < NST; ++st) gload(min(st, nk - 1) * BK, ra[st], rb[st]);
   sstore(0, ra[0], rb[0]);
   __syncthreads();
-  for (int kt = 0; kt < nk; kt += 2) {
+  for (int kt = 0; kt < nk; kt += NST) {
     step(kt, ra[0], rb[0], ra[1], rb[1]);
-    if (kt + 1 < nk) step(kt + 1, ra[1], rb[1], ra[0], rb[0]);
+    if (kt + 1 < nk) step(kt + 1, ra[1], rb[1], ra[2 % NST], rb[2 % NST]);
+    if constexpr (NST == 3) {
+      if (kt + 2 < nk) step(kt + 2, ra[2], rb[2], ra[0], rb[0]);
+    }
   }
 
   // D layout of a 32x32 block: lane column lane & 31; register r holds row
@@ -787,13 +793,15 @@ constexpr Shape kQKV{4096, HID}, kO{HID, NQH * HDIM}, kGU{2 * INTER, HID}, kDown
 int tile_n(int M) { return M >= 256 ? 128 : 64; }
 
 // split-K factor: double while the tile grid is below its target and the K range still splits
-// into whole 64-wide steps. Targets: 128 workgroups below 256 rows (every split writes a full
-// f32 partial tile, which at 128 rows outweighs the weights it streams), one per CU from 256
-// rows, two per CU from 512 rows (where each split still runs a long K loop)
-int splits_for(int M, int N, int K) {
+// into whole K steps. Targets: 128 workgroups below 256 rows (every split writes a full f32
+// partial tile, which at 128 rows outweighs the weights it streams), one per CU from 256 rows.
+// The SwiGLU GEMM is never split: its fused epilogue beats the unfused reduction at every M
+// (measured at 128, 512 and 2048 rows), and its tile grid is the widest of the layer.
+int splits_for(int M, int N, int K, bool swiglu = false) {
+  if (swiglu) return 1;
   const int tn = tile_n(M), bk = tn == 64 ? bk_of<64>() : bk_of<128>();
   const int tiles = ((M + BM - 1) / BM) * (N / tn);
-  const int target = M >= 512 ? 512 : (M >= 256 ? 256 : 128);
+  const int target = M >= 256 ? 256 : 128;
   int ks = 1;
   while (tiles * ks < target && ks < MAX_SPLIT && (K / bk) % (2 * ks) == 0) ks *= 2;
   return ks;
@@ -817,7 +825,7 @@ Layout layout(int S, int vocab) {
   L.hb = take(HID * 2);
   L.logits = take((size_t)(vocab > 0 ? vocab : MAXV) * 2);
   size_t pb = 0;
-  for (Shape sh : {kQKV, kO, kGU, kDown}) {
+  for (Shape sh : {kQKV, kO, kDown}) {
     const int ks = splits_for(S, sh.N, sh.K);
     if (ks > 1) pb = std::max(pb, (size_t)ks * S * sh.N * 4);
   }
@@ -842,7 +850,7 @@ void gemm_launch(const GemmArgs& g, int ks, bool reduce, hipStream_t st) {
 // `reduce` is false, else reduced here. Returns the split count (0 on a launch error).
 template <int WM, int EPI>
 int gemm(GemmArgs& g, hipStream_t st, bool reduce = true) {
-  const int ks = splits_for(g.M, g.N, g.K);
+  const int ks = splits_for(g.M, g.N, g.K, EPI == E_SWIGLU);
   g.kchunk = g.K / ks;
   if (tile_n(g.M) == 128) gemm_launch<WM, EPI, 128>(g, ks, reduce, st);
   else gemm_launch<WM, EPI, 64>(g, ks, reduce, st);
