@@ -239,3 +239,7 @@ def test_qtts_backbone_prefill(lib, model):
               S, None, _ptr(xd), _ptr(hid), None, 0, None, None, 0, -1, 0, None, 0, _stream()) != 0
     assert fn(_ptr(ws), wsb, _ptr(table), 2, _ptr(norm), _ptr(cos), _ptr(sin), _ptr(kc), _ptr(vc), max_seq, 50, S,
               None, _ptr(xd), _ptr(hid), None, 0, None, None, 0, -1, 0, None, 0, _stream()) != 0
+    # an empty prompt is rejected too (and has no workspace size)
+    assert fn(_ptr(ws), wsb, _ptr(table), 2, _ptr(norm), _ptr(cos), _ptr(sin), _ptr(kc), _ptr(vc), max_seq, 0, 0,
+              None, _ptr(xd), _ptr(hid), None, 0, None, None, 0, -1, 0, None, 0, _stream()) != 0
+    assert lib.qtts_prefill_workspace_bytes(0, 0) == 0

@@ -134,11 +134,13 @@ def test_prefill_full_model_and_first_token(pkg):
 
 
 def test_prefill_rejects_bad_arguments(pkg, small):
-    """Host-side validation before any launch: a prompt past max_seq_len, a wrong embedding
-    width, a pos3 of the wrong shape; the decoder's position is left unchanged."""
+    """Host-side validation before any launch: an empty prompt, a prompt past max_seq_len, a
+    wrong embedding width, a pos3 of the wrong shape; the decoder's position is left unchanged."""
     dsd, _ = small
     bb = pkg.TTSMegakernelGenerator(model=dsd, max_seq_len=64)
     bb.set_position(60)
+    with pytest.raises(RuntimeError, match=r"embeds must be \[S, 1024\], got \[0, 1024\]"):
+        bb.prefill(torch.zeros(0, 1024, dtype=torch.bfloat16, device="cuda"))
     with pytest.raises(RuntimeError, match="max_seq_len"):
         bb.prefill(torch.zeros(5, 1024, dtype=torch.bfloat16, device="cuda"))
     with pytest.raises(RuntimeError, match="embeds"):
