@@ -178,3 +178,30 @@ def test_prefill_then_decode_handoff(pkg, small):
     print(f"prefill + decode handoff: worst decode hidden rel_l2 {worst:.2e}", flush=True)
     assert worst < TOL
     assert bb.position == S + 3
+
+
+def test_prefill_fills_the_cache_in_one_or_two_calls(pkg, small):
+    """Maximum size: a 4096-token prompt fills the whole cache (max_seq_len 4096) in one call,
+    and again as two 2048-token calls, the second continuing from the first one's cache. Causal
+    attention makes the two equivalent; they differ only in summation order (the GEMMs split K
+    differently at 4096 and 2048 rows), so K, V and the last hidden agree within TOL. (The
+    oracle is too slow at this size; the 2-layer cases above pin the arithmetic.)"""
+    dsd, _ = small
+    S = 4096
+    x = torch.randn(S, 1024, generator=torch.Generator().manual_seed(4096)).to(torch.bfloat16).cuda()
+    one = pkg.TTSMegakernelGenerator(model=dsd, max_seq_len=S)
+    _print("prefill 2 layers S=4096 in one call: launching")
+    h1 = one.prefill(x)
+    two = pkg.TTSMegakernelGenerator(model=dsd, max_seq_len=S)
+    _print("prefill 2 layers S=4096 as 2 x 2048: launching")
+    two.prefill(x[:2048])
+    h2 = two.prefill(x[2048:])
+    torch.cuda.synchronize()
+    one.check_error()
+    two.check_error()
+    ek = rel_l2(one.get_k_cache().float().cpu(), two.get_k_cache().float().cpu())
+    ev = rel_l2(one.get_v_cache().float().cpu(), two.get_v_cache().float().cpu())
+    eh = rel_l2(h1.cpu(), h2.cpu())
+    _print(f"S=4096 one call vs two: K rel_l2 {ek:.2e}, V {ev:.2e}, hidden {eh:.2e}")
+    assert ek < TOL and ev < TOL and eh < TOL
+    assert one.position == S and two.position == S
