@@ -42,6 +42,23 @@ def test_workspace_bytes_is_callable_without_a_gpu():
     assert 0 < n < 8 << 20 and n % 256 == 0
 
 
+def test_prefill_workspace_bytes_without_a_gpu():
+    """qtts_prefill_workspace_bytes is a host-only size query: 0 for an empty prompt or an
+    out-of-range vocabulary; otherwise at least the bf16 activations of every prompt row
+    (hidden, normed, q|k|v, attention, SwiGLU: 1024 + 1024 + 4096 + 2048 + 3072 per row) plus the
+    head logits. Not monotone in the prompt length (the split-K factor, and so the partials
+    buffer, changes with the row count)."""
+    lib = ctypes.CDLL(str(LIB))
+    f = lib.qtts_prefill_workspace_bytes
+    f.restype = ctypes.c_size_t
+    f.argtypes = [ctypes.c_int, ctypes.c_int]
+    assert f(0, 0) == 0 and f(-1, 0) == 0 and f(128, -1) == 0 and f(128, 3073) == 0
+    for n in (1, 7, 40, 127, 128, 129, 255, 256, 333, 511, 512, 1100, 2048, 4096):
+        lower = n * (1024 + 1024 + 4096 + 2048 + 3072) * 2 + 3072 * 2
+        assert f(n, 0) >= lower, n
+        assert f(n, 3072) >= f(n, 0), n
+
+
 def test_torch_extension_exposes_reference_classes(pkg):
     ext = pkg._ext.load()
     for cls, methods in {
