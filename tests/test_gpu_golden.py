@@ -144,3 +144,23 @@ def test_c2_generate_with_mfma_prefill(c2_gen):
     bb.prefill(prefill[0].cuda(), tok, cases.EOS_ID, True)
     _print(f"mfma prefill generate: first frame {frames[0][:4]}..., prefill token {int(tok.item())}")
     assert frames[0][0] == int(tok.item())
+
+
+@pytest.mark.parametrize("k", [2, 13])
+def test_c2_greedy_stops_at_eos(pkg, k):
+    """The frame loop's EOS stop (generator.py:122-127: a group-0 EOS ends generation before
+    its frame is kept; EOS suppressed while fewer than min_new_tokens frames exist, :108-109,
+    :170). With the EOS id set to the group-0 token that the fixture's greedy run first chooses
+    at frame k (never chosen before), suppressing it in earlier frames changes none of their
+    argmaxes, so generate() returns exactly the fixture's first k frames. k = 13 is not a
+    multiple of sync_every (8): frames queued after the EOS frame must leave no records."""
+    fx = cases.load("c2_frames")
+    g0 = fx["greedy"][:, 0]
+    assert g0[k] not in g0[:k]
+    eos = int(g0[k])
+    gen = pkg.NativeTTSGenerator(model=_weights(pkg, "c2", "c2"), eos_token_id=eos, max_seq_len=1024)
+    prefill, trailing, pad = cases.c2_inputs()
+    frames = gen.generate(prefill, None, trailing, pad, max_tokens=len(g0), min_new_tokens=2, prefill="steps")
+    got = np.array(frames, dtype=np.int32).reshape(-1, 16)
+    _print(f"c2 greedy with EOS = {eos} (frame {k}): {len(frames)} frames")
+    assert got.shape == (k, 16) and np.array_equal(got, fx["greedy"][:k])
