@@ -77,13 +77,17 @@ class BatchedTTSDecoder:
     def cp_frames(self, hidden: torch.Tensor, g0: torch.Tensor, text_rows: Optional[torch.Tensor],
                   tokens_out: torch.Tensor, combined_out: torch.Tensor, eos_id: int = -1,
                   do_sample: bool = False, temperature: float = 0.9, top_k: int = 50, seed: int = 0,
-                  frame_step: int = 0) -> None:
+                  frame_step: int = 0, done: Optional[torch.Tensor] = None) -> None:
         """A code-predictor frame per stream: ``tokens_out[s]`` (int32 [16]) gets g0 and the 15
         group ids, ``combined_out[s]`` (bf16 [1024]) the embedding sum plus ``text_rows[s]``.
-        Up to 8 streams share one launch, stream s on XCD s (``frames_streams``); stream s draws
-        with key ``seed + s``."""
+        A stream whose g0 is ``eos_id`` writes nothing and sets ``done[s]`` (device int32 [n],
+        kept by the caller across frames; a fresh one when None). Up to 8 streams share one
+        launch, stream s on XCD s (``frames_streams``); stream s draws with key ``seed + s``."""
         n = self.n_streams
-        done = torch.zeros(n, dtype=torch.int32, device=self.device)
+        if done is None:
+            done = torch.zeros(n, dtype=torch.int32, device=self.device)
+        elif done.dtype != torch.int32 or done.numel() != n or not done.is_contiguous():
+            raise ValueError("done must be a contiguous device int32 tensor with one entry per stream")
         hid = hidden.to(self.device, torch.float32).contiguous()
         g = g0.to(self.device, torch.int32).contiguous()
         tr = text_rows.to(self.device, torch.bfloat16).contiguous() if text_rows is not None else None
@@ -92,6 +96,83 @@ class BatchedTTSDecoder:
             self.cp.decoder.frames_streams(hid[b:e], g[b:e], tr[b:e] if tr is not None else None, tokens_out[b:e],
                                            combined_out[b:e], int(eos_id), done[b:e], bool(do_sample),
                                            float(temperature), int(top_k), 1.0, int(seed) + b, int(frame_step))
+
+    def generate(self, talker_input_embeds: Sequence[torch.Tensor], trailing_text_hidden: Sequence[torch.Tensor],
+                 tts_pad_embed: torch.Tensor, eos_token_id: int, max_tokens: int = 500, do_sample: bool = False,
+                 temperature: float = 0.9, top_k: int = 50, top_p: float = 1.0, cp_do_sample: bool = False,
+                 cp_temperature: float = 0.9, cp_top_k: int = 50, min_new_tokens: int = 2,
+                 repetition_penalty: float = 1.0, *, seed: int = 0, sync_every: int = 8,
+                 prefill: str = "mfma") -> List[List[List[int]]]:
+        """``NativeTTSGenerator.generate`` (generator.py:77-176) for ``n_streams`` utterances at
+        once: one prompt ``[1, seq_s, 1024]`` and one trailing text ``[1, T_s, 1024]`` per stream
+        (ragged lengths), a shared pad row. Each stream is prefilled on its own, then every frame
+        is one code-predictor launch and one backbone launch for all streams, queued with no host
+        sync; the host checks the EOS flags every ``sync_every`` frames and stops when every
+        stream has ended. Stream s samples with key ``seed + s`` and returns exactly what a
+        single-stream ``generate(..., seed=seed + s)`` returns for its inputs."""
+        n = self.n_streams
+        if len(talker_input_embeds) != n or len(trailing_text_hidden) != n:
+            raise ValueError(f"one prompt and one trailing text per stream ({n}) expected")
+        if prefill not in ("mfma", "steps"):
+            raise ValueError(f"prefill={prefill!r}: 'mfma' or 'steps'")
+        dev = self.device
+        max_tokens = int(max_tokens)
+        groups = self.cp.n_groups
+        i32 = dict(dtype=torch.int32, device=dev)
+        g0 = torch.zeros(n, **i32)
+        done = torch.zeros(n, **i32)
+        hist = torch.zeros(n, max(max_tokens, 1), **i32)
+        records = torch.full((max(max_tokens, 1), n, groups + 1), -1, **i32)
+        combined = torch.empty(n, 1024, dtype=torch.bfloat16, device=dev)
+        pad = tts_pad_embed.reshape(-1).to(dev, torch.bfloat16)
+        # per-stream text rows for every frame (the trailing text, then the pad row)
+        rows = pad.expand(n, max(max_tokens, 1), 1024).clone()
+        hidden = torch.empty(n, 1024, dtype=torch.float32, device=dev)
+        for s in range(n):
+            emb = talker_input_embeds[s]
+            if emb.dim() != 3 or emb.shape[0] != 1 or emb.shape[2] != 1024:
+                raise ValueError(f"prompt {s} must be [1, seq, 1024], got {tuple(emb.shape)}")
+            seq = emb.shape[1]
+            dec = self.streams[s]
+            if seq < 1 or seq + max_tokens > dec.max_seq_len:
+                raise ValueError(f"stream {s}: prefill {seq} + max_tokens {max_tokens} exceeds max_seq_len "
+                                 f"{dec.max_seq_len}")
+            text = trailing_text_hidden[s][0].to(dev, torch.bfloat16)
+            t = min(int(text.shape[0]), max_tokens)
+            rows[s, :t] = text[:t]
+            e = emb[0].to(dev, torch.bfloat16).contiguous()
+            bb = dec.decoder
+            bb.reset()
+            if prefill == "mfma":
+                bb.prefill(e, g0[s:s + 1], int(eos_token_id), min_new_tokens > 0, bool(do_sample),
+                           float(temperature), int(top_k), float(top_p), int(seed) + s)
+            else:
+                for i in range(seq - 1):
+                    bb.decode_step_with_embedding(e[i])
+                bb.decode_step_select(e[seq - 1], g0[s:s + 1], hist[s], 0, float(repetition_penalty),
+                                      int(eos_token_id), min_new_tokens > 0, bool(do_sample), float(temperature),
+                                      int(top_k), float(top_p), int(seed) + s, 0)
+            hidden[s] = bb.hidden_state_buffer()
+        for step in range(max_tokens):
+            self.cp_frames(hidden, g0, rows[:, step].contiguous(), records[step], combined, int(eos_token_id),
+                           bool(cp_do_sample), float(cp_temperature), int(cp_top_k), int(seed), step, done)
+            hist[:, step] = g0          # this frame's group 0 joins the penalty history
+            hidden = self.step_select(combined, g0, int(eos_token_id), hist, [step + 1] * n,
+                                      float(repetition_penalty), step + 1 < min_new_tokens, bool(do_sample),
+                                      float(temperature), int(top_k), float(top_p), int(seed), step + 1)
+            if (step + 1) % sync_every == 0 and bool(done.all()):
+                break
+        rec = records.cpu()
+        self.check_error()
+        out = []
+        for s in range(n):
+            frames = []
+            for r in rec[:, s].tolist():
+                if r[0] < 0:
+                    break
+                frames.append(r)
+            out.append(frames)
+        return out
 
     def check_error(self):
         for dec in self.streams:

@@ -166,3 +166,39 @@ def test_cp_frames_streams_match_batch1(pkg, n, sample):
         assert torch.equal(comb[s], c1), f"stream {s}: combined input differs"
     dec.check_error()
     print(f"cp frames {n} streams: first stream groups {toks[0, 1:6].tolist()}...", flush=True)
+
+
+@pytest.mark.parametrize("sample", [False, True], ids=["greedy", "sampled"])
+def test_batched_generate_matches_single_stream(pkg, sample):
+    """BatchedTTSDecoder.generate() -- per-stream prefill, then one code-predictor launch and one
+    backbone launch per frame for all streams -- against NativeTTSGenerator.generate() of each
+    stream with key seed + s, frame for frame and id for id: 3 streams with ragged prompts (40,
+    97, 160 tokens) and trailing texts (5, 1, 30 rows). The EOS id is a group-0 token that
+    stream 0 first chooses at a frame k >= 5 (not a multiple of sync_every) in a run with EOS
+    suppressed, so stream 0 ends there while the others may run on; suppressing that id earlier
+    changes no earlier choice, since it was never chosen before."""
+    cfg = pkg.SyntheticConfig(n_bb_layers=4, n_cp_layers=2, n_groups=15)
+    dsd = {k: v.cuda() for k, v in pkg.synthetic_state_dict(seed=77, cfg=cfg).items()}
+    g = torch.Generator().manual_seed(78)
+    prompts = [torch.randn(1, S, 1024, generator=g).to(torch.bfloat16) for S in (40, 97, 160)]
+    texts = [torch.randn(1, T, 1024, generator=g).to(torch.bfloat16) for T in (5, 1, 30)]
+    pad = torch.randn(1, 1, 1024, generator=g).to(torch.bfloat16)
+    n, frames_max = 3, 24
+    kw = dict(do_sample=sample, temperature=0.9, top_k=40, top_p=0.9, cp_do_sample=sample, cp_temperature=0.8,
+              cp_top_k=30, repetition_penalty=1.1, seed=5)
+    dec = pkg.BatchedTTSDecoder(dsd, n, max_seq_len=256)
+    print(f"batched generate sample={sample}: EOS suppressed run", flush=True)
+    free = dec.generate(prompts, texts, pad, 3000, max_tokens=frames_max, min_new_tokens=frames_max, **kw)
+    assert [len(f) for f in free] == [frames_max] * n
+    g0 = [f[0] for f in free[0]]
+    k = next(i for i in range(5, frames_max - 2) if g0[i] not in g0[:i] and i % 8 != 0)
+    eos = g0[k]
+    print(f"batched generate sample={sample}: EOS = {eos} (stream 0, frame {k})", flush=True)
+    out = dec.generate(prompts, texts, pad, eos, max_tokens=frames_max, min_new_tokens=2, **kw)
+    assert len(out[0]) == k and out[0] == free[0][:k]
+    gen = pkg.NativeTTSGenerator(model=dsd, eos_token_id=eos, max_seq_len=256)
+    for s in range(n):
+        kws = dict(kw, seed=kw["seed"] + s)
+        ref = gen.generate(prompts[s], None, texts[s], pad, max_tokens=frames_max, min_new_tokens=2, **kws)
+        print(f"stream {s}: batched {len(out[s])} frames, single-stream {len(ref)}", flush=True)
+        assert out[s] == ref, f"stream {s} differs"
