@@ -128,15 +128,21 @@ class BatchedTTSDecoder:
         # per-stream text rows for every frame (the trailing text, then the pad row)
         rows = pad.expand(n, max(max_tokens, 1), 1024).clone()
         hidden = torch.empty(n, 1024, dtype=torch.float32, device=dev)
+        # every stream's arguments are checked before any stream is touched
         for s in range(n):
-            emb = talker_input_embeds[s]
+            emb, txt = talker_input_embeds[s], trailing_text_hidden[s]
             if emb.dim() != 3 or emb.shape[0] != 1 or emb.shape[2] != 1024:
                 raise ValueError(f"prompt {s} must be [1, seq, 1024], got {tuple(emb.shape)}")
+            if txt.dim() != 3 or txt.shape[0] != 1 or txt.shape[2] != 1024:
+                raise ValueError(f"trailing text {s} must be [1, T, 1024], got {tuple(txt.shape)}")
+            seq = emb.shape[1]
+            if seq < 1 or seq + max_tokens > self.streams[s].max_seq_len:
+                raise ValueError(f"stream {s}: prefill {seq} + max_tokens {max_tokens} exceeds max_seq_len "
+                                 f"{self.streams[s].max_seq_len}")
+        for s in range(n):
+            emb = talker_input_embeds[s]
             seq = emb.shape[1]
             dec = self.streams[s]
-            if seq < 1 or seq + max_tokens > dec.max_seq_len:
-                raise ValueError(f"stream {s}: prefill {seq} + max_tokens {max_tokens} exceeds max_seq_len "
-                                 f"{dec.max_seq_len}")
             text = trailing_text_hidden[s][0].to(dev, torch.bfloat16)
             t = min(int(text.shape[0]), max_tokens)
             rows[s, :t] = text[:t]

@@ -202,3 +202,27 @@ def test_batched_generate_matches_single_stream(pkg, sample):
         ref = gen.generate(prompts[s], None, texts[s], pad, max_tokens=frames_max, min_new_tokens=2, **kws)
         print(f"stream {s}: batched {len(out[s])} frames, single-stream {len(ref)}", flush=True)
         assert out[s] == ref, f"stream {s} differs"
+
+
+def test_batched_generate_rejects_bad_arguments(pkg):
+    """Argument checks of BatchedTTSDecoder.generate run for every stream before any stream is
+    prefilled: a wrong prompt shape, a wrong trailing-text shape, a prompt too long for
+    max_seq_len, or a prompt count different from n_streams raise ValueError and leave every
+    stream's position untouched."""
+    cfg = pkg.SyntheticConfig(n_bb_layers=1, n_cp_layers=1, n_groups=15)
+    dsd = {k: v.cuda() for k, v in pkg.synthetic_state_dict(seed=5, cfg=cfg).items()}
+    dec = pkg.BatchedTTSDecoder(dsd, 2, max_seq_len=64)
+    for s in range(2):
+        dec.streams[s].set_position(7)
+    ok = torch.zeros(1, 10, 1024, dtype=torch.bfloat16)
+    txt = torch.zeros(1, 3, 1024, dtype=torch.bfloat16)
+    pad = torch.zeros(1, 1, 1024, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="prompt 1"):
+        dec.generate([ok, torch.zeros(10, 1024)], [txt, txt], pad, 2150, max_tokens=4)
+    with pytest.raises(ValueError, match="trailing text 1"):
+        dec.generate([ok, ok], [txt, torch.zeros(3, 1024)], pad, 2150, max_tokens=4)
+    with pytest.raises(ValueError, match="stream 1"):
+        dec.generate([ok, torch.zeros(1, 60, 1024, dtype=torch.bfloat16)], [txt, txt], pad, 2150, max_tokens=8)
+    with pytest.raises(ValueError, match="one prompt"):
+        dec.generate([ok], [txt], pad, 2150, max_tokens=4)
+    assert dec.positions() == [7, 7]
