@@ -115,11 +115,30 @@ def cpu_baseline(sample_seconds: float = 15.0) -> dict:
         if time.perf_counter() - tp0 >= 3.0:
             break
     pf_rate = npf / (time.perf_counter() - tp0)
-    return {"value": n / el, "unit": "frames/s", "cores": threads, "kind": "port",
+    return {"value": n / el, "unit": "frames/s", "cores": threads, "kind": "port", "cpu_model": _cpu_model(),
             "backbone_steps_per_s": round(n / t_parts[1], 2), "cp_steps_per_s": round(15 * n / t_parts[0], 2),
             "prefill_tokens_per_s": round(pf_rate, 2),
             "sample": f"{n} frames (1 backbone step at 512 context + 16 code-predictor steps, HF-bf16 eager "
                       f"PyTorch oracle) in {el:.1f} s"}
+
+
+def _cpu_model() -> str:
+    """The host CPU's model name (lscpu "Model name", else /proc/cpuinfo "model name")."""
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.strip().startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def prefill_flops(S: int) -> int:
@@ -325,6 +344,12 @@ def main():
         out["prefill"] = prefill_figures(bbg)
     if not args.no_batched:
         out["batched_c4"] = batched_c4(pkg, sd)
+    # the decoders and their device memory are released before the CPU leg and before exit,
+    # with the device idle, so nothing device-side is left to the interpreter's teardown
+    del bb, cp, bbg, cpg, hidden
+    torch.cuda.synchronize()
+    pkg._ext.load().shutdown()
+    torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)

@@ -1,8 +1,8 @@
 /*
  * qwentts_amd.h -- C ABI of the MI355X (gfx950) decode kernels for Qwen3-TTS.
  *
- * Two persistent HIP kernels each run a full per-token transformer pass in one cooperative
- * launch:
+ * Two persistent HIP kernels each run a full per-token transformer pass in one launch of
+ * 256 co-resident workgroups (one per CU):
  *   - backbone ("talker") kernel: N layers of RMSNorm -> QKV -> interleaved 3D mRoPE -> GQA
  *     attention over a bf16 KV cache -> SwiGLU MLP, final RMSNorm, optional codec-head logits
  *     and on-device token selection;
@@ -57,9 +57,10 @@ typedef TTSLayerWeights CPLayerWeights;
  * meaning at the boundary: on return hidden_buffer holds the last layer's residual stream
  * (bf16 [1024] for the backbone, f32 [1024] for the code predictor) and g_normalized the
  * final-RMSNorm hidden (f32 [1024]). The inter-workgroup exchange buffers these kernels need
- * live in a library-owned workspace per device (allocated on first use with hipMalloc);
- * calls that overlap in time on one device share it and therefore race, exactly as the
- * reference's per-object scratch does.
+ * live in a library-owned workspace per (device, stream), allocated with hipMalloc on the
+ * first call on that stream and freed by qtts_shutdown(): calls on one stream are ordered, and
+ * calls on different streams use different workspaces, so concurrent callers on separate
+ * streams (e.g. a backbone and a code-predictor decoder) do not share exchange slots.
  *
  * k_cache / v_cache: [num_layers, 8, max_seq_len, 128], bf16 (backbone) or f32 (CP).
  * cache_len must equal position + 1 (the reference passes it that way) and position must be
@@ -100,13 +101,28 @@ hipError_t launch_cp_decode_with_embedding(
 
 typedef struct QttsWorkspace QttsWorkspace; /* opaque, device-resident */
 
-/* Bytes of device memory a workspace needs; the memory must be zero-filled before first use. */
+/* Bytes of device memory a workspace needs. */
 size_t qtts_workspace_bytes(void);
 
-/* Validates the device (gfx950, 256 CUs in 8 XCDs, cooperative launch) once per device and
- * binds a caller-allocated, zero-filled workspace of qtts_workspace_bytes() bytes.
+/* Validates the device (gfx950, 256 CUs in 8 XCDs, one workgroup of each kernel per CU) once
+ * per device and binds a caller-allocated workspace of qtts_workspace_bytes() bytes (256-byte
+ * aligned): the first launch that uses it zero-fills it on the launch stream.
  * Returns hipErrorInvalidDevice when the device cannot run these kernels. */
 hipError_t qtts_workspace_init(void* workspace, int device);
+
+/* Forgets the launch sequence of `count` consecutive workspaces at `workspace`; call before
+ * their memory is freed or reused (the next launch on that memory zero-fills it first). */
+hipError_t qtts_workspace_release(void* workspace, int count);
+
+/* Frees the library-owned workspaces of the reference-compatible launchers (after
+ * synchronising their devices) and forgets every workspace's launch sequence. Call when no
+ * launch is in flight, e.g. at process teardown while the HIP runtime is still up; the
+ * library stays usable afterwards (workspaces are re-created on demand). */
+hipError_t qtts_shutdown(void);
+
+/* Test hook: sets the launch sequence of one workspace (1 .. 2^20 - 1) so that a test can
+ * cross the point where the sequence space is used up and the workspace is zero-filled. */
+hipError_t qtts_debug_set_sequence(void* workspace, unsigned int sequence);
 
 /* Reads and clears the device-side error word of a workspace (synchronises the stream).
  * *error_code = 0 when every wait completed; bit 0 = a wait timed out. */
@@ -196,6 +212,8 @@ typedef struct QttsBackboneStream {
     const int* history;           /* int32 [n_history] previously generated group-0 tokens */
     int n_history;
     unsigned long long seed;      /* sampler key */
+    const int* skip_if;           /* device int or NULL: nonzero = this stream computes nothing
+                                     (its XCD idles; used for streams that reached EOS) */
 } QttsBackboneStream;
 
 /* Backbone steps (codec head + selection as in qtts_backbone_step) of n_streams (1..8) independent

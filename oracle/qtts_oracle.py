@@ -26,8 +26,8 @@ Precision policies (``policy=``):
     in a fixed order in f64) and as bf16 where the reference stores bf16: the backbone residual
     between layers (fused_decode_tts.cu:541) and backbone KV (fused_decode_tts.cu:270-271).
     The code predictor keeps f32 residuals and KV (fused_decode_code_predictor.cu:288-289,
-    :553). cos/sin come from the bf16 tables. Logits are ``W_bf16 . bf16(h)`` in f64, kept
-    as f32. With f64 accumulation on both sides every f32/bf16 rounding agrees except with
+    :553). cos/sin come from the bf16 tables. Logits are ``W_bf16 . bf16(h)`` in f64, rounded
+    to bf16 as the reference's bf16 ``torch.mv`` returns them. With f64 accumulation on both sides every f32/bf16 rounding agrees except with
     ~1e-8 probability per value, so greedy tokens are reproducible.
   * ``"exact"``   -- the same formulas in f64 with no storage rounding and f32 cos/sin (the
     values transformers' rotary embedding produces); used to pin the math against
@@ -443,11 +443,13 @@ class DecoderOracle:
 # ------------------------------------------------------------------------------------------
 
 def head_logits(w: torch.Tensor, hidden: torch.Tensor) -> torch.Tensor:
-    """W_bf16 . bf16(hidden) accumulated in f64, returned as f32 logits (generator.py:158, :351;
-    the reference rounds the logits to bf16, these stay f32 so greedy ties are rare)."""
+    """W_bf16 . bf16(hidden) accumulated in f64, rounded to f32 and then to bf16, returned as
+    f32 tensor of bf16 values: the reference's ``torch.mv`` over bf16 operands returns bf16
+    logits (generator.py:158, :351), so greedy ties (lowest id wins, as torch.argmax) are
+    those of the reference."""
     wd = w.detach().to("cpu", torch.float64)
     h = hidden.detach().to("cpu", torch.float32).reshape(-1).to(torch.bfloat16).to(torch.float64)
-    return (wd @ h).to(torch.float32)
+    return rb((wd @ h).to(torch.float32))
 
 
 def suppress_mask(vocab: int, eos_id: int) -> torch.Tensor:
@@ -466,14 +468,16 @@ def apply_repetition_penalty(logits: torch.Tensor, history: Sequence[int], penal
     out = logits.clone()
     prev = torch.tensor(sorted(set(int(h) for h in history)), dtype=torch.long)
     s = logits[prev]
-    out[prev] = torch.where(s > 0, s / penalty, s * penalty)
+    # the reference computes on bf16 logits, so each penalised value is rounded to bf16
+    out[prev] = rb(torch.where(s > 0, s / penalty, s * penalty))
     return out
 
 
 def filter_logits(logits: torch.Tensor, temperature: float, top_k: int, top_p: float) -> torch.Tensor:
     """Temperature, top-k and top-p filtering (generator.py:189-204); dropped ids become -inf.
 
-    * temperature: f32 division, as ``logits / temperature`` on f32 logits.
+    * temperature: f32 division rounded to bf16, as ``logits / temperature`` on the
+      reference's bf16 logits (generator.py:189).
     * top-k keeps every value >= the k-th largest, ties included (generator.py:192-194).
     * top-p keeps x when the softmax mass of the strictly larger kept values is <= top_p,
       with probabilities exp(s - max) summed in f64. On distinct values this is the
@@ -481,7 +485,7 @@ def filter_logits(logits: torch.Tensor, temperature: float, top_k: int, top_p: f
       descending order survives iff cumprobs[i-1] <= top_p); on exact ties it keeps every
       tied value, which makes the kept set independent of sort order.
     """
-    scaled = logits.to(torch.float32) / temperature
+    scaled = rb(logits.to(torch.float32) / temperature)
     if top_k > 0 and top_k < scaled.numel():
         kth = torch.topk(scaled, top_k)[0][-1]
         scaled = torch.where(scaled < kth, torch.full_like(scaled, float("-inf")), scaled)
@@ -618,6 +622,19 @@ class TalkerOracle:
         lg[mask] = float("-inf")
         g0 = sample_token(lg, do_sample, temperature, top_k, top_p,
                           eos_id if min_new_tokens > 0 else None, seed=seed, frame_step=0, group=0)
+        return self.decode_frames(hidden, g0, trailing_text_hidden, tts_pad_embed, eos_id, max_tokens, do_sample,
+                                  temperature, top_k, top_p, cp_do_sample, cp_temperature, cp_top_k, min_new_tokens,
+                                  repetition_penalty, seed, trace)
+
+    def decode_frames(self, hidden, g0: int, trailing_text_hidden, tts_pad_embed, eos_id: int, max_tokens=500,
+                      do_sample=False, temperature=0.9, top_k=50, top_p=1.0, cp_do_sample=False, cp_temperature=0.9,
+                      cp_top_k=50, min_new_tokens=2, repetition_penalty=1.0, seed: int = 0,
+                      trace: Optional[dict] = None, on_frame=None) -> List[List[int]]:
+        """The frame loop of generator.py:122-174 after the prefill: ``hidden`` is the backbone's
+        final-norm hidden of the last prompt token, ``g0`` the group-0 id selected from it, and the
+        backbone cache (``self.bb``) holds the prompt at positions 0 .. position - 1."""
+        vocab = self.w.codec_head.shape[0]
+        mask = suppress_mask(vocab, eos_id)
         frames, hist = [], []
         n_text = trailing_text_hidden.shape[1]
         for step in range(max_tokens):
@@ -639,6 +656,8 @@ class TalkerOracle:
             g0 = sample_token(lg, do_sample, temperature, top_k, top_p,
                               eos_id if step + 1 < min_new_tokens else None,
                               seed=seed, frame_step=step + 1, group=0)
+            if on_frame is not None:
+                on_frame(step, frames)
         return frames
 
 

@@ -6,6 +6,7 @@ other device raises from ``qtts_workspace_init``.
 """
 from __future__ import annotations
 
+import atexit
 import importlib.util
 import sys
 from pathlib import Path
@@ -39,4 +40,15 @@ def load():
     spec.loader.exec_module(mod)
     sys.modules["_qwentts_amd_C"] = mod
     _MOD = mod
+    # library-owned device memory is freed while the HIP runtime is still up (Python's atexit
+    # handlers run before the C runtime's exit handlers tear the runtime down)
+    atexit.register(_shutdown)
     return mod
+
+
+def _shutdown():
+    if _MOD is not None:
+        try:
+            _MOD.shutdown()
+        except RuntimeError:
+            pass

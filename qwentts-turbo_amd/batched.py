@@ -51,12 +51,16 @@ class BatchedTTSDecoder:
                     history: Optional[torch.Tensor] = None, n_history: Sequence[int] = (),
                     repetition_penalty: float = 1.0, suppress_eos: bool = False, do_sample: bool = False,
                     temperature: float = 0.9, top_k: int = 50, top_p: float = 1.0, seed: int = 0,
-                    frame_step: int = 0) -> torch.Tensor:
+                    frame_step: int = 0, skip: Optional[torch.Tensor] = None) -> torch.Tensor:
         """One backbone step per stream at its own position, codec head, suppress mask (ids
         [V-1024, V) except EOS), optional repetition penalty over ``history[s][:n_history[s]]``
         and selection of each stream's group-0 token into ``tokens_out[s]`` (device int32), with
         sampling key ``seed + s``. Up to 8 streams share one launch, stream s on XCD s
-        (``decode_steps_streams``). Returns the final-norm hiddens (f32 [n_streams, 1024], device)."""
+        (``decode_steps_streams``). A stream whose ``skip[s]`` (device int32 [n]) is nonzero computes
+        nothing and leaves its outputs as they were. Returns the final-norm hiddens (f32
+        [n_streams, 1024], device)."""
+        if skip is not None and (skip.dtype != torch.int32 or skip.numel() != self.n_streams or not skip.is_contiguous()):
+            raise ValueError("skip must be a contiguous device int32 tensor with one entry per stream")
         if embeds.shape != (self.n_streams, 1024):
             raise ValueError(f"embeds must be [{self.n_streams}, 1024], got {tuple(embeds.shape)}")
         if tokens_out.dtype != torch.int32 or tokens_out.numel() < self.n_streams:
@@ -71,7 +75,8 @@ class BatchedTTSDecoder:
             lead.decode_steps_streams([d.decoder for d in self.streams[b:e]], emb[b:e], tokens_out[b:e],
                                       hidden[b:e], hist[b:e] if hist is not None else None, nh[b:e],
                                       float(repetition_penalty), int(eos_id), bool(suppress_eos), bool(do_sample),
-                                      float(temperature), int(top_k), float(top_p), int(seed) + b, int(frame_step))
+                                      float(temperature), int(top_k), float(top_p), int(seed) + b, int(frame_step),
+                                      skip[b:e] if skip is not None else None)
         return hidden
 
     def cp_frames(self, hidden: torch.Tensor, g0: torch.Tensor, text_rows: Optional[torch.Tensor],
@@ -165,7 +170,8 @@ class BatchedTTSDecoder:
             hist[:, step] = g0          # this frame's group 0 joins the penalty history
             hidden = self.step_select(combined, g0, int(eos_token_id), hist, [step + 1] * n,
                                       float(repetition_penalty), step + 1 < min_new_tokens, bool(do_sample),
-                                      float(temperature), int(top_k), float(top_p), int(seed), step + 1)
+                                      float(temperature), int(top_k), float(top_p), int(seed), step + 1,
+                                      skip=done)   # streams that reached EOS leave their XCD idle
             if (step + 1) % sync_every == 0 and bool(done.all()):
                 break
         rec = records.cpu()

@@ -124,6 +124,12 @@ class MegakernelTTSDecoder {
     ws_ = make_workspace(dev_);
     position_ = 0;
   }
+  ~MegakernelTTSDecoder() {
+    qtts_workspace_release(ws_.data_ptr(), 1);
+    if (ws_streams_.defined()) qtts_workspace_release(ws_streams_.data_ptr(), kMaxStreams);
+  }
+  MegakernelTTSDecoder(const MegakernelTTSDecoder&) = delete;
+  MegakernelTTSDecoder& operator=(const MegakernelTTSDecoder&) = delete;
 
   torch::Tensor decode_step(int64_t input_token_id) {
     TORCH_CHECK(input_token_id >= 0 && input_token_id < embed_weight_.size(0), "token id out of range");
@@ -238,7 +244,8 @@ class MegakernelTTSDecoder {
   void decode_steps_streams(std::vector<MegakernelTTSDecoder*> decs, torch::Tensor embeds, torch::Tensor out_tokens,
                             torch::Tensor hidden_out, c10::optional<torch::Tensor> history, std::vector<int64_t> n_history,
                             double repetition_penalty, int64_t eos_id, bool suppress_eos, bool do_sample,
-                            double temperature, int64_t top_k, double top_p, int64_t seed, int64_t frame_step) {
+                            double temperature, int64_t top_k, double top_p, int64_t seed, int64_t frame_step,
+                            c10::optional<torch::Tensor> skip) {
     const int64_t n = (int64_t)decs.size();
     TORCH_CHECK(n >= 1 && n <= kMaxStreams, "decode_steps_streams takes 1..", kMaxStreams, " decoders, got ", n);
     c10::hip::HIPGuardMasqueradingAsCUDA guard(dev_);
@@ -255,6 +262,9 @@ class MegakernelTTSDecoder {
                       history->dim() == 2 && history->size(0) >= n, "history must be a contiguous int32 [n, H] GPU tensor");
       hist_stride = history->size(1);
     }
+    if (skip.has_value())
+      TORCH_CHECK(skip->is_cuda() && skip->scalar_type() == torch::kInt32 && skip->is_contiguous() && skip->numel() >= n,
+                  "skip must be a contiguous int32 GPU tensor with >= ", n, " entries");
     std::vector<QttsBackboneStream> io(n);
     for (int64_t st = 0; st < n; ++st) {
       MegakernelTTSDecoder* d = decs[st];
@@ -286,6 +296,7 @@ class MegakernelTTSDecoder {
       q.history = nh > 0 ? history->data_ptr<int>() + st * hist_stride : nullptr;
       q.n_history = nh;
       q.seed = (unsigned long long)(seed + st);
+      q.skip_if = skip.has_value() ? skip->data_ptr<int>() + st : nullptr;
     }
     if (!ws_streams_.defined()) {
       ws_streams_ = torch::zeros({(int64_t)(kMaxStreams * qtts_workspace_bytes())}, torch::dtype(torch::kUInt8).device(dev_));
@@ -395,6 +406,12 @@ class MegakernelCodePredictorDecoder {
     ws_ = make_workspace(dev_);
     position_ = 0;
   }
+  ~MegakernelCodePredictorDecoder() {
+    qtts_workspace_release(ws_.data_ptr(), 1);
+    if (ws_streams_.defined()) qtts_workspace_release(ws_streams_.data_ptr(), kMaxStreams);
+  }
+  MegakernelCodePredictorDecoder(const MegakernelCodePredictorDecoder&) = delete;
+  MegakernelCodePredictorDecoder& operator=(const MegakernelCodePredictorDecoder&) = delete;
 
   torch::Tensor decode_step_with_embedding(torch::Tensor input_embedding) {
     TORCH_CHECK(position_ < max_seq_len_, "position ", position_, " >= max_seq_len ", max_seq_len_, " (KV cache full)");
@@ -567,6 +584,8 @@ class MegakernelCodePredictorDecoder {
 PYBIND11_MODULE(_qwentts_amd_C, m) {
   m.doc() = "MI355X decode kernels for Qwen3-TTS (backbone + code predictor)";
   m.def("workspace_bytes", []() { return (int64_t)qtts_workspace_bytes(); });
+  m.def("shutdown", []() { hip_check(qtts_shutdown(), "qtts_shutdown"); },
+        "Free the library-owned workspaces (synchronises their devices); registered with atexit by the loader.");
   m.def("set_trace", [](c10::optional<torch::Tensor> buf) {
     if (!buf.has_value()) { hip_check(qtts_debug_trace(nullptr, 0), "qtts_debug_trace"); return; }
     TORCH_CHECK(buf->is_cuda() && buf->is_contiguous(), "trace buffer must be a contiguous GPU tensor");
@@ -601,7 +620,8 @@ PYBIND11_MODULE(_qwentts_amd_C, m) {
       .def("decode_steps_streams", &MegakernelTTSDecoder::decode_steps_streams, py::arg("decoders"), py::arg("embeds"),
            py::arg("out_tokens"), py::arg("hidden_out"), py::arg("history"), py::arg("n_history"),
            py::arg("repetition_penalty"), py::arg("eos_id"), py::arg("suppress_eos"), py::arg("do_sample"),
-           py::arg("temperature"), py::arg("top_k"), py::arg("top_p"), py::arg("seed"), py::arg("frame_step"))
+           py::arg("temperature"), py::arg("top_k"), py::arg("top_p"), py::arg("seed"), py::arg("frame_step"),
+           py::arg("skip") = py::none())
       .def("check_error_streams", &MegakernelTTSDecoder::check_error_streams)
       .def("check_error", &MegakernelTTSDecoder::check_error);
   py::class_<MegakernelCodePredictorDecoder>(m, "MegakernelCodePredictorDecoder")

@@ -6,7 +6,7 @@
 // with the interleaved 3D mRoPE of rope_multimodal.cuh:9-54 (t, h, w may differ) and the
 // frame glue of generator.py:116-174, 178-207, 309-362 moved on-device.
 //
-// Work decomposition (one cooperative launch of 256 workgroups, one per CU):
+// Work decomposition (one launch of 256 workgroups, one per CU, all co-resident):
 //   * Tensor-parallel over the 8 XCDs. XCD x owns KV head x with query heads 2x, 2x+1
 //     (512 rows of Wq|Wk|Wv), intermediate rows [384x, 384x+384) of Wgate/Wup, and the
 //     matching column slices of Wo ([:, 256x:256x+256]) and Wdown ([:, 384x:384x+384]).
@@ -25,8 +25,10 @@
 //     the polls on their own wave keeps them out of the math waves' in-order load queue.
 #include <hip/hip_runtime.h>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <unordered_map>
+#include <utility>
 #include "qtts_common.h"
 #include "qtts_select.h"
 #include "qwentts_amd.h"
@@ -1138,15 +1140,18 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       v[r] = r < 3 && r < nrows ? dot8d(tq.p[2 * r + 1], xv + 8, dot8d(tq.p[2 * r], xv, 0.0)) : 0.0;
     const double t = rs_sum<5, 4>(v, lane);   // row lane >> 4 in lanes 0, 16, 32, 48
     const int r = lane >> 4;
+    // logits are bf16 values, as the reference's torch.mv over bf16 operands returns them
+    // (generator.py:158, :351); ties then go to the lowest id, as torch.argmax
     if (cp_greedy) {
-      float cv = ((lane & 15) == 0 && r < nrows) ? (float)t : -INFINITY;
+      float cv = ((lane & 15) == 0 && r < nrows) ? rbf((float)t) : -INFINITY;
       int ci = row0 + r;
       best_merge(cv, ci, xlane_f<4>(cv), (int)xlane<4>((uint32_t)ci));
       best_merge(cv, ci, xlane_f<5>(cv), (int)xlane<5>((uint32_t)ci));
       best_merge(bv, bi, cv, ci);
     } else if ((lane & 15) == 0 && r < nrows) {
-      pub_cross(&ws->logits[pi & 1][row0 + r], (float)t, tg);
-      if (!a.cp_frame && SIO(out_logits)) SIO(out_logits[row0 + r]) = (float)t;
+      const float lv = rbf((float)t);
+      pub_cross(&ws->logits[pi & 1][row0 + r], lv, tg);
+      if (!a.cp_frame && SIO(out_logits)) SIO(out_logits[row0 + r]) = lv;
     }
   };
   // greedy code-predictor head: only the workgroup's best (value, lowest id on ties) is published;
@@ -1249,8 +1254,8 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         for (int i = lane; i < n; i += 64) {
           if (s.pen_bits[i >> 5] & (1u << (i & 31))) {
-            const float v = s.stage[i];
-            s.stage[i] = v > 0.f ? v / a.rep_penalty : v * a.rep_penalty;
+            const float v = s.stage[i];   // bf16 arithmetic of the reference: the result is rounded to bf16
+            s.stage[i] = rbf(v > 0.f ? v / a.rep_penalty : v * a.rep_penalty);
           }
         }
       }
@@ -1610,32 +1615,44 @@ namespace {
 using qtts::KArgs;
 using qtts::Workspace;
 
-constexpr uint32_t kSpinCap = 1u << 22;   // ~4 s of polling before a wait is declared failed
+constexpr uint32_t kSpinCap = 1u << 22;          // ~4 s of polling before a wait is declared failed
+constexpr uint32_t kSeqLimit = (1u << 20) - 1u;  // tag = (sequence << 12) | (layer pass * 8 + slot)
 
 struct DeviceCheck {
   bool done = false;
   hipError_t status = hipSuccess;
+  // Ordering of this library's launches on the device: a launch on another stream than the
+  // previous one first waits for it. Two persistent launches that overlapped could each hold
+  // part of the CUs while waiting for workgroups of their own that cannot be placed.
+  hipEvent_t last = nullptr;
+  hipStream_t last_stream = nullptr;
+  bool has_last = false;
 };
 std::mutex g_mu;
 std::unordered_map<int, DeviceCheck> g_dev;
-struct TagSeq {
-  uint32_t seq = 0;    // launch sequence number
-  size_t bytes = 0;    // widest block cleared on a wrap
-};
-std::unordered_map<const void*, TagSeq> g_seq;   // launch sequence per workspace (block)
-std::unordered_map<int, void*> g_lib_ws;           // library-owned workspace per device
-uint64_t* g_trace = nullptr;                       // optional step timeline buffer
+// Launch sequence of every workspace, keyed by its device address: the tag base of the next
+// launch that uses it. Absent = never used (or released): its first launch zero-fills it.
+std::unordered_map<const void*, uint32_t> g_seq;
+// Library-owned workspaces of the reference-compatible launchers, one per (device, stream):
+// launches on one stream are ordered, so they never overlap on a workspace.
+std::map<std::pair<int, hipStream_t>, void*> g_lib_ws;
+uint64_t* g_trace = nullptr;   // optional step timeline buffer
 
-__global__ void xcc_probe_kernel(int* out) {
-  if (threadIdx.x == 0) out[blockIdx.x] = (int)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15u);
+// XCC id of every workgroup of the probe launch (a static device array: the set-up allocates nothing)
+__device__ int g_xcc_probe[qtts::NWG];
+
+__global__ void xcc_probe_kernel() {
+  if (threadIdx.x == 0) g_xcc_probe[blockIdx.x] = (int)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15u);
 }
 __global__ void zero_kernel(uint4* p, size_t n16) {
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x)
     p[i] = make_uint4(0, 0, 0, 0);
 }
 
-// gfx950 with 256 CUs, cooperative launch, and a cooperative grid of 256 workgroups whose
-// XCC ids are a rotation of blockIdx % 8 with 32 workgroups per XCD.
+// gfx950 with 256 CUs, room for one workgroup of every instantiation on each CU (so a launch of
+// 256 workgroups is co-resident when the device is not shared with other kernels), and workgroup
+// b placed on XCC (b + r) % 8 for a fixed rotation r, 32 workgroups per XCD. Every in-kernel wait
+// is bounded, so a launch that is not co-resident ends with the error word set instead of hanging.
 hipError_t check_device(int device) {
   std::lock_guard<std::mutex> lk(g_mu);
   DeviceCheck& dc = g_dev[device];
@@ -1644,25 +1661,19 @@ hipError_t check_device(int device) {
   hipDeviceProp_t prop;
   hipError_t e = hipGetDeviceProperties(&prop, device);
   if (e != hipSuccess) return dc.status = e;
-  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0 || prop.multiProcessorCount != qtts::NWG || !prop.cooperativeLaunch)
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0 || prop.multiProcessorCount != qtts::NWG)
     return dc.status = hipErrorInvalidDevice;
-  int occ = 0;
-  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)qtts::qtts_decode_kernel<true, false>, qtts::NTHR, 0);
-  if (e != hipSuccess || occ < 1) return dc.status = (e != hipSuccess ? e : hipErrorInvalidDevice);
-  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)qtts::qtts_decode_kernel<false, false>, qtts::NTHR, 0);
-  if (e != hipSuccess || occ < 1) return dc.status = (e != hipSuccess ? e : hipErrorInvalidDevice);
-  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)qtts::qtts_decode_kernel<false, true>, qtts::NTHR, 0);
-  if (e != hipSuccess || occ < 1) return dc.status = (e != hipSuccess ? e : hipErrorInvalidDevice);
-  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)qtts::qtts_decode_kernel<true, true>, qtts::NTHR, 0);
-  if (e != hipSuccess || occ < 1) return dc.status = (e != hipSuccess ? e : hipErrorInvalidDevice);
-  int* d = nullptr;
-  if ((e = hipMalloc(&d, qtts::NWG * sizeof(int))) != hipSuccess) return dc.status = e;
-  void* args[] = {&d};
-  e = hipLaunchCooperativeKernel((const void*)xcc_probe_kernel, dim3(qtts::NWG), dim3(64), args, 0, 0);
+  const void* fns[] = {(const void*)qtts::qtts_decode_kernel<true, false>, (const void*)qtts::qtts_decode_kernel<false, false>,
+                       (const void*)qtts::qtts_decode_kernel<false, true>, (const void*)qtts::qtts_decode_kernel<true, true>};
+  for (const void* fn : fns) {
+    int occ = 0;
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, qtts::NTHR, 0);
+    if (e != hipSuccess || occ < 1) return dc.status = (e != hipSuccess ? e : hipErrorInvalidDevice);
+  }
+  hipLaunchKernelGGL(xcc_probe_kernel, dim3(qtts::NWG), dim3(64), 0, 0);
+  e = hipGetLastError();
   int h[qtts::NWG];
-  if (e == hipSuccess) e = hipMemcpy(h, d, sizeof(h), hipMemcpyDeviceToHost);
-  const hipError_t fe = hipFree(d);
-  if (e == hipSuccess) e = fe;
+  if (e == hipSuccess) e = hipMemcpyFromSymbol(h, HIP_SYMBOL(g_xcc_probe), sizeof(h), 0, hipMemcpyDeviceToHost);
   if (e != hipSuccess) return dc.status = e;
   int count[16] = {0};
   for (int b = 0; b < qtts::NWG; ++b) {
@@ -1671,24 +1682,32 @@ hipError_t check_device(int device) {
   }
   for (int x = 0; x < qtts::NXCD; ++x)
     if (count[x] != qtts::WPX) return dc.status = hipErrorInvalidDevice;
+  if ((e = hipEventCreateWithFlags(&dc.last, hipEventDisableTiming)) != hipSuccess) return dc.status = e;
   return dc.status = hipSuccess;
 }
 
-uint32_t next_tag_base(void* ws, size_t bytes, hipStream_t stream, hipError_t* err) {
-  std::lock_guard<std::mutex> lk(g_mu);
-  TagSeq& ts = g_seq[ws];
-  uint32_t& seq = ts.seq;
-  // the widest block any launch has used from this address: a wrap clears all of it, so no
-  // workspace of a multi-stream block keeps a tag of the previous cycle
-  ts.bytes = bytes > ts.bytes ? bytes : ts.bytes;
-  if (seq == 0 || seq >= (1u << 20) - 1u) {
-    // first use (or tag wrap): clear every exchange slot with a fill kernel
-    const size_t n16 = ts.bytes / 16;
-    hipLaunchKernelGGL(zero_kernel, dim3(256), dim3(256), 0, stream, reinterpret_cast<uint4*>(ws), n16);
+// Tag base of a launch over the n consecutive workspaces at ws. The launch takes the largest
+// sequence of its workspaces and moves all n past it, so its tags differ from every tag they
+// hold. When one of them is new, or the sequence space is used up, exactly these n workspaces
+// are zero-filled (a fill kernel on the launch stream) and the sequence restarts at 1.
+// Called with g_mu held.
+uint32_t next_tag_base(void* ws, int n, hipStream_t stream, hipError_t* err) {
+  uint32_t seq = 0;
+  bool fresh = false;
+  for (int i = 0; i < n; ++i) {
+    const auto it = g_seq.find(reinterpret_cast<Workspace*>(ws) + i);
+    if (it == g_seq.end()) fresh = true;
+    else seq = it->second > seq ? it->second : seq;
+  }
+  *err = hipSuccess;
+  if (fresh || seq == 0 || seq >= kSeqLimit) {
+    hipLaunchKernelGGL(zero_kernel, dim3(256), dim3(256), 0, stream, reinterpret_cast<uint4*>(ws),
+                       (size_t)n * sizeof(Workspace) / 16);
     *err = hipGetLastError();
     seq = 1;
   }
-  return (seq++) << 12;
+  for (int i = 0; i < n; ++i) g_seq[reinterpret_cast<Workspace*>(ws) + i] = seq + 1;
+  return seq << 12;
 }
 
 // xl: one stream per XCD, n_streams workspaces of one block starting at a.io[0].ws
@@ -1699,27 +1718,34 @@ hipError_t launch(bool bb, KArgs& a, hipStream_t stream, bool xl = false, int n_
   if ((e = check_device(dev)) != hipSuccess) return e;
   if (a.num_layers < 1 || a.n_pos < 1 || a.num_layers * a.n_pos > qtts::MAX_LAYER_PASSES) return hipErrorInvalidValue;
   if (a.io[0].pos0 < 0 || a.io[0].pos0 + a.n_pos > a.max_seq) return hipErrorInvalidValue;
+  std::lock_guard<std::mutex> lk(g_mu);
+  DeviceCheck& dc = g_dev[dev];
+  if (dc.has_last && dc.last_stream != stream && (e = hipStreamWaitEvent(stream, dc.last, 0)) != hipSuccess) return e;
   hipError_t ze = hipSuccess;
-  a.tag_base = next_tag_base(a.io[0].ws, (size_t)n_streams * sizeof(Workspace), stream, &ze);
+  a.tag_base = next_tag_base(a.io[0].ws, n_streams, stream, &ze);
   if (ze != hipSuccess) return ze;
   a.spin_cap = kSpinCap;
   a.trace = g_trace;
   void* args[] = {&a};
   const void* fn = bb ? (xl ? (const void*)qtts::qtts_decode_kernel<true, true> : (const void*)qtts::qtts_decode_kernel<true, false>)
                       : (xl ? (const void*)qtts::qtts_decode_kernel<false, true> : (const void*)qtts::qtts_decode_kernel<false, false>);
-  return hipLaunchCooperativeKernel(fn, dim3(qtts::NWG), dim3(qtts::NTHR), args, 0, stream);
+  if ((e = hipLaunchKernel(fn, dim3(qtts::NWG), dim3(qtts::NTHR), args, 0, stream)) != hipSuccess) return e;
+  if ((e = hipEventRecord(dc.last, stream)) != hipSuccess) return e;
+  dc.last_stream = stream;
+  dc.has_last = true;
+  return hipSuccess;
 }
 
-void* lib_workspace(hipError_t* err) {
+void* lib_workspace(hipStream_t stream, hipError_t* err) {
   int dev = 0;
   *err = hipGetDevice(&dev);
   if (*err != hipSuccess) return nullptr;
   std::lock_guard<std::mutex> lk(g_mu);
-  void*& p = g_lib_ws[dev];
+  void*& p = g_lib_ws[{dev, stream}];
   if (p == nullptr) {
     *err = hipMalloc(&p, sizeof(Workspace));
     if (*err != hipSuccess) { p = nullptr; return nullptr; }
-    *err = hipMemset(p, 0, sizeof(Workspace));
+    g_seq.erase(p);   // a new workspace: its first launch zero-fills it
   }
   return p;
 }
@@ -1751,7 +1777,7 @@ hipError_t ref_launch(bool bb, int token, const void* embed, const void* emb, co
       g_normalized == nullptr || (emb == nullptr && embed == nullptr))
     return hipErrorInvalidValue;
   hipError_t e;
-  void* ws = lib_workspace(&e);
+  void* ws = lib_workspace(stream, &e);
   if (ws == nullptr) return e;
   KArgs a;
   base_args(a, layers, num_layers, final_norm, cos_t, sin_t, kc, vc, max_seq_len);
@@ -1818,7 +1844,56 @@ hipError_t qtts_debug_trace(void* device_buffer, size_t bytes) {
 
 hipError_t qtts_workspace_init(void* workspace, int device) {
   if (workspace == nullptr || (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return hipErrorInvalidValue;
-  return check_device(device);
+  const hipError_t e = check_device(device);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lk(g_mu);
+  g_seq.erase(workspace);   // new memory: the first launch that uses it zero-fills it
+  return hipSuccess;
+}
+
+hipError_t qtts_workspace_release(void* workspace, int count) {
+  if (workspace == nullptr || count < 1) return hipErrorInvalidValue;
+  std::lock_guard<std::mutex> lk(g_mu);
+  for (int i = 0; i < count; ++i) g_seq.erase(reinterpret_cast<Workspace*>(workspace) + i);
+  return hipSuccess;
+}
+
+hipError_t qtts_debug_set_sequence(void* workspace, unsigned int sequence) {
+  if (workspace == nullptr || sequence < 1 || sequence > kSeqLimit) return hipErrorInvalidValue;
+  std::lock_guard<std::mutex> lk(g_mu);
+  g_seq[workspace] = sequence;
+  return hipSuccess;
+}
+
+hipError_t qtts_shutdown(void) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  g_seq.clear();
+  g_trace = nullptr;
+  if (g_lib_ws.empty() && g_dev.empty()) return hipSuccess;   // nothing on any device: no HIP call
+  int cur = 0;
+  hipError_t first = hipGetDevice(&cur);
+  for (auto& kv : g_lib_ws) {
+    if (kv.second == nullptr) continue;
+    hipError_t e = hipSetDevice(kv.first.first);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e == hipSuccess) e = hipFree(kv.second);
+    if (first == hipSuccess) first = e;
+  }
+  g_lib_ws.clear();
+  g_seq.clear();
+  g_trace = nullptr;
+  for (auto& kv : g_dev) {
+    if (kv.second.last == nullptr) continue;
+    const hipError_t e = hipEventDestroy(kv.second.last);
+    if (first == hipSuccess) first = e;
+  }
+  const bool any = !g_dev.empty();
+  g_dev.clear();   // the next launch validates its device again
+  if (any) {
+    const hipError_t e = hipSetDevice(cur);
+    if (first == hipSuccess) first = e;
+  }
+  return first;
 }
 
 hipError_t qtts_workspace_check(void* workspace, unsigned int* error_code, hipStream_t stream) {
@@ -1927,6 +2002,7 @@ hipError_t qtts_backbone_step_streams(int n_streams, void* workspaces, const TTS
     io.history = in.history;
     io.n_history = in.n_history;
     io.seed = in.seed;
+    io.skip = in.skip_if;
   }
   // stream 0's position is the one launch() validates; the others were checked above
   return launch(true, a, stream, true, n_streams);

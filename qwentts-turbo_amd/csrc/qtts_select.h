@@ -55,12 +55,14 @@ struct SelScratch {
 };
 
 // Temperature / top-k / top-p / Gumbel-max over lg[0..n), n <= MAXV, one wave.
-// lg holds the masked logits (suppressed ids = -inf). Returns the same id on every lane.
+// lg holds the masked logits (bf16 values; suppressed ids = -inf). Returns the same id on
+// every lane.
 __device__ inline int wave_select(const float* lg, int n, const SelParams& sp, SelScratch* sc) {
   if (!sp.do_sample) return wave_argmax(lg, n);
   const int lane = threadIdx.x & 63;
   for (int i = lane; i < n; i += 64) {
-    const float v = lg[i] / sp.temperature;
+    // logits / temperature on bf16 logits rounds to bf16 in the reference (generator.py:189)
+    const float v = rbf(lg[i] / sp.temperature);
     sc->s[i] = v;
     sc->key[i] = fkey(v);
   }

@@ -4,7 +4,8 @@
 
   c0  backbone step: 28 layers, KV prefilled by 128 tokens, decode at position 128 (L=129)
   c1  code-predictor frame: 15 greedy groups from a backbone hidden and a group-0 id
-  c2  frame loop: 128-token prefill, 64 greedy frames; 32 sampled frames (top-k 50, T 0.9)
+  c2  frame loop: 128-token prefill, 64 greedy frames; 32 sampled frames (top-k 50, T 0.9);
+      12 frames with every head sampled (code predictor too, cp_do_sample)
   c3  long context: KV of 2044 tokens, 4 decode steps with distinct monotone (t, h, w)
   c4  batch of 8 streams with ragged attended lengths in [128, 1024]: one backbone step
       (codec head, suppress mask, greedy g0) and one code-predictor frame per stream
@@ -23,6 +24,10 @@ EOS_ID = 2150
 C2_GREEDY_FRAMES = 64
 C2_SAMPLED_FRAMES = 32
 C2_SAMPLING = dict(do_sample=True, temperature=0.9, top_k=50, top_p=1.0, repetition_penalty=1.05, seed=7)
+# sampled backbone and sampled code predictor (generate(cp_do_sample=True)): every head samples
+C2_CP_SAMPLED_FRAMES = 12
+C2_CP_SAMPLING = dict(do_sample=True, temperature=0.9, top_k=50, top_p=0.9, repetition_penalty=1.05, seed=11,
+                      cp_do_sample=True, cp_temperature=0.8, cp_top_k=40)
 C3_KV = 2044
 C3_STEPS = 4
 

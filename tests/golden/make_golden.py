@@ -97,24 +97,40 @@ def c1(pkg, manifest):
 
 
 def c2(pkg, manifest):
-    """Frame loop, greedy and sampled."""
+    """Frame loop from one 128-token prefill: greedy, sampled, and sampled with a sampled code
+    predictor (cp_do_sample)."""
     sd = cases.weights(pkg, "c2")
     tw = TalkerWeights.from_state_dict(sd, 28, 5)
     prefill, trailing, pad = cases.c2_inputs()
     talker = TalkerOracle(tw, max_seq=4096)
-    greedy = talker.generate(prefill, trailing, pad, cases.EOS_ID, max_tokens=cases.C2_GREEDY_FRAMES,
-                             min_new_tokens=cases.C2_GREEDY_FRAMES)
+    hidden = talker.prefill(prefill)
+    k0, v0, pos0 = talker.bb.k.clone(), talker.bb.v.clone(), talker.bb.position
+    lg0 = head_logits(tw.codec_head, hidden)
+    lg0[suppress_mask(tw.codec_head.shape[0], cases.EOS_ID)] = float("-inf")
+
+    def run(n, sampling):
+        talker.bb.k.copy_(k0)
+        talker.bb.v.copy_(v0)
+        talker.bb.position = pos0
+        s = dict(do_sample=False, temperature=0.9, top_k=50, top_p=1.0, repetition_penalty=1.0, seed=0,
+                 cp_do_sample=False, cp_temperature=0.9, cp_top_k=50)
+        s.update(sampling)
+        g0 = sample_token(lg0, s["do_sample"], s["temperature"], s["top_k"], s["top_p"], cases.EOS_ID,
+                          seed=s["seed"], frame_step=0, group=0)
+        return talker.decode_frames(hidden, g0, trailing, pad, cases.EOS_ID, max_tokens=n, min_new_tokens=n, **s)
+
+    greedy = run(cases.C2_GREEDY_FRAMES, {})
     log("c2 greedy frames", len(greedy), greedy[0], greedy[-1])
-    s = cases.C2_SAMPLING
-    sampled = talker.generate(prefill, trailing, pad, cases.EOS_ID, max_tokens=cases.C2_SAMPLED_FRAMES,
-                              do_sample=s["do_sample"], temperature=s["temperature"], top_k=s["top_k"],
-                              top_p=s["top_p"], repetition_penalty=s["repetition_penalty"], seed=s["seed"],
-                              min_new_tokens=cases.C2_SAMPLED_FRAMES)
+    sampled = run(cases.C2_SAMPLED_FRAMES, cases.C2_SAMPLING)
     log("c2 sampled frames", len(sampled), sampled[0], sampled[-1])
-    np.savez_compressed(HERE / "c2_frames.npz", greedy=np.array(greedy, dtype=np.int32), sampled=np.array(sampled, dtype=np.int32))
+    cp_sampled = run(cases.C2_CP_SAMPLED_FRAMES, cases.C2_CP_SAMPLING)
+    log("c2 cp-sampled frames", len(cp_sampled), cp_sampled[0], cp_sampled[-1])
+    np.savez_compressed(HERE / "c2_frames.npz", greedy=np.array(greedy, dtype=np.int32),
+                        sampled=np.array(sampled, dtype=np.int32), cp_sampled=np.array(cp_sampled, dtype=np.int32))
     manifest["cases"]["c2"] = {"seed": cases.SEEDS["c2"], "norm_mean": 1.0, "weights": cases.weight_digest(sd),
                                "eos_id": cases.EOS_ID, "greedy_frames": len(greedy), "sampled_frames": len(sampled),
-                               "sampling": s}
+                               "sampling": cases.C2_SAMPLING, "cp_sampled_frames": len(cp_sampled),
+                               "cp_sampling": cases.C2_CP_SAMPLING}
 
 
 def c3(pkg, manifest):

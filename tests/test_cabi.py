@@ -71,3 +71,20 @@ def test_torch_extension_exposes_reference_classes(pkg):
         c = getattr(ext, cls)
         for m in methods:
             assert hasattr(c, m), (cls, m)
+
+
+def test_workspace_hooks_validate_arguments_without_a_gpu():
+    """The host-only workspace hooks reject bad arguments; qtts_shutdown with nothing on any
+    device makes no HIP call and succeeds."""
+    lib = ctypes.CDLL(str(LIB))
+    P = ctypes.c_void_p
+    lib.qtts_workspace_release.argtypes = [P, ctypes.c_int]
+    lib.qtts_debug_set_sequence.argtypes = [P, ctypes.c_uint]
+    assert lib.qtts_workspace_release(None, 1) != 0
+    assert lib.qtts_workspace_release(P(4096), 0) != 0
+    assert lib.qtts_workspace_release(P(4096), 2) == 0
+    assert lib.qtts_debug_set_sequence(None, 5) != 0
+    assert lib.qtts_debug_set_sequence(P(4096), 0) != 0 and lib.qtts_debug_set_sequence(P(4096), 1 << 20) != 0
+    assert lib.qtts_debug_set_sequence(P(4096), 5) == 0
+    assert lib.qtts_workspace_release(P(4096), 1) == 0
+    assert lib.qtts_shutdown() == 0

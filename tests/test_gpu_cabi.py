@@ -146,7 +146,7 @@ class QttsBackboneStream(ctypes.Structure):
     """include/qwentts_amd.h QttsBackboneStream."""
     _fields_ = [("k_cache", P), ("v_cache", P), ("position", I), ("pos3", I * 3), ("input_embedding", P),
                 ("out_hidden", P), ("out_residual", P), ("out_logits", P), ("out_token", P), ("history", P),
-                ("n_history", I), ("seed", ctypes.c_ulonglong)]
+                ("n_history", I), ("seed", ctypes.c_ulonglong), ("skip_if", P)]
 
 
 def test_qtts_backbone_step_streams(lib, model):
@@ -196,6 +196,22 @@ def test_qtts_backbone_step_streams(lib, model):
         assert rel_l2(bufs[s]["kc"][:, :, pos].float().cpu(), orcs[s].k[:, :, pos].float()) < TOL
     print(f"qtts_backbone_step_streams, 3 streams: worst rel_l2 {worst:.2e}", flush=True)
     assert worst < TOL
+    # a stream whose skip flag is set computes nothing and writes nothing (streams that ended)
+    flags = torch.tensor([0, 1, 0], dtype=torch.int32, device="cuda")
+    marker = torch.full((1024,), 7.0, device="cuda")
+    bufs[1]["hid"].copy_(marker)
+    for s in range(3):
+        arr[s].skip_if = flags.data_ptr() + 4 * s
+        arr[s].position = positions[s] + 1
+        arr[s].pos3[0] = arr[s].pos3[1] = arr[s].pos3[2] = positions[s] + 1
+    assert fn(3, _ptr(ws), _ptr(table), 2, _ptr(norm), _ptr(cos), _ptr(sin), max_seq, arr, None, 0, 0, 1.0, -1, 0,
+              None, 0, _stream()) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(bufs[1]["hid"], marker)
+    assert int(bufs[1]["kc"][:, :, positions[1] + 1].float().abs().sum()) == 0
+    for s in (0, 2):
+        hr, _ = orcs[s].step(xs[s], pos=positions[s] + 1)
+        assert rel_l2(bufs[s]["hid"].cpu(), hr) < TOL
     # a stream position outside the cache is rejected before any launch
     arr[2].position = max_seq
     assert fn(3, _ptr(ws), _ptr(table), 2, _ptr(norm), _ptr(cos), _ptr(sin), max_seq, arr, None, 0, 0, 1.0, -1, 0,
@@ -243,3 +259,88 @@ def test_qtts_backbone_prefill(lib, model):
     assert fn(_ptr(ws), wsb, _ptr(table), 2, _ptr(norm), _ptr(cos), _ptr(sin), _ptr(kc), _ptr(vc), max_seq, 0, 0,
               None, _ptr(xd), _ptr(hid), None, 0, None, None, 0, -1, 0, None, 0, _stream()) != 0
     assert lib.qtts_prefill_workspace_bytes(0, 0) == 0
+
+
+def _bb_step_args(b, table, norm, cos, sin, max_seq, pos):
+    return (_ptr(b["x"][pos]), _ptr(table), _ptr(norm), _ptr(cos), _ptr(sin), _ptr(b["kc"]), _ptr(b["vc"]),
+            _ptr(b["res"][pos]), None, None, None, None, None, None, None, _ptr(b["hid"][pos]), 2, pos, pos + 1,
+            max_seq, 128 ** -0.5)
+
+
+def test_reference_launchers_on_two_streams(lib, model):
+    """A backbone decoder on one HIP stream and a code-predictor decoder on another, their
+    launches queued alternately with no synchronisation in between (the reference gives every
+    decoder object its own scratch). The library keeps one workspace per (device, stream) and
+    orders its launches across streams, so every step equals the oracle's."""
+    sd, tw = model
+    steps, max_seq = 6, 32
+    cos, sin = (t.cuda() for t in rope_tables(max_seq, 128, 1e6))
+    g = torch.Generator().manual_seed(21)
+    dec = {}
+    for kind, lw, nrm, kv_dt in (("backbone", tw.bb_layers, tw.bb_norm, torch.bfloat16),
+                                  ("cp", tw.cp_layers, tw.cp_norm, torch.float32)):
+        layers = [[t.cuda().contiguous() for t in l] for l in lw]
+        x = torch.randn(steps, 1024, generator=g).to(torch.bfloat16)
+        dec[kind] = dict(layers=layers, table=_layer_table(layers), norm=nrm.cuda(), xh=x, x=x.cuda(),
+                         kc=torch.zeros(2, 8, max_seq, 128, dtype=kv_dt, device="cuda"),
+                         vc=torch.zeros(2, 8, max_seq, 128, dtype=kv_dt, device="cuda"),
+                         res=torch.zeros(steps, 1024, dtype=kv_dt, device="cuda"),
+                         hid=torch.zeros(steps, 1024, device="cuda"),
+                         orc=DecoderOracle(lw, nrm, max_seq, kind, "kernel"))
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    for pos in range(steps):
+        for kind, st, fn in (("backbone", sa, lib.launch_tts_decode_with_embedding),
+                             ("cp", sb, lib.launch_cp_decode_with_embedding)):
+            b = dec[kind]
+            assert fn(*_bb_step_args(b, b["table"], b["norm"], cos, sin, max_seq, pos), ctypes.c_void_p(st.cuda_stream)) == 0
+    torch.cuda.synchronize()
+    worst = 0.0
+    for kind, b in dec.items():
+        for pos in range(steps):
+            hr, outs = b["orc"].step(b["xh"][pos], pos=pos)
+            worst = max(worst, rel_l2(b["hid"][pos].cpu(), hr), rel_l2(b["res"][pos].float().cpu(), outs[-1]))
+    print(f"reference launchers on two streams, {steps} steps each: worst rel_l2 {worst:.2e}", flush=True)
+    assert worst < TOL
+
+
+def test_sequence_wrap_keeps_results(lib, model):
+    """The tag sequence of a workspace runs out after 2^20 - 2 launches; the launch that finds it
+    used up zero-fills the workspace and restarts. Steps on either side of that point (set
+    through the test hook) equal the oracle's."""
+    sd, tw = model
+    layers = [[t.cuda().contiguous() for t in lw] for lw in tw.bb_layers]
+    table = _layer_table(layers)
+    norm = tw.bb_norm.cuda()
+    max_seq = 16
+    cos, sin = (t.cuda() for t in rope_tables(max_seq, 128, 1e6))
+    lib.qtts_workspace_bytes.restype = ctypes.c_size_t
+    ws = torch.zeros(lib.qtts_workspace_bytes(), dtype=torch.uint8, device="cuda")
+    lib.qtts_workspace_init.argtypes = [P, I]
+    lib.qtts_workspace_init.restype = I
+    lib.qtts_debug_set_sequence.argtypes = [P, ctypes.c_uint]
+    lib.qtts_debug_set_sequence.restype = I
+    assert lib.qtts_workspace_init(_ptr(ws), torch.cuda.current_device()) == 0
+    fn = lib.qtts_backbone_step
+    fn.argtypes = [P, P, I, P, P, P, P, P, I, I, P, P, P, I, P, P, P, I, P, P, I, P, I, F, I, I, P, I, P, P]
+    fn.restype = I
+    kc = torch.zeros(2, 8, max_seq, 128, dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros_like(kc)
+    hid = torch.empty(1024, device="cuda")
+    orc = DecoderOracle(tw.bb_layers, tw.bb_norm, max_seq, "backbone", "kernel")
+    g = torch.Generator().manual_seed(31)
+    worst = 0.0
+    for pos in range(6):
+        if pos == 2:
+            assert lib.qtts_debug_set_sequence(_ptr(ws), (1 << 20) - 3) == 0   # two launches before the wrap
+        x = torch.randn(1024, generator=g).to(torch.bfloat16)
+        xd = x.cuda()
+        assert fn(_ptr(ws), _ptr(table), 2, _ptr(norm), _ptr(cos), _ptr(sin), _ptr(kc), _ptr(vc), max_seq, pos, None,
+                  _ptr(xd), None, 0, _ptr(hid), None, None, 0, None, None, 0, None, 0, 1.0, -1, 0, None, 0, None,
+                  _stream()) == 0
+        torch.cuda.synchronize()
+        hr, _ = orc.step(x, pos=pos)
+        worst = max(worst, rel_l2(hid.cpu(), hr))
+    assert lib.qtts_debug_set_sequence(_ptr(ws), 0) != 0 and lib.qtts_debug_set_sequence(_ptr(ws), 1 << 20) != 0
+    print(f"sequence wrap: 6 steps across it, worst rel_l2 {worst:.2e}", flush=True)
+    assert worst < TOL

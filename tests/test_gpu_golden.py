@@ -16,7 +16,7 @@ import pytest
 import torch
 
 from golden import cases
-from oracle.qtts_oracle import rel_l2
+from oracle.qtts_oracle import TalkerOracle, TalkerWeights, head_logits, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -47,8 +47,7 @@ def test_c0_backbone_prefill_and_step(pkg, gains):
     bb.check_error()
     e_k = rel_l2(h, torch.from_numpy(fx[f"{gains}_kernel_hidden"]))
     e_h = rel_l2(h, torch.from_numpy(fx[f"{gains}_hf_bf16_hidden"]))
-    w = dsd["talker.codec_head.weight"]
-    lg = (w.double() @ h.cuda().to(torch.bfloat16).double()).float().cpu()
+    lg = head_logits(dsd["talker.codec_head.weight"].cpu(), h)
     e_lk = rel_l2(lg, torch.from_numpy(fx[f"{gains}_kernel_logits"]))
     e_lh = rel_l2(lg, torch.from_numpy(fx[f"{gains}_hf_bf16_logits"]))
     _print(f"c0 gains {gains}: hidden vs oracle {e_k:.2e}, vs HF-bf16 {e_h:.2e}; logits vs oracle {e_lk:.2e}, "
@@ -129,21 +128,81 @@ def test_c3_long_context_mrope(pkg):
     assert worst < TOL
 
 
-def test_c2_generate_with_mfma_prefill(c2_gen):
-    """generate() with its default one-call MFMA prefill: the first frame's group 0 is the token
-    that prefill selects from the prompt (bf16 forward, suppress mask, EOS removed), every frame
-    holds 16 in-range ids, and the frame count is max_tokens while EOS stays suppressed."""
+def test_c2_cp_sampled_frames(c2_gen):
+    """Every head sampled, the 15 code-predictor heads included (generate(cp_do_sample=True):
+    full-logit gather and top-k / temperature / Gumbel-max selection in every poller wave)."""
+    fx = cases.load("c2_frames")
     prefill, trailing, pad = cases.c2_inputs()
-    n = 6
-    frames = c2_gen.generate(prefill, None, trailing, pad, max_tokens=n, min_new_tokens=n)
-    assert len(frames) == n and all(len(f) == 16 for f in frames)
-    assert all(0 <= t < 3072 for f in frames for t in f)
+    n = cases.C2_CP_SAMPLED_FRAMES
+    s = cases.C2_CP_SAMPLING
+    frames = c2_gen.generate(prefill, None, trailing, pad, max_tokens=n, do_sample=s["do_sample"],
+                             temperature=s["temperature"], top_k=s["top_k"], top_p=s["top_p"],
+                             cp_do_sample=s["cp_do_sample"], cp_temperature=s["cp_temperature"],
+                             cp_top_k=s["cp_top_k"], repetition_penalty=s["repetition_penalty"], min_new_tokens=n,
+                             seed=s["seed"], prefill="steps")
+    got = np.array(frames, dtype=np.int32)
+    first_diff = next((i for i in range(min(len(got), len(fx["cp_sampled"]))) if (got[i] != fx["cp_sampled"][i]).any()),
+                      None)
+    _print(f"c2 cp-sampled: {len(frames)} frames, first differing frame {first_diff}")
+    assert got.shape == fx["cp_sampled"].shape and first_diff is None
+
+
+def test_c2_generate_mfma_prefill_greedy_64_vs_oracle(c2_gen, pkg):
+    """The default generate() (prefill="mfma": the one-call bf16 MFMA prefill, then the decode
+    kernels) for 64 greedy frames against the oracle's frame loop continuing from the GPU
+    prefill's own state: its K/V of the 128 prompt positions, its final hidden and its first
+    group-0 token. The prefill is run once on its own to capture that state; generate() must
+    reproduce it bit for bit (same first token, same prompt K/V) before the 64 frames are
+    compared id for id."""
+    prefill, trailing, pad = cases.c2_inputs()
+    n = cases.C2_GREEDY_FRAMES
     bb = c2_gen.backbone_mega.decoder
     bb.reset()
     tok = torch.full((1,), -1, dtype=torch.int32, device="cuda")
     bb.prefill(prefill[0].cuda(), tok, cases.EOS_ID, True)
-    _print(f"mfma prefill generate: first frame {frames[0][:4]}..., prefill token {int(tok.item())}")
-    assert frames[0][0] == int(tok.item())
+    torch.cuda.synchronize()
+    S = prefill.shape[1]
+    k0 = bb.get_k_cache()[:, :, :S].cpu().clone()
+    v0 = bb.get_v_cache()[:, :, :S].cpu().clone()
+    hidden = bb.hidden_state_buffer().cpu().clone()
+    g0 = int(tok.item())
+    frames = c2_gen.generate(prefill, None, trailing, pad, max_tokens=n, min_new_tokens=n)
+    assert torch.equal(bb.get_k_cache()[:, :, :S].cpu(), k0) and torch.equal(bb.get_v_cache()[:, :, :S].cpu(), v0)
+    assert frames[0][0] == g0
+    sd = cases.weights(pkg, "c2")
+    talker = TalkerOracle(TalkerWeights.from_state_dict(sd, 28, 5), max_seq=S + n + 8, policy="kernel")
+    talker.bb.set_kv(k0, v0)
+    talker.bb.position = S
+
+    def progress(step, fr):
+        if (step + 1) % 8 == 0:
+            _print(f"  oracle frame {step + 1}/{n}")
+
+    ref = talker.decode_frames(hidden, g0, trailing, pad, cases.EOS_ID, max_tokens=n, min_new_tokens=n,
+                               on_frame=progress)
+    got, exp = np.array(frames, dtype=np.int32), np.array(ref, dtype=np.int32)
+    first_diff = next((i for i in range(min(len(got), len(exp))) if (got[i] != exp[i]).any()), None)
+    _print(f"mfma-prefill generate: {len(frames)} frames, first frame {frames[0][:4]}..., first differing frame {first_diff}")
+    assert got.shape == (n, 16) and first_diff is None
+
+
+def test_c2_sampled_256_frames(c2_gen):
+    """Config 2's full length: 256 sampled frames (top-k 50, T 0.9) from the 128-token prompt
+    with EOS held back (min_new_tokens = 256): 256 frames of 16 in-range ids, error word clear.
+    (Token-exact checks of this loop are the 64 / 32 / 12-frame fixtures above.)"""
+    prefill, trailing, pad = cases.c2_inputs()
+    n = 256
+    s = cases.C2_SAMPLING
+    frames = c2_gen.generate(prefill, None, trailing, pad, max_tokens=n, do_sample=True, temperature=0.9,
+                             top_k=50, top_p=1.0, repetition_penalty=s["repetition_penalty"], min_new_tokens=n,
+                             seed=s["seed"])
+    c2_gen.backbone_mega.decoder.check_error()
+    c2_gen.cp_mega.decoder.check_error()
+    arr = np.array(frames, dtype=np.int64)
+    _print(f"c2 256 sampled frames: shape {arr.shape}, distinct g0 {len(set(arr[:, 0].tolist()))}")
+    assert arr.shape == (n, 16)
+    assert (arr[:, 0] >= 0).all() and (arr[:, 0] < 2048).all()   # g0 outside the suppressed tail [2048, 3072)
+    assert (arr[:, 1:] >= 0).all() and (arr[:, 1:] < 2048).all()
 
 
 @pytest.mark.parametrize("k", [2, 13])

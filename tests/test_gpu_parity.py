@@ -245,3 +245,33 @@ def test_reference_kv_roundtrip(full, pkg):
     assert torch.equal(bb.get_k_cache()[:, :, :17].cpu(), k)
     assert torch.equal(bb.get_v_cache()[:, :, :17].cpu(), v)
     assert int(bb.get_k_cache()[:, :, 17:].abs().sum()) == 0
+
+
+def test_decode_step_token_id_and_argmax(full, pkg):
+    """The reference's token-id entry points (megakernel_backbone.py:218-227): decode_step(id)
+    gathers the codec embedding row and returns the final hidden; decode_step_with_argmax(id)
+    returns argmax(bf16(codec_head . bf16(h))) with no suppress mask, lowest id on ties."""
+    sd, dsd, tw = full
+    n = 2
+    sd2 = {k: v for k, v in dsd.items() if not k.startswith("talker.model.layers.") or int(k.split(".")[3]) < n}
+    bb = pkg.TTSMegakernelGenerator(model=sd2, max_seq_len=64)
+    orc = DecoderOracle(tw.bb_layers[:n], tw.bb_norm, 64, "backbone", "kernel")
+    emb = tw.codec_embedding.to(torch.bfloat16)
+    ids = [17, 2900, 1024, 3071, 0, 555]
+    worst = 0.0
+    for i, t in enumerate(ids):
+        if i % 2 == 0:
+            h = bb.decoder.decode_step(t).cpu()
+            hr, _ = orc.step(emb[t], pos=i)
+            worst = max(worst, rel_l2(h, hr))
+        else:
+            got = bb.decoder.decode_step_with_argmax(t)
+            hr, _ = orc.step(emb[t], pos=i)
+            lg = head_logits(tw.codec_head, hr)
+            ref = int(torch.nonzero(lg == lg.max())[0, 0])
+            _print(f"decode_step_with_argmax({t}): gpu {got} oracle {ref}")
+            assert got == ref
+    bb.check_error()
+    _print(f"decode_step(id): worst hidden rel_l2 {worst:.2e}")
+    assert worst < TOL
+    assert bb.decoder.position() == len(ids)

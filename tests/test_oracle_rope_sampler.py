@@ -111,8 +111,9 @@ def test_greedy_lowest_index_on_ties_and_eos_suppression():
 
 
 def _reference_rule(logits, temperature, top_k, top_p):
-    """generator.py:189-204 as written there: topk threshold, then sort / cumsum / shift."""
-    scaled = logits / temperature
+    """generator.py:189-204 as written there, on the reference's bf16 logits: topk threshold,
+    then sort / cumsum / shift."""
+    scaled = logits.to(torch.bfloat16) / temperature
     if top_k > 0:
         kth = torch.topk(scaled, min(top_k, scaled.size(-1)))[0][-1]
         scaled = scaled.clone()
@@ -128,13 +129,32 @@ def _reference_rule(logits, temperature, top_k, top_p):
     return scaled
 
 
+def _distinct_bf16(n, seed):
+    """n distinct bf16 values: a random choice among all bf16 values of magnitude in
+    [2^-10, 32) (both signs; 3840 of them), in random order."""
+    g = torch.Generator().manual_seed(seed)
+    mag = torch.arange((127 - 10) << 7, (127 + 5) << 7, dtype=torch.int32)     # exponent and mantissa bits
+    bits = torch.cat([mag, mag | 0x8000]).to(torch.int16)
+    vals = bits.view(torch.bfloat16).float()
+    assert vals.numel() >= n
+    return vals[torch.randperm(vals.numel(), generator=g)[:n]]
+
+
 @pytest.mark.parametrize("seed", range(6))
 @pytest.mark.parametrize("top_k,top_p", [(50, 1.0), (0, 0.8), (20, 0.5), (0, 0.05), (7, 0.95)])
 def test_filter_matches_reference_rule_on_distinct_values(seed, top_k, top_p):
-    g = torch.Generator().manual_seed(seed)
-    lg = torch.randn(3072, generator=g) * 3
-    a = torch.isfinite(filter_logits(lg, 0.9, top_k, top_p))
-    b = torch.isfinite(_reference_rule(lg, 0.9, top_k, top_p))
+    lg = _distinct_bf16(3072, seed)
+    # temperature 0.5 scales bf16 values exactly, so the scaled values stay distinct
+    a = torch.isfinite(filter_logits(lg, 0.5, top_k, top_p))
+    b = torch.isfinite(_reference_rule(lg, 0.5, top_k, top_p))
+    assert torch.equal(a, b)
+
+
+def test_temperature_scaling_rounds_to_bf16_like_the_reference():
+    """logits / temperature on bf16 logits is a bf16 tensor in the reference (generator.py:189)."""
+    lg = _distinct_bf16(3072, 9)
+    a = filter_logits(lg, 0.9, 0, 1.0)
+    b = (lg.to(torch.bfloat16) / 0.9).float()
     assert torch.equal(a, b)
 
 
