@@ -85,6 +85,27 @@ hipError_t launch_tts_decode_with_embedding(
     void* g_normalized, int num_layers, int position, int cache_len, int max_seq_len,
     float attn_scale, hipStream_t stream);
 
+/* No counterpart in the reference. For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): the same step as
+ * launch_tts_decode_with_embedding, but the exchange workspace is a static device array of
+ * QTTS_STATIC_SCRATCH_BYTES per GPU (one qtts_workspace_bytes() workspace), held until the
+ * process ends; no hipMalloc / hipFree / allocating routine is called (the first call on a
+ * device runs the one-time device set-up: property queries, a probe launch, an event).
+ * num_layers must be in [1, 440] (the launch tags of one workspace cover 440 layers); larger
+ * values return hipErrorInvalidValue. Every call on a GPU uses that GPU's one array, which
+ * keeps the last call's contents (the library zero-fills it before its first use and tags
+ * every later exchange, so nothing needs clearing between calls). The library orders its own
+ * launches on a device, but calls that are made to overlap on one GPU (other processes,
+ * graphs replayed concurrently on several streams) race on the array. */
+#define QTTS_STATIC_SCRATCH_BYTES 971008u
+hipError_t launch_tts_decode_with_embedding_static(
+    const void* input_embedding, const TTSLayerWeights* layer_weights,
+    const void* final_norm_weight, const void* cos_table, const void* sin_table,
+    void* k_cache, void* v_cache, void* hidden_buffer, void* g_activations, void* g_residual,
+    void* g_q, void* g_k, void* g_v, void* g_attn_out, void* g_mlp_intermediate,
+    void* g_normalized, int num_layers, int position, int cache_len, int max_seq_len,
+    float attn_scale, hipStream_t stream);
+
 /* Replaces: launch_cp_decode_with_embedding (/root/reference/qwentts_turbo/csrc/fused_decode_code_predictor.cu:674-730) */
 hipError_t launch_cp_decode_with_embedding(
     const void* input_embedding, const CPLayerWeights* layer_weights,

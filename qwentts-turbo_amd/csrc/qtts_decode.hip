@@ -1627,6 +1627,7 @@ struct DeviceCheck {
   hipEvent_t last = nullptr;
   hipStream_t last_stream = nullptr;
   bool has_last = false;
+  void* scratch = nullptr;   // device address of this device's copy of `scratch`
 };
 std::mutex g_mu;
 std::unordered_map<int, DeviceCheck> g_dev;
@@ -1641,6 +1642,13 @@ uint64_t* g_trace = nullptr;   // optional step timeline buffer
 // XCC id of every workgroup of the probe launch (a static device array: the set-up allocates nothing)
 __device__ int g_xcc_probe[qtts::NWG];
 
+// Exchange workspace of launch_tts_decode_with_embedding_static: one Workspace per device,
+// held until the process ends. In host code `scratch` is only a handle for
+// hipGetSymbolAddress; the device address is kept per device in DeviceCheck::scratch.
+constexpr size_t kStaticScratchBytes = sizeof(Workspace);
+static_assert(kStaticScratchBytes == QTTS_STATIC_SCRATCH_BYTES, "QTTS_STATIC_SCRATCH_BYTES must equal sizeof(Workspace)");
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
 __global__ void xcc_probe_kernel() {
   if (threadIdx.x == 0) g_xcc_probe[blockIdx.x] = (int)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15u);
 }
@@ -1653,37 +1661,51 @@ __global__ void zero_kernel(uint4* p, size_t n16) {
 // 256 workgroups is co-resident when the device is not shared with other kernels), and workgroup
 // b placed on XCC (b + r) % 8 for a fixed rotation r, 32 workgroups per XCD. Every in-kernel wait
 // is bounded, so a launch that is not co-resident ends with the error word set instead of hanging.
+// Runs its HIP calls with `device` current (the caller's current device is restored).
+hipError_t check_device_locked(int device, DeviceCheck& dc);
 hipError_t check_device(int device) {
   std::lock_guard<std::mutex> lk(g_mu);
   DeviceCheck& dc = g_dev[device];
   if (dc.done) return dc.status;
   dc.done = true;
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return dc.status = e;
+  if (cur != device && (e = hipSetDevice(device)) != hipSuccess) return dc.status = e;
+  dc.status = check_device_locked(device, dc);
+  if (cur != device && (e = hipSetDevice(cur)) != hipSuccess && dc.status == hipSuccess) dc.status = e;
+  return dc.status;
+}
+hipError_t check_device_locked(int device, DeviceCheck& dc) {
   hipDeviceProp_t prop;
   hipError_t e = hipGetDeviceProperties(&prop, device);
-  if (e != hipSuccess) return dc.status = e;
+  if (e != hipSuccess) return e;
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0 || prop.multiProcessorCount != qtts::NWG)
-    return dc.status = hipErrorInvalidDevice;
+    return hipErrorInvalidDevice;
   const void* fns[] = {(const void*)qtts::qtts_decode_kernel<true, false>, (const void*)qtts::qtts_decode_kernel<false, false>,
                        (const void*)qtts::qtts_decode_kernel<false, true>, (const void*)qtts::qtts_decode_kernel<true, true>};
   for (const void* fn : fns) {
     int occ = 0;
     e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, qtts::NTHR, 0);
-    if (e != hipSuccess || occ < 1) return dc.status = (e != hipSuccess ? e : hipErrorInvalidDevice);
+    if (e != hipSuccess || occ < 1) return e != hipSuccess ? e : hipErrorInvalidDevice;
   }
   hipLaunchKernelGGL(xcc_probe_kernel, dim3(qtts::NWG), dim3(64), 0, 0);
   e = hipGetLastError();
   int h[qtts::NWG];
   if (e == hipSuccess) e = hipMemcpyFromSymbol(h, HIP_SYMBOL(g_xcc_probe), sizeof(h), 0, hipMemcpyDeviceToHost);
-  if (e != hipSuccess) return dc.status = e;
+  if (e != hipSuccess) return e;
   int count[16] = {0};
   for (int b = 0; b < qtts::NWG; ++b) {
-    if (h[b] < 0 || h[b] >= qtts::NXCD || ((h[b] - b) & 7) != ((h[0] - 0) & 7)) return dc.status = hipErrorInvalidDevice;
+    if (h[b] < 0 || h[b] >= qtts::NXCD || ((h[b] - b) & 7) != ((h[0] - 0) & 7)) return hipErrorInvalidDevice;
     ++count[h[b]];
   }
   for (int x = 0; x < qtts::NXCD; ++x)
-    if (count[x] != qtts::WPX) return dc.status = hipErrorInvalidDevice;
-  if ((e = hipEventCreateWithFlags(&dc.last, hipEventDisableTiming)) != hipSuccess) return dc.status = e;
-  return dc.status = hipSuccess;
+    if (count[x] != qtts::WPX) return hipErrorInvalidDevice;
+  if ((e = hipEventCreateWithFlags(&dc.last, hipEventDisableTiming)) != hipSuccess) return e;
+  // this device's copy of the static exchange workspace (the no-allocation entry point's)
+  if ((e = hipGetSymbolAddress(&dc.scratch, HIP_SYMBOL(scratch))) != hipSuccess) return e;
+  if (dc.scratch == nullptr || (reinterpret_cast<uintptr_t>(dc.scratch) & 255u) != 0) return hipErrorInvalidSymbol;
+  return hipSuccess;
 }
 
 // Tag base of a launch over the n consecutive workspaces at ws. The launch takes the largest
@@ -1768,17 +1790,28 @@ void base_args(KArgs& a, const TTSLayerWeights* layers, int num_layers, const vo
   a.sel.top_p = 1.0f;
 }
 
+// static_ws: use this device's static exchange workspace instead of the library-owned one
 hipError_t ref_launch(bool bb, int token, const void* embed, const void* emb, const TTSLayerWeights* layers,
                       const void* final_norm, const void* cos_t, const void* sin_t, void* kc, void* vc,
                       void* hidden_buffer, void* g_normalized, int num_layers, int position, int cache_len,
-                      int max_seq_len, float attn_scale, hipStream_t stream) {
+                      int max_seq_len, float attn_scale, hipStream_t stream, bool static_ws = false) {
   if (cache_len != position + 1 || position < 0 || position >= max_seq_len) return hipErrorInvalidValue;
   if (layers == nullptr || final_norm == nullptr || cos_t == nullptr || sin_t == nullptr || kc == nullptr || vc == nullptr ||
       g_normalized == nullptr || (emb == nullptr && embed == nullptr))
     return hipErrorInvalidValue;
   hipError_t e;
-  void* ws = lib_workspace(stream, &e);
-  if (ws == nullptr) return e;
+  void* ws = nullptr;
+  if (static_ws) {
+    int dev = 0;
+    if ((e = hipGetDevice(&dev)) != hipSuccess) return e;
+    if ((e = check_device(dev)) != hipSuccess) return e;   // first call on a device: set-up, scratch address
+    std::lock_guard<std::mutex> lk(g_mu);
+    ws = g_dev[dev].scratch;
+    if (ws == nullptr) return hipErrorInvalidSymbol;
+  } else {
+    ws = lib_workspace(stream, &e);
+    if (ws == nullptr) return e;
+  }
   KArgs a;
   base_args(a, layers, num_layers, final_norm, cos_t, sin_t, kc, vc, max_seq_len);
   a.scale = attn_scale;
@@ -1818,6 +1851,19 @@ hipError_t launch_tts_decode_with_embedding(const void* input_embedding, const T
   return ref_launch(true, 0, nullptr, input_embedding, layer_weights, final_norm_weight, cos_table, sin_table, k_cache,
                     v_cache, hidden_buffer, g_normalized, num_layers, position, cache_len, max_seq_len, attn_scale,
                     stream);
+}
+
+hipError_t launch_tts_decode_with_embedding_static(const void* input_embedding, const TTSLayerWeights* layer_weights,
+                                                   const void* final_norm_weight, const void* cos_table,
+                                                   const void* sin_table, void* k_cache, void* v_cache,
+                                                   void* hidden_buffer, void*, void*, void*, void*, void*, void*, void*,
+                                                   void* g_normalized, int num_layers, int position, int cache_len,
+                                                   int max_seq_len, float attn_scale, hipStream_t stream) {
+  // the static workspace's tags cover at most MAX_LAYER_PASSES layers in one launch
+  if (input_embedding == nullptr || num_layers < 1 || num_layers > qtts::MAX_LAYER_PASSES) return hipErrorInvalidValue;
+  return ref_launch(true, 0, nullptr, input_embedding, layer_weights, final_norm_weight, cos_table, sin_table, k_cache,
+                    v_cache, hidden_buffer, g_normalized, num_layers, position, cache_len, max_seq_len, attn_scale,
+                    stream, /*static_ws=*/true);
 }
 
 hipError_t launch_cp_decode_with_embedding(const void* input_embedding, const CPLayerWeights* layer_weights,
