@@ -125,8 +125,8 @@ class MegakernelTTSDecoder {
     position_ = 0;
   }
   ~MegakernelTTSDecoder() {
-    qtts_workspace_release(ws_.data_ptr(), 1);
-    if (ws_streams_.defined()) qtts_workspace_release(ws_streams_.data_ptr(), kMaxStreams);
+    (void)qtts_workspace_release(ws_.data_ptr(), 1);
+    if (ws_streams_.defined()) (void)qtts_workspace_release(ws_streams_.data_ptr(), kMaxStreams);
   }
   MegakernelTTSDecoder(const MegakernelTTSDecoder&) = delete;
   MegakernelTTSDecoder& operator=(const MegakernelTTSDecoder&) = delete;
@@ -407,8 +407,8 @@ class MegakernelCodePredictorDecoder {
     position_ = 0;
   }
   ~MegakernelCodePredictorDecoder() {
-    qtts_workspace_release(ws_.data_ptr(), 1);
-    if (ws_streams_.defined()) qtts_workspace_release(ws_streams_.data_ptr(), kMaxStreams);
+    (void)qtts_workspace_release(ws_.data_ptr(), 1);
+    if (ws_streams_.defined()) (void)qtts_workspace_release(ws_streams_.data_ptr(), kMaxStreams);
   }
   MegakernelCodePredictorDecoder(const MegakernelCodePredictorDecoder&) = delete;
   MegakernelCodePredictorDecoder& operator=(const MegakernelCodePredictorDecoder&) = delete;

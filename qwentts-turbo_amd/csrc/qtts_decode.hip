@@ -708,6 +708,16 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   // The lane holds channels c = lane and c + 64 (the rotate_half partners) of q head 0, q head 1,
   // k and v (the QKV slot order pairs them).
   bool kv_pending = false;
+  // The KV entry of the new token is read only by workgroups of this XCD (KV head = XCD), at
+  // later positions, through this XCD's L2 (L1-bypassing loads). Its stores reaching L2 before
+  // this wave's next slot publish is therefore all the ordering needed: a wait for the wave's
+  // outstanding vector stores, not an agent-scope release (whose L2 write-back would sit on
+  // the critical path of every layer).
+  auto kv_write_done = [&]() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  };
   auto prep_att = [&](int lp, int layer, int pos, int C) {
     const int par = lp & 1;
     const double cl = rc[0], ch = rc[1], sl = rsn[0], sh = rsn[1];
@@ -750,7 +760,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
         gput(vc, vl); gput(vc + 64, vh);
       }
       // ordered before this wave's next slot publish (prep_gu), where the wait for the stores
-      // costs nothing: the entry is read from memory only at later positions or launches
+      // costs nothing: the entry is read only at later positions or launches
       kv_pending = true;
     }
   };
@@ -793,7 +803,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       }
       poll_sum8_rows(P, ws->opart[par], 32 * li, tag_of(lp, T_OPART), sm);
       if (kv_pending) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");   // the KV entry written in prep_att
+        kv_write_done();   // the KV entry written in prep_att
         kv_pending = false;
       }
 #pragma unroll
@@ -806,7 +816,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       double s0, s1;
       poll_sum8(P, ws->opart[par], 32 * li, tag_of(lp, T_OPART), s0, s1);
       if (kv_pending) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");   // the KV entry written in prep_att
+        kv_write_done();   // the KV entry written in prep_att
         kv_pending = false;
       }
       if (lane < 16) pub_local2(&ws->h1[xcd][par][row], (float)((double)r0 + s0), (float)((double)r1 + s1), tag_of(lp, T_H1));
