@@ -13,6 +13,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <type_traits>
 
 namespace qtts {
 
@@ -66,6 +67,22 @@ __device__ __forceinline__ double dot8d(const u32x4 w, const double* x, double a
   return acc;
 }
 
+// The same in f32 (per-lane FMA chain; the code-predictor kernel's arithmetic, as the reference's
+// CP kernel accumulates in f32).
+__device__ __forceinline__ float dot8f(const u32x4 w, const float* x, float acc) {
+  acc = fmaf(bflo(w.x), x[0], acc);
+  acc = fmaf(bfhi(w.x), x[1], acc);
+  acc = fmaf(bflo(w.y), x[2], acc);
+  acc = fmaf(bfhi(w.y), x[3], acc);
+  acc = fmaf(bflo(w.z), x[4], acc);
+  acc = fmaf(bfhi(w.z), x[5], acc);
+  acc = fmaf(bflo(w.w), x[6], acc);
+  acc = fmaf(bfhi(w.w), x[7], acc);
+  return acc;
+}
+__device__ __forceinline__ double dot8a(const u32x4 w, const double* x, double acc) { return dot8d(w, x, acc); }
+__device__ __forceinline__ float dot8a(const u32x4 w, const float* x, float acc) { return dot8f(w, x, acc); }
+
 // Value the optimizer must treat as unknown (an empty asm that claims to modify it): derived
 // quantities cannot be hoisted or CSE'd across the point where it is produced.
 __device__ __forceinline__ int opaque(int x) {
@@ -106,6 +123,22 @@ __device__ __forceinline__ double rcp_d(double x) {
   y = fma(y, fma(-x, y, 1.0), y);
   return y;
 }
+// 1 / sqrt(x) for normal x > 0 in f32: the hardware estimate refined by one Newton step.
+__device__ __forceinline__ float rsqrt_f(float x) {
+  float y = __builtin_amdgcn_rsqf(x);
+  const float h = 0.5f * x;
+  return fmaf(y, fmaf(-(h * y), y, 0.5f), y);
+}
+// 1 / x for normal x > 0 in f32: the hardware estimate refined by one Newton step.
+__device__ __forceinline__ float rcp_f(float x) {
+  float y = __builtin_amdgcn_rcpf(x);
+  return fmaf(y, fmaf(-x, y, 1.0f), y);
+}
+__device__ __forceinline__ double rsqrt_a(double x) { return rsqrt_d(x); }
+__device__ __forceinline__ float rsqrt_a(float x) { return rsqrt_f(x); }
+__device__ __forceinline__ double exp_a(double x) { return exp(x); }
+__device__ __forceinline__ float exp_a(float x) { return __expf(x); }
+
 // store through the global address space (a global_store, not a flat one)
 template <class T>
 __device__ __forceinline__ void gput(T* p, T v) {
@@ -145,14 +178,15 @@ __device__ __forceinline__ double xlane_d(double v) {
   const uint64_t r = (uint64_t)xlane<STEP>((uint32_t)u) | ((uint64_t)xlane<STEP>((uint32_t)(u >> 32)) << 32);
   return __builtin_bit_cast(double, r);
 }
-// a pair of doubles reduced together (e.g. a gate and an up projection of one row)
-struct d2 { double a, b; };
-__device__ __forceinline__ d2 operator+(d2 x, d2 y) { return d2{x.a + y.a, x.b + y.b}; }
+// a pair of values reduced together (e.g. a gate and an up projection of one row)
+template <class T> struct pair2 { T a, b; };
+template <class T>
+__device__ __forceinline__ pair2<T> operator+(pair2<T> x, pair2<T> y) { return pair2<T>{x.a + y.a, x.b + y.b}; }
 template <int STEP, typename T>
 __device__ __forceinline__ T xlane_t(T v) {
-  if constexpr (sizeof(T) == 16) return T{xlane_d<STEP>(v.a), xlane_d<STEP>(v.b)};
-  else if constexpr (sizeof(T) == 8) return xlane_d<STEP>(v);
-  else return xlane_f<STEP>(v);
+  if constexpr (std::is_same_v<T, double>) return xlane_d<STEP>(v);
+  else if constexpr (std::is_same_v<T, float>) return xlane_f<STEP>(v);
+  else return T{xlane_t<STEP>(v.a), xlane_t<STEP>(v.b)};
 }
 
 // Sum / max over aligned groups of WIDTH lanes (WIDTH in {16, 32, 64}); every lane of a group

@@ -136,7 +136,9 @@ struct Lds {
     double red[NMATH][2][8][64];   // chunked attention partials [wave][head][dim % 8][lane group * 16 + dim / 8]
     float vst[16][HDIM];           // code-predictor local attention: V of the context positions
   };
-  double pl[2][16];                // code-predictor local attention: p_j = exp(s_j - M) per head
+  double pl[2][16];                // (unused by the f32 code-predictor attention; kept for layout)
+  alignas(16) float plf[2][16];    // code-predictor local attention: p_j = exp(s_j - M) per head
+  float redmf[NMATH][2];           // its per-wave score maxima
   double redl[NMATH][4][2];         // their softmax sums
   double redm[2][NMATH][2];         // per (pass parity, wave, head) score max
   double wts[2][MAXC + 1];          // per head: chunk weights exp(m_c - M), then 1 / Z
@@ -465,6 +467,10 @@ __device__ __forceinline__ void step_barrier() {
 template <bool BB, bool XL>
 __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   __shared__ Lds s;
+  // Accumulation type: f64 in the backbone (its bf16 residual and KV make every stored rounding
+  // reproducible against the f64 oracle), f32 in the code predictor (f32 residual and KV, as
+  // the reference's CP kernel computes them).
+  using A = std::conditional_t<BB, double, float>;
   // lane index, re-derived opaquely at every step (see walk) so that lane-dependent slot
   // offsets are recomputed where used instead of being hoisted out of the step loop and
   // kept live (and spilled) across all steps
@@ -569,23 +575,23 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     }
   };
   // RMSNorm statistic of the lane-distributed 1024-vector: 1 / sqrt(mean(x^2) + eps) in f64
-  auto rstd_of = [&](const float (&xv)[16]) -> double {
-    double s4[4] = {0.0, 0.0, 0.0, 0.0};
+  auto rstd_of = [&](const float (&xv)[16]) -> A {
+    A s4[4] = {A(0), A(0), A(0), A(0)};
 #pragma unroll
-    for (int j = 0; j < 16; ++j) s4[j & 3] = fma((double)xv[j], (double)xv[j], s4[j & 3]);
-    const double ss = group_sum<64>((s4[0] + s4[1]) + (s4[2] + s4[3]));
-    return rsqrt_d(ss / (double)HID + EPSD);
+    for (int j = 0; j < 16; ++j) s4[j & 3] = fma((A)xv[j], (A)xv[j], s4[j & 3]);
+    const A ss = group_sum<64>((s4[0] + s4[1]) + (s4[2] + s4[3]));
+    return rsqrt_a(ss / (A)HID + (A)EPSD);
   };
   // normalized values f32((x * rstd) * g) of the lane's 16 elements
   // f64 copy of a gain slice, made before the step's poll (off the critical path)
-  auto gains_d = [&](const uint32_t (&g)[8], double (&gd)[16]) {
+  auto gains_d = [&](const uint32_t (&g)[8], A (&gd)[16]) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) { gd[2 * k] = bflo(g[k]); gd[2 * k + 1] = bfhi(g[k]); }
   };
-  auto normed = [&](const float (&xv)[16], const double (&gd)[16], float (&y)[16]) {
-    const double r = rstd_of(xv);
+  auto normed = [&](const float (&xv)[16], const A (&gd)[16], float (&y)[16]) {
+    const A r = rstd_of(xv);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) y[j] = (float)(((double)xv[j] * r) * gd[j]);
+    for (int j = 0; j < 16; ++j) y[j] = (float)(((A)xv[j] * r) * gd[j]);
   };
   auto store_pairs = [&](float* dst, const float (&v)[16]) {
 #pragma unroll
@@ -599,7 +605,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
 
   // ---- poller: input of layer 0 of position pi (embedding source) -> xres, xn
   auto prep_input0 = [&](int pi) {
-    double gd[16];
+    A gd[16];
     gains_d(g_in, gd);
     float xv[16];
     if (a.cp_frame && pi == 0) {
@@ -671,7 +677,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   // ---- poller: next layer input (after ar2 of lp) -> xres, xn
   auto prep_input_next = [&](int lp) {
     float xv[16], y[16];
-    double gd[16];
+    A gd[16];
     gains_d(g_in, gd);
     poll_vec_regs(P, ws->xl[xcd][lp & 1], tag_of(lp, T_XL), xv);
     store_pairs(s.xres, xv);
@@ -681,7 +687,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   // ---- poller: final norm (after ar2 of lp) -> hb (bf16-rounded), outputs
   auto prep_final = [&](int lp) {
     float xv[16], y[16];
-    double gd[16];
+    A gd[16];
     gains_d(g_fin, gd);
     poll_vec_regs(P, ws->xl[xcd][lp & 1], tag_of(lp, T_XL), xv);
     store_pairs(s.xres, xv);
@@ -720,22 +726,22 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   };
   auto prep_att = [&](int lp, int layer, int pos, int C) {
     const int par = lp & 1;
-    const double cl = rc[0], ch = rc[1], sl = rsn[0], sh = rsn[1];
+    const A cl = rc[0], ch = rc[1], sl = rsn[0], sh = rsn[1];
     float v[8];   // [head][j]: head 0, 1 = q, 2 = k, 3 = v; j = 0: channel c, 1: channel c + 64
     {
       const uint32_t o = ws_off(P, ws->qkv[xcd][par]);
       poll_regs<4>(P, LROWS / 2, tag_of(lp, T_QKV), v, [o](int i) { return o + 16u * (uint32_t)i; });
     }
-    double ss[3];
+    A ss[3];
 #pragma unroll
-    for (int h = 0; h < 3; ++h) ss[h] = fma((double)v[2 * h], (double)v[2 * h], (double)v[2 * h + 1] * (double)v[2 * h + 1]);
+    for (int h = 0; h < 3; ++h) ss[h] = fma((A)v[2 * h], (A)v[2 * h], (A)v[2 * h + 1] * (A)v[2 * h + 1]);
     group_sum_n<64, 3>(ss);
     float outl[3], outh[3];
 #pragma unroll
     for (int h = 0; h < 3; ++h) {
-      const double r = rsqrt_d(ss[h] / (double)HDIM + EPSD);
-      const double gl = h < 2 ? qn[0] : kn[0], gh = h < 2 ? qn[1] : kn[1];
-      const double nl = ((double)v[2 * h] * r) * gl, nh = ((double)v[2 * h + 1] * r) * gh;
+      const A r = rsqrt_a(ss[h] / (A)HDIM + (A)EPSD);
+      const A gl = h < 2 ? qn[0] : kn[0], gh = h < 2 ? qn[1] : kn[1];
+      const A nl = ((A)v[2 * h] * r) * gl, nh = ((A)v[2 * h + 1] * r) * gh;
       outl[h] = (float)(nl * cl - nh * sl);
       outh[h] = (float)(nl * sh + nh * ch);
     }
@@ -822,7 +828,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       if (lane < 16) pub_local2(&ws->h1[xcd][par][row], (float)((double)r0 + s0), (float)((double)r1 + s1), tag_of(lp, T_H1));
     }
     float xv[16], y[16];
-    double gd[16];
+    A gd[16];
     gains_d(g_post, gd);
     poll_vec_regs(P, ws->h1[xcd][par], tag_of(lp, T_H1), xv);
     store_pairs(s.h1res, xv);
@@ -984,81 +990,92 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     step_barrier();   // s.red is reused by the next attention; s.attn complete
   };
 
-  // ---- math: code-predictor attention over the whole context (L <= 16). Lane group g of math
-  // wave w takes position j = 4 w + g: its score per head (8 dims per lane, summed over the 16
-  // lanes), the workgroup maximum M, then p_j = exp(s_j - M); p and V_j go to LDS and thread
-  // (h, d) forms f32((sum_j p_j V_j[d]) * (1 / sum_j p_j)) in f64. Positions j >= L carry p = 0
-  // and V = 0 (the tile's out-of-range lanes read zeros), so the sums run over all 16 exactly.
+  // ---- math: code-predictor attention over the whole context (L <= 16), in f32. Lane group g of
+  // math wave w takes position j = 4 w + g: its score per head (8 dims per lane, summed over
+  // the 16 lanes), the wave maximum, then after one barrier the workgroup maximum M and
+  // p_j = exp(s_j - M); p and V_j go to LDS and, after a second barrier, thread (h, d) forms
+  // (sum_j p_j V_j[d]) / (sum_j p_j) from operands it loads all at once. Positions j >= L carry
+  // p = 0 and V = 0 (the tile's out-of-range lanes read zeros), so the sums run over all 16.
   auto attention_cp_local = [&](int L) {
     const int Lold = L - 1;
     const int d0 = 8 * (lane & 15), g = lane >> 4;
     const int j = 4 * mw + g;
     float kv[8], vv[8];
+    const float4 qa0 = *reinterpret_cast<const float4*>(&s.q[0][d0]), qb0 = *reinterpret_cast<const float4*>(&s.q[0][d0 + 4]);
+    const float4 qa1 = *reinterpret_cast<const float4*>(&s.q[1][d0]), qb1 = *reinterpret_cast<const float4*>(&s.q[1][d0 + 4]);
     if (j == Lold) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) { kv[i] = s.knew[d0 + i]; vv[i] = s.vnew[d0 + i]; }
+      const float4 ka = *reinterpret_cast<const float4*>(&s.knew[d0]), kb = *reinterpret_cast<const float4*>(&s.knew[d0 + 4]);
+      const float4 va = *reinterpret_cast<const float4*>(&s.vnew[d0]), vb = *reinterpret_cast<const float4*>(&s.vnew[d0 + 4]);
+      kv[0] = ka.x; kv[1] = ka.y; kv[2] = ka.z; kv[3] = ka.w; kv[4] = kb.x; kv[5] = kb.y; kv[6] = kb.z; kv[7] = kb.w;
+      vv[0] = va.x; vv[1] = va.y; vv[2] = va.z; vv[3] = va.w; vv[4] = vb.x; vv[5] = vb.y; vv[6] = vb.z; vv[7] = vb.w;
     } else {
       unpack8<BB>(tk, true, 0, kv);
       unpack8<BB>(tk, false, 0, vv);
     }
-    double sc[2] = {0.0, 0.0};
+    const float q0[8] = {qa0.x, qa0.y, qa0.z, qa0.w, qb0.x, qb0.y, qb0.z, qb0.w};
+    const float q1[8] = {qa1.x, qa1.y, qa1.z, qa1.w, qb1.x, qb1.y, qb1.z, qb1.w};
+    float sc[2] = {0.0f, 0.0f};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      sc[0] = fma((double)s.q[0][d0 + i], (double)kv[i], sc[0]);
-      sc[1] = fma((double)s.q[1][d0 + i], (double)kv[i], sc[1]);
+      sc[0] = fmaf(q0[i], kv[i], sc[0]);
+      sc[1] = fmaf(q1[i], kv[i], sc[1]);
     }
     group_sum_n<16>(sc);
-    double mx[2];
+    float mx[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      sc[h] = j < L ? (double)(float)(sc[h] * (double)a.scale) : -INFINITY;
-      double u = xlane_d<4>(sc[h]);
-      mx[h] = u > sc[h] ? u : sc[h];
-      u = xlane_d<5>(mx[h]);
-      mx[h] = u > mx[h] ? u : mx[h];
+      sc[h] = j < L ? sc[h] * a.scale : -INFINITY;
+      mx[h] = fmaxf(sc[h], xlane_f<4>(sc[h]));
+      mx[h] = fmaxf(mx[h], xlane_f<5>(mx[h]));
     }
-    if (lane == 0) { s.redm[0][mw][0] = mx[0]; s.redm[0][mw][1] = mx[1]; }
-    step_barrier();
-    double p[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      double M = s.redm[0][0][h];
-#pragma unroll
-      for (int w = 1; w < NMATH; ++w) M = s.redm[0][w][h] > M ? s.redm[0][w][h] : M;
-      p[h] = j < L ? exp(sc[h] - M) : 0.0;
-    }
-    if ((lane & 15) == 0) { s.pl[0][j] = p[0]; s.pl[1][j] = p[1]; }
+    if (lane == 0) { s.redmf[mw][0] = mx[0]; s.redmf[mw][1] = mx[1]; }
+    // V of this lane's position, staged for the weighted sums (read after the second barrier)
     *reinterpret_cast<float4*>(&s.vst[j][d0]) = make_float4(vv[0], vv[1], vv[2], vv[3]);
     *reinterpret_cast<float4*>(&s.vst[j][d0 + 4]) = make_float4(vv[4], vv[5], vv[6], vv[7]);
     step_barrier();
+    float p[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float M = fmaxf(fmaxf(s.redmf[0][h], s.redmf[1][h]), fmaxf(s.redmf[2][h], s.redmf[3][h]));
+      p[h] = j < L ? __expf(sc[h] - M) : 0.0f;
+    }
+    if ((lane & 15) == 0) { s.plf[0][j] = p[0]; s.plf[1][j] = p[1]; }
+    step_barrier();
     const int t = threadIdx.x;   // 0..255: head t >> 7, dim t & 127
     const int h = t >> 7, d = t & 127;
+    float pj[16], vj[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 pp = *reinterpret_cast<const float4*>(&s.plf[h][4 * q]);
+      pj[4 * q] = pp.x; pj[4 * q + 1] = pp.y; pj[4 * q + 2] = pp.z; pj[4 * q + 3] = pp.w;
+    }
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) vj[jj] = s.vst[jj][d];
     // four independent chains (positions jj = 4 i + c), combined at the end
-    double A4[4] = {0.0, 0.0, 0.0, 0.0}, Z4[4] = {0.0, 0.0, 0.0, 0.0};
+    float A4[4] = {0.0f, 0.0f, 0.0f, 0.0f}, Z4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int jj = 0; jj < 16; ++jj) {
-      const double pj = s.pl[h][jj];
-      Z4[jj & 3] += pj;
-      A4[jj & 3] = fma(pj, (double)s.vst[jj][d], A4[jj & 3]);
+      Z4[jj & 3] += pj[jj];
+      A4[jj & 3] = fmaf(pj[jj], vj[jj], A4[jj & 3]);
     }
-    const double A = (A4[0] + A4[1]) + (A4[2] + A4[3]), Z = (Z4[0] + Z4[1]) + (Z4[2] + Z4[3]);
-    s.attn[t] = (float)(A * rcp_d(Z));
-    step_barrier();   // s.attn complete; vst / pl are reused by the next attention
+    const float As = (A4[0] + A4[1]) + (A4[2] + A4[3]), Z = (Z4[0] + Z4[1]) + (Z4[2] + Z4[3]);
+    s.attn[t] = As * rcp_f(Z);
+    step_barrier();   // s.attn complete; vst / plf are reused by the next attention
   };
 
   // ---- math: GEMV stages (f64 accumulation, f32 results)
-  auto load_x16 = [&](const float* x, double* xv) {
+  auto load_x16 = [&](const float* x, A* xv) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) { xv[i] = x[8 * lane + i]; xv[8 + i] = x[512 + 8 * lane + i]; }
   };
   auto math_qkv = [&](int lp, int lg, const TileQKV& tq) {
-    double xv[16];
+    A xv[16];
     load_x16(s.xn, xv);
     const uint32_t tg = tag_of(lp, T_QKV);
-    double v[4];
+    A v[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) v[r] = dot8d(tq.p[2 * r + 1], xv + 8, dot8d(tq.p[2 * r], xv, 0.0));
-    const double t = rs_sum<5, 4>(v, lane);   // row lane >> 4 in lanes 0, 16, 32, 48
+    for (int r = 0; r < 4; ++r) v[r] = dot8a(tq.p[2 * r + 1], xv + 8, dot8a(tq.p[2 * r], xv, A(0)));
+    const A t = rs_sum<5, 4>(v, lane);   // row lane >> 4 in lanes 0, 16, 32, 48
     // slot order pairs the rotate_half partners: channel c' of head h goes to slot
     // 128 h + 2 (c' mod 64) + c' / 64, so one 16-byte pair holds channels c and c + 64
     const int lr = 16 * lg + 4 * mw + (lane >> 4), cc = lr & 127;
@@ -1081,51 +1098,52 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   };
   auto math_o = [&](int lp, int lg, const TileO& to) {
     const int col = 8 * (lane & 31);
-    double xv[8];
+    A xv[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) xv[i] = s.attn[col + i];
     const uint32_t tg = tag_of(lp, T_OPART);
-    double v[4];
+    A v[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = dot8d(to.p[j], xv, 0.0);
+    for (int j = 0; j < 4; ++j) v[j] = dot8a(to.p[j], xv, A(0));
     // per half-wave: row pair j = (lane >> 3) & 3 ends in lanes 0, 8, 16, 24 (+32)
-    const double t = rs_sum<4, 4>(v, lane);
+    const A t = rs_sum<4, 4>(v, lane);
     if ((lane & 7) == 0)
       pub_cross(&ws->opart[lp & 1][xcd][32 * lg + 8 * mw + 2 * ((lane >> 3) & 3) + (lane >> 5)], (float)t, tg);
   };
   auto math_gu = [&](int lp, int lg, const TileGU& tgu) {
-    double xv[16];
+    A xv[16];
     load_x16(s.hn, xv);
     const uint32_t tg = tag_of(lp, T_INTER);
-    d2 c[4];
+    using P2 = pair2<A>;
+    P2 c[4];
 #pragma unroll
     for (int r = 0; r < 3; ++r)
-      c[r] = d2{dot8d(tgu.g[2 * r + 1], xv + 8, dot8d(tgu.g[2 * r], xv, 0.0)),
-                dot8d(tgu.u[2 * r + 1], xv + 8, dot8d(tgu.u[2 * r], xv, 0.0))};
-    c[3] = d2{0.0, 0.0};
-    const d2 t = rs_sum<5, 4>(c, lane);   // (gate, up) of row lane >> 4 in lanes 0, 16, 32
+      c[r] = P2{dot8a(tgu.g[2 * r + 1], xv + 8, dot8a(tgu.g[2 * r], xv, A(0))),
+                dot8a(tgu.u[2 * r + 1], xv + 8, dot8a(tgu.u[2 * r], xv, A(0)))};
+    c[3] = P2{A(0), A(0)};
+    const P2 t = rs_sum<5, 4>(c, lane);   // (gate, up) of row lane >> 4 in lanes 0, 16, 32
     const int r = lane >> 4;
     if ((lane & 15) == 0 && r < 3) {
-      const double act = t.a / (1.0 + exp(-t.a)) * t.b;
+      const A act = t.a / (A(1) + exp_a(-t.a)) * t.b;
       pub_local(&ws->inter[xcd][lp & 1][12 * lg + 3 * mw + r], (float)act, tg);
     }
   };
   auto math_down = [&](int lp, int lg, const TileD& td) {
-    double xv[24];
+    A xv[24];
 #pragma unroll
     for (int j = 0; j < 3; ++j)
 #pragma unroll
       for (int i = 0; i < 8; ++i) xv[8 * j + i] = s.inter[8 * ((lane & 15) + 16 * j) + i];
     const uint32_t tg = tag_of(lp, T_DPART);
-    double v[2];
+    A v[2];
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
-      v[g] = 0.0;
+      v[g] = A(0);
 #pragma unroll
-      for (int j = 0; j < 3; ++j) v[g] = dot8d(td.p[3 * g + j], xv + 8 * j, v[g]);
+      for (int j = 0; j < 3; ++j) v[g] = dot8a(td.p[3 * g + j], xv + 8 * j, v[g]);
     }
     // per 16-lane group: row set g = (lane >> 3) & 1 ends in lanes 0 and 8
-    const double t = rs_sum<3, 2>(v, lane);
+    const A t = rs_sum<3, 2>(v, lane);
     if ((lane & 7) == 0)
       pub_cross(&ws->dpart[lp & 1][xcd][32 * lg + 8 * mw + 4 * ((lane >> 3) & 1) + (lane >> 4)], (float)t, tg);
   };
@@ -1141,14 +1159,14 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   auto head_group = [&](int pi, int sub, const TileQKV& tq, float& bv, int& bi) {
     int row0, nrows;
     head_rows(sub, row0, nrows);
-    double xv[16];
+    A xv[16];
     load_x16(s.hb, xv);
     const uint32_t tg = a.tag_base + TAG_HEAD + (uint32_t)pi;
-    double v[4];
+    A v[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      v[r] = r < 3 && r < nrows ? dot8d(tq.p[2 * r + 1], xv + 8, dot8d(tq.p[2 * r], xv, 0.0)) : 0.0;
-    const double t = rs_sum<5, 4>(v, lane);   // row lane >> 4 in lanes 0, 16, 32, 48
+      v[r] = r < 3 && r < nrows ? dot8a(tq.p[2 * r + 1], xv + 8, dot8a(tq.p[2 * r], xv, A(0))) : A(0);
+    const A t = rs_sum<5, 4>(v, lane);   // row lane >> 4 in lanes 0, 16, 32, 48
     const int r = lane >> 4;
     // logits are bf16 values, as the reference's torch.mv over bf16 operands returns them
     // (generator.py:158, :351); ties then go to the lowest id, as torch.argmax

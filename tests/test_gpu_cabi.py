@@ -137,7 +137,9 @@ def test_launch_cp_decode_with_embedding(lib, model):
         worst = max(worst, rel_l2(hid.cpu(), hr), rel_l2(res.cpu(), outs[-1]))
     print(f"launch_cp_decode_with_embedding, 16 steps: worst rel_l2 {worst:.2e}", flush=True)
     assert worst < TOL
-    assert rel_l2(kc[:, :, :16].cpu(), orc.k[:, :, :16]) == 0.0
+    # the code predictor accumulates in f32 (the reference's CP arithmetic) against the f64
+    # oracle: its f32 cache agrees to f32 rounding
+    assert rel_l2(kc[:, :, :16].cpu(), orc.k[:, :, :16]) < TOL
 
 
 # ---- the extended entry points, bound the same way ------------------------------------------
