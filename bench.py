@@ -38,7 +38,7 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch measured with rocprofv3 PMC counters on the same workload
 # (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000 KiB, both factors from a plain 512 MiB device copy);
 # the summary with the commands is profiles/qtts_decode_kernel_frame512_pmc_traffic.md.
-PMC_TRAFFIC = {"cp_frame": 2_786_327_266, "backbone_step": 996_234_657}
+PMC_TRAFFIC = {"cp_frame": 2_784_211_538, "backbone_step": 990_528_542}
 
 
 def backbone_bytes(L: int) -> int:
@@ -322,7 +322,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16 weights, f64 accumulation",
+        "dtype": "bf16 weights; f64 accumulation (backbone), f32 (code predictor)",
         "data": "synthetic (seeded random-init weights, random bf16 KV cache)",
         "config": {"workload": "codec frame at 512 context: backbone 28 layers (L=512) + code predictor "
                                "5 layers x 16 positions, 15 lm-heads; batch 1 (BASELINE configs[2] frame)",

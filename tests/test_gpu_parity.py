@@ -1,8 +1,11 @@
 """GPU parity: the HIP decode kernels against the CPU oracle on the same seeded inputs.
 
-Both sides accumulate in f64 and round to f32 / bf16 at the same storage points, so
-per-step hidden states must agree within rel-L2 <= 1e-5 (the north-star bar against the
-reference's PyTorch path is 1e-2, checked in test_gpu_hf_policy.py), greedy tokens exactly.
+The oracle's kernel policy accumulates in f64 and rounds to f32 / bf16 at the reference's
+storage points. The backbone kernel does the same (f64 sums), so its states agree bit for bit
+in practice; the code-predictor kernel accumulates in f32, as the reference's CP kernel does,
+so its states agree to f32 rounding. Both are held to rel-L2 <= 1e-5 (the north-star bar
+against the reference's PyTorch path is 1e-2, checked in test_gpu_golden.py), and greedy
+tokens must be identical.
 """
 import math
 
