@@ -43,9 +43,13 @@ Precision policies (``policy=``):
 Pinning (see tests/test_oracle_*.py): layer math against transformers ``Qwen3DecoderLayer``
 (fp32 and bf16), interleaved mRoPE against transformers ``Qwen3VLTextRotaryEmbedding``,
 t=h=w reduction to 1D RoPE, GQA against repeated-KV attention, Philox against numpy, sampler
-distribution against softmax by exact enumeration. The in-kernel 2-token CP prefill (positions
-0 and 1 computed by the CP kernel instead of the reference's PyTorch CP prefill,
-generator.py:318-344) follows the kernel policy; it has no reference fixture.
+distribution against softmax by exact enumeration. The frame loop (the 2-token CP prefill
+``[bf16(h), emb_bb[g0]]`` at positions 0 and 1, ``lm_head[g]`` / ``emb[g-1]`` per group, the
+embedding combine plus the text or pad row; generator.py:309-362) against transformers'
+Qwen3-Omni talker ``prepare_inputs_for_generation`` and its code predictor's ``generate``, in the
+``"exact"`` policy (tests/test_oracle_frame_loop.py). The GPU's code predictor accumulates in f32
+(the reference CP kernel's arithmetic) where this policy sums in f64; the two agree to f32
+rounding.
 """
 from __future__ import annotations
 
