@@ -182,39 +182,64 @@ def prefill_figures(bbg, reps: int = 5) -> dict:
     return out
 
 
+def batched_frame_bytes(lengths) -> int:
+    """Algorithmic bytes of one weight-shared batch frame: every weight once for all streams, each
+    stream's own KV (backbone at its length, code predictor at L = 2..16)."""
+    n = len(lengths)
+    bb = W_BB + sum(KV_BB * L + KV_BB for L in lengths)
+    cp = sum(W_CP + n * (KV_CP * L + KV_CP) for L in range(2, 17))
+    return bb + cp
+
+
 def batched_c4(pkg, sd, frames: int = 10) -> dict:
     """Config 4: 8 independent streams with ragged attended lengths in [128, 1024]; one frame =
-    per stream one backbone step (head + greedy g0) and one code-predictor frame."""
+    per stream one backbone step (head + greedy g0) and one code-predictor frame. Both multi-stream
+    kernels are timed: the weight-shared one (the figure) and the one-stream-per-XCD one."""
     import torch
     g = torch.Generator().manual_seed(1238)
     lengths = [int(x) for x in torch.randint(128, 1025, (8,), generator=g)]
-    dec = pkg.BatchedTTSDecoder(sd, 8, max_seq_len=max(lengths) + frames + 8)
-    gd = torch.Generator(device="cuda").manual_seed(7)
-    for s, L in enumerate(lengths):
-        k = torch.randn(28, 8, L - 1, 128, generator=gd, device="cuda").to(torch.bfloat16)
-        v = torch.randn(28, 8, L - 1, 128, generator=gd, device="cuda").to(torch.bfloat16)
-        dec.set_kv_cache(s, k, v)
-    i32 = dict(dtype=torch.int32, device="cuda")
-    g0 = torch.zeros(8, **i32)
-    toks = torch.zeros(8, 16, **i32)
-    comb = torch.randn(8, 1024, generator=gd, device="cuda").to(torch.bfloat16)
-    text = torch.randn(8, 1024, generator=gd, device="cuda").to(torch.bfloat16)
+    out = {"streams": 8, "lengths": lengths, "frames": frames}
+    for mode in ("shared", "per_xcd"):
+        dec = pkg.BatchedTTSDecoder(sd, 8, max_seq_len=max(lengths) + 2 * frames + 8, mode=mode)
+        gd = torch.Generator(device="cuda").manual_seed(7)
+        for s, L in enumerate(lengths):
+            k = torch.randn(28, 8, L - 1, 128, generator=gd, device="cuda").to(torch.bfloat16)
+            v = torch.randn(28, 8, L - 1, 128, generator=gd, device="cuda").to(torch.bfloat16)
+            dec.set_kv_cache(s, k, v)
+        i32 = dict(dtype=torch.int32, device="cuda")
+        g0 = torch.zeros(8, **i32)
+        toks = torch.zeros(8, 16, **i32)
+        comb = torch.randn(8, 1024, generator=gd, device="cuda").to(torch.bfloat16)
+        text = torch.randn(8, 1024, generator=gd, device="cuda").to(torch.bfloat16)
 
-    def frame(i):
-        hidden = dec.step_select(comb, g0, -1, frame_step=i)
-        dec.cp_frames(hidden, g0, text, toks, comb, frame_step=i)
+        def frame(i):
+            hidden = dec.step_select(comb, g0, -1, frame_step=i)
+            dec.cp_frames(hidden, g0, text, toks, comb, frame_step=i)
 
-    frame(0)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(frames):
-        frame(1 + i)
-    torch.cuda.synchronize()
-    el = time.perf_counter() - t0
-    dec.check_error()
-    return {"streams": 8, "lengths": lengths, "frames": frames,
-            "frames_per_s_total": round(8 * frames / el, 2), "frames_per_s_per_stream": round(frames / el, 2),
-            "note": "one backbone launch and one code-predictor launch for all streams per frame, stream s on XCD s"}
+        frame(0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(frames):
+            frame(1 + i)
+        torch.cuda.synchronize()
+        el = time.perf_counter() - t0
+        dec.check_error()
+        if mode == "shared":
+            # the streams attend lengths[s] + 1 .. + frames over the timed frames
+            mid = [L + 1 + frames // 2 for L in lengths]
+            nbytes = batched_frame_bytes(mid)
+            gbs = nbytes * frames / el / 1e9
+            out.update({"frames_per_s_total": round(8 * frames / el, 2), "frames_per_s_per_stream": round(frames / el, 2),
+                        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                     "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_batch_frame": nbytes,
+                                     "note": "weights counted once per batch frame (both launches), KV per stream"}})
+        else:
+            out["per_xcd_frames_per_s_total"] = round(8 * frames / el, 2)
+        del dec
+        torch.cuda.synchronize()
+    out["note"] = ("weight-shared: one backbone launch and one code-predictor launch for all 8 streams per frame, "
+                   "every weight read once (bf16 MFMA); per_xcd: stream s on XCD s, each XCD reading all weights")
+    return out
 
 
 def main():

@@ -291,6 +291,34 @@ hipError_t qtts_cp_frame_streams(
     const void* text_rows, int* out_tokens, void* out_combined,
     int eos_id, int* done, const QttsSampling* sampling, int frame_step, hipStream_t stream);
 
+/* Weight-shared decode of several streams (config 4); no counterpart in the reference, whose
+ * decode is batch 1 (fused_decode_tts.cu:728-831, fused_decode_code_predictor.cu:565-668).
+ * Same arguments as qtts_backbone_step_streams / qtts_cp_frame_streams, but the n_streams (1..8)
+ * streams share every weight read: each workgroup applies its weight tile to all streams at once
+ * on bf16 MFMA, with each stream's f32 input split exactly into three bf16 pieces and f32 sums
+ * (the reference's f32 GEMV accuracy; results agree with the batch-1 kernels to rounding, not bit
+ * for bit). One workspace of qtts_shared_workspace_bytes() serves all streams of a launch
+ * (256-byte aligned; zero-filled by its first launch, or after qtts_workspace_release(ws, 1)).
+ * Backbone: each stream at its own position and length; codec_head rows vocab / 256 <= 16.
+ * Code predictor: n_groups + 1 <= 16, cp_vocab / 256 <= 16. qtts_shared_workspace_check reads
+ * and clears the workspace's wait-timeout error word (synchronises the stream). */
+size_t qtts_shared_workspace_bytes(void);
+hipError_t qtts_shared_workspace_check(void* workspace, unsigned int* error_code, hipStream_t stream);
+hipError_t qtts_backbone_step_shared(
+    int n_streams, void* workspace, const TTSLayerWeights* layer_weights, int num_layers,
+    const void* final_norm_weight, const void* cos_table, const void* sin_table, int max_seq_len,
+    const QttsBackboneStream* streams, const void* codec_head, int vocab, int mask_tail,
+    float repetition_penalty, int eos_id, int suppress_eos, const QttsSampling* sampling,
+    int frame_step, hipStream_t stream);
+hipError_t qtts_cp_frame_shared(
+    int n_streams, void* workspace, const CPLayerWeights* layer_weights, int num_layers,
+    const void* final_norm_weight, const void* cos_table, const void* sin_table,
+    void* k_caches, void* v_caches, int max_seq_len,
+    const float* bb_hidden, const int* g0, const void* bb_embedding,
+    const void* const* lm_heads, const void* const* cp_embeddings, int n_groups, int cp_vocab,
+    const void* text_rows, int* out_tokens, void* out_combined,
+    int eos_id, int* done, const QttsSampling* sampling, int frame_step, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -2,11 +2,16 @@
 
 Each stream keeps its own backbone KV cache and position; all streams share one copy of the
 weights and one code-predictor decoder. A frame of the batch is two launches per 8 streams: the
-backbone steps (codec head + selection) and the code-predictor frames. In both, stream s runs
-on XCD s alone, its 32 workgroups acting as the 8 virtual XCDs of the batch-1 decomposition,
-so every exchange stays in that XCD's L2. Everything is queued on
-the current stream with no host sync, and every stream's results are bit-identical to its
-batch-1 results.
+backbone steps (codec head + selection) and the code-predictor frames, queued on the current
+stream with no host sync. Two kernels serve them:
+
+* ``mode="shared"`` (default): the weight-shared kernels. Every weight byte is read once per
+  launch for all streams: each workgroup applies its weight tile to the 8 streams' inputs at once
+  on bf16 MFMA (each f32 input split exactly into three bf16 pieces, f32 sums), and wave s of
+  every workgroup does stream s's vector work. Results agree with batch 1 to f32 rounding.
+* ``mode="per_xcd"``: stream s runs on XCD s alone, its 32 workgroups acting as the 8 virtual
+  XCDs of the batch-1 decomposition (every exchange in that XCD's L2), and every stream's results
+  are bit-identical to its batch-1 results; each XCD reads the whole weight set for its stream.
 
 The reference has no batched decode (its megakernels are batch 1, fused_decode_tts.cu:728-831).
 """
@@ -23,12 +28,16 @@ from .megakernel_code_predictor import CodePredictorMegakernelGenerator
 class BatchedTTSDecoder:
     """``n_streams`` backbone decoders over shared weights plus one code predictor."""
 
-    MAX_PER_LAUNCH = 8   # streams per launch: one per XCD
+    MAX_PER_LAUNCH = 8   # streams per launch (one per wave, or one per XCD)
+    MODES = ("shared", "per_xcd")
 
     def __init__(self, model, n_streams: int, max_seq_len: int = 4096, cp_max_seq_len: int = 32,
-                 device="cuda"):
+                 device="cuda", mode: str = "shared"):
         if n_streams < 1:
             raise ValueError("n_streams must be >= 1")
+        if mode not in self.MODES:
+            raise ValueError(f"mode={mode!r}: one of {self.MODES}")
+        self.mode = mode
         first = TTSMegakernelGenerator(model=model, max_seq_len=max_seq_len, device=device)
         self.streams: List[TTSMegakernelGenerator] = [first] + [
             TTSMegakernelGenerator(max_seq_len=max_seq_len, device=device, shared_weights=first.weights)
@@ -55,8 +64,7 @@ class BatchedTTSDecoder:
         """One backbone step per stream at its own position, codec head, suppress mask (ids
         [V-1024, V) except EOS), optional repetition penalty over ``history[s][:n_history[s]]``
         and selection of each stream's group-0 token into ``tokens_out[s]`` (device int32), with
-        sampling key ``seed + s``. Up to 8 streams share one launch, stream s on XCD s
-        (``decode_steps_streams``). A stream whose ``skip[s]`` (device int32 [n]) is nonzero computes
+        sampling key ``seed + s``. Up to 8 streams share one launch (``decode_steps_streams``). A stream whose ``skip[s]`` (device int32 [n]) is nonzero computes
         nothing and leaves its outputs as they were. Returns the final-norm hiddens (f32
         [n_streams, 1024], device)."""
         if skip is not None and (skip.dtype != torch.int32 or skip.numel() != self.n_streams or not skip.is_contiguous()):
@@ -76,7 +84,7 @@ class BatchedTTSDecoder:
                                       hidden[b:e], hist[b:e] if hist is not None else None, nh[b:e],
                                       float(repetition_penalty), int(eos_id), bool(suppress_eos), bool(do_sample),
                                       float(temperature), int(top_k), float(top_p), int(seed) + b, int(frame_step),
-                                      skip[b:e] if skip is not None else None)
+                                      skip[b:e] if skip is not None else None, self.mode == "shared")
         return hidden
 
     def cp_frames(self, hidden: torch.Tensor, g0: torch.Tensor, text_rows: Optional[torch.Tensor],
@@ -87,7 +95,7 @@ class BatchedTTSDecoder:
         group ids, ``combined_out[s]`` (bf16 [1024]) the embedding sum plus ``text_rows[s]``.
         A stream whose g0 is ``eos_id`` writes nothing and sets ``done[s]`` (device int32 [n],
         kept by the caller across frames; a fresh one when None). Up to 8 streams share one
-        launch, stream s on XCD s (``frames_streams``); stream s draws with key ``seed + s``."""
+        launch (``frames_streams``); stream s draws with key ``seed + s``."""
         n = self.n_streams
         if done is None:
             done = torch.zeros(n, dtype=torch.int32, device=self.device)
@@ -100,7 +108,8 @@ class BatchedTTSDecoder:
             e = min(n, b + self.MAX_PER_LAUNCH)
             self.cp.decoder.frames_streams(hid[b:e], g[b:e], tr[b:e] if tr is not None else None, tokens_out[b:e],
                                            combined_out[b:e], int(eos_id), done[b:e], bool(do_sample),
-                                           float(temperature), int(top_k), 1.0, int(seed) + b, int(frame_step))
+                                           float(temperature), int(top_k), 1.0, int(seed) + b, int(frame_step),
+                                           self.mode == "shared")
 
     def generate(self, talker_input_embeds: Sequence[torch.Tensor], trailing_text_hidden: Sequence[torch.Tensor],
                  tts_pad_embed: torch.Tensor, eos_token_id: int, max_tokens: int = 500, do_sample: bool = False,
@@ -113,8 +122,9 @@ class BatchedTTSDecoder:
         (ragged lengths), a shared pad row. Each stream is prefilled on its own, then every frame
         is one code-predictor launch and one backbone launch for all streams, queued with no host
         sync; the host checks the EOS flags every ``sync_every`` frames and stops when every
-        stream has ended. Stream s samples with key ``seed + s`` and returns exactly what a
-        single-stream ``generate(..., seed=seed + s)`` returns for its inputs."""
+        stream has ended. Stream s samples with key ``seed + s``; in ``per_xcd`` mode it returns
+        exactly what a single-stream ``generate(..., seed=seed + s)`` returns for its inputs, in
+        ``shared`` mode the same up to choices that f32 rounding can tip (near-ties)."""
         n = self.n_streams
         if len(talker_input_embeds) != n or len(trailing_text_hidden) != n:
             raise ValueError(f"one prompt and one trailing text per stream ({n}) expected")
@@ -171,7 +181,7 @@ class BatchedTTSDecoder:
             hidden = self.step_select(combined, g0, int(eos_token_id), hist, [step + 1] * n,
                                       float(repetition_penalty), step + 1 < min_new_tokens, bool(do_sample),
                                       float(temperature), int(top_k), float(top_p), int(seed), step + 1,
-                                      skip=done)   # streams that reached EOS leave their XCD idle
+                                      skip=done)   # streams that reached EOS compute nothing
             if (step + 1) % sync_every == 0 and bool(done.all()):
                 break
         rec = records.cpu()

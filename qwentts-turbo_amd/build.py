@@ -50,7 +50,8 @@ def build_library(verbose: bool = False) -> Path:
     LIB.parent.mkdir(exist_ok=True)
     tmp = LIB.with_suffix(".so.tmp")
     _run([ROCM / "bin" / "hipcc", *HIP_FLAGS, "-shared", f"-I{ROOT / 'include'}", f"-I{PKG / 'csrc'}",
-          PKG / "csrc" / "qtts_decode.hip", PKG / "csrc" / "qtts_prefill.hip", "-o", tmp], verbose)
+          PKG / "csrc" / "qtts_decode.hip", PKG / "csrc" / "qtts_prefill.hip", PKG / "csrc" / "qtts_shared.hip",
+          "-o", tmp], verbose)
     os.replace(tmp, LIB)
     return LIB
 

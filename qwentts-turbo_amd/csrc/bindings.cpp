@@ -82,6 +82,19 @@ QttsSampling sampling(bool do_sample, double temperature, int64_t top_k, double 
   return s;
 }
 
+// the weight-shared launches' workspace, allocated on first use (its first launch zero-fills it)
+void ensure_shared_ws(torch::Tensor& ws, const torch::Device& dev) {
+  if (ws.defined()) return;
+  ws = torch::empty({(int64_t)qtts_shared_workspace_bytes()}, torch::dtype(torch::kUInt8).device(dev));
+  hip_check(qtts_workspace_init(ws.data_ptr(), dev.index()), "qtts_workspace_init");
+}
+void check_shared_error(const torch::Tensor& ws) {
+  if (!ws.defined()) return;
+  unsigned int code = 0;
+  hip_check(qtts_shared_workspace_check(ws.data_ptr(), &code, cur_stream()), "qtts_shared_workspace_check");
+  TORCH_CHECK(code == 0, "weight-shared decode kernel reported a device-side wait timeout (error word ", code, ")");
+}
+
 void check_device_error(const torch::Tensor& ws) {
   unsigned int code = 0;
   hip_check(qtts_workspace_check(ws.data_ptr(), &code, cur_stream()), "qtts_workspace_check");
@@ -127,6 +140,7 @@ class MegakernelTTSDecoder {
   ~MegakernelTTSDecoder() {
     (void)qtts_workspace_release(ws_.data_ptr(), 1);
     if (ws_streams_.defined()) (void)qtts_workspace_release(ws_streams_.data_ptr(), kMaxStreams);
+    if (ws_shared_.defined()) (void)qtts_workspace_release(ws_shared_.data_ptr(), 1);
   }
   MegakernelTTSDecoder(const MegakernelTTSDecoder&) = delete;
   MegakernelTTSDecoder& operator=(const MegakernelTTSDecoder&) = delete;
@@ -245,7 +259,7 @@ class MegakernelTTSDecoder {
                             torch::Tensor hidden_out, c10::optional<torch::Tensor> history, std::vector<int64_t> n_history,
                             double repetition_penalty, int64_t eos_id, bool suppress_eos, bool do_sample,
                             double temperature, int64_t top_k, double top_p, int64_t seed, int64_t frame_step,
-                            c10::optional<torch::Tensor> skip) {
+                            c10::optional<torch::Tensor> skip, bool shared) {
     const int64_t n = (int64_t)decs.size();
     TORCH_CHECK(n >= 1 && n <= kMaxStreams, "decode_steps_streams takes 1..", kMaxStreams, " decoders, got ", n);
     c10::hip::HIPGuardMasqueradingAsCUDA guard(dev_);
@@ -298,11 +312,22 @@ class MegakernelTTSDecoder {
       q.seed = (unsigned long long)(seed + st);
       q.skip_if = skip.has_value() ? skip->data_ptr<int>() + st : nullptr;
     }
+    QttsSampling samp = sampling(do_sample, temperature, top_k, top_p, seed);
+    if (shared) {
+      ensure_shared_ws(ws_shared_, dev_);
+      hip_check(qtts_backbone_step_shared((int)n, ws_shared_.data_ptr(), reinterpret_cast<const TTSLayerWeights*>(d_layer_weights_.data_ptr()),
+                                          num_layers_, final_norm_weight_.data_ptr(), cos_table_.data_ptr(), sin_table_.data_ptr(),
+                                          max_seq_len_, io.data(), codec_head_weight_.data_ptr(), (int)codec_head_weight_.size(0),
+                                          1, (float)repetition_penalty, (int)eos_id, suppress_eos ? 1 : 0, &samp, (int)frame_step,
+                                          cur_stream()),
+                "qtts_backbone_step_shared");
+      for (auto* d : decs) d->position_++;
+      return;
+    }
     if (!ws_streams_.defined()) {
       ws_streams_ = torch::zeros({(int64_t)(kMaxStreams * qtts_workspace_bytes())}, torch::dtype(torch::kUInt8).device(dev_));
       hip_check(qtts_workspace_init(ws_streams_.data_ptr(), dev_.index()), "qtts_workspace_init");
     }
-    QttsSampling samp = sampling(do_sample, temperature, top_k, top_p, seed);
     hip_check(qtts_backbone_step_streams((int)n, ws_streams_.data_ptr(), reinterpret_cast<const TTSLayerWeights*>(d_layer_weights_.data_ptr()),
                                          num_layers_, final_norm_weight_.data_ptr(), cos_table_.data_ptr(), sin_table_.data_ptr(),
                                          max_seq_len_, io.data(), codec_head_weight_.data_ptr(), (int)codec_head_weight_.size(0),
@@ -313,6 +338,7 @@ class MegakernelTTSDecoder {
   }
   // the wait-timeout error words of the decode_steps_streams() workspaces
   void check_error_streams() const {
+    check_shared_error(ws_shared_);
     if (!ws_streams_.defined()) return;
     for (int st = 0; st < kMaxStreams; ++st) {
       unsigned int code = 0;
@@ -376,6 +402,7 @@ class MegakernelTTSDecoder {
   std::vector<torch::Tensor> layer_weights_tensors_;
   torch::Tensor k_cache_, v_cache_, hidden_buffer_, g_normalized_, logits_, token_, ws_;
   torch::Tensor ws_streams_;   // decode_steps_streams(): per-stream workspaces
+  torch::Tensor ws_shared_;    // decode_steps_streams(shared=True): the weight-shared launches' workspace
   torch::Tensor pf_ws_;        // prefill(): activations and split-K partials (grown on demand)
 };
 
@@ -409,6 +436,7 @@ class MegakernelCodePredictorDecoder {
   ~MegakernelCodePredictorDecoder() {
     (void)qtts_workspace_release(ws_.data_ptr(), 1);
     if (ws_streams_.defined()) (void)qtts_workspace_release(ws_streams_.data_ptr(), kMaxStreams);
+    if (ws_shared_.defined()) (void)qtts_workspace_release(ws_shared_.data_ptr(), 1);
   }
   MegakernelCodePredictorDecoder(const MegakernelCodePredictorDecoder&) = delete;
   MegakernelCodePredictorDecoder& operator=(const MegakernelCodePredictorDecoder&) = delete;
@@ -492,7 +520,8 @@ class MegakernelCodePredictorDecoder {
   // workspace and KV cache, allocated on first use); row s of each argument belongs to stream s.
   void frames_streams(torch::Tensor bb_hidden, torch::Tensor g0, c10::optional<torch::Tensor> text_rows,
                       torch::Tensor out_tokens, torch::Tensor out_combined, int64_t eos_id, torch::Tensor done,
-                      bool do_sample, double temperature, int64_t top_k, double top_p, int64_t seed, int64_t frame_step) {
+                      bool do_sample, double temperature, int64_t top_k, double top_p, int64_t seed, int64_t frame_step,
+                      bool shared) {
     TORCH_CHECK(!heads_.empty(), "call set_heads() before frames_streams()");
     c10::hip::HIPGuardMasqueradingAsCUDA guard(dev_);
     const int64_t n = bb_hidden.size(0);
@@ -515,14 +544,28 @@ class MegakernelCodePredictorDecoder {
                   "text_rows must be contiguous bf16 [n, 1024]");
       tr = text_rows->data_ptr();
     }
-    if (!ws_streams_.defined()) {
-      ws_streams_ = torch::zeros({(int64_t)(kMaxStreams * qtts_workspace_bytes())}, torch::dtype(torch::kUInt8).device(dev_));
-      hip_check(qtts_workspace_init(ws_streams_.data_ptr(), dev_.index()), "qtts_workspace_init");
+    if (!k_streams_.defined()) {
       auto f32 = torch::dtype(torch::kFloat32).device(dev_);
       k_streams_ = torch::zeros({kMaxStreams, num_layers_, kKVHeads, max_seq_len_, kHeadDim}, f32);
       v_streams_ = torch::zeros({kMaxStreams, num_layers_, kKVHeads, max_seq_len_, kHeadDim}, f32);
     }
     QttsSampling smp = sampling(do_sample, temperature, top_k, top_p, seed);
+    if (shared) {
+      ensure_shared_ws(ws_shared_, dev_);
+      hip_check(qtts_cp_frame_shared((int)n, ws_shared_.data_ptr(), reinterpret_cast<const CPLayerWeights*>(d_layer_weights_.data_ptr()),
+                                     num_layers_, final_norm_weight_.data_ptr(), cos_table_.data_ptr(), sin_table_.data_ptr(),
+                                     k_streams_.data_ptr(), v_streams_.data_ptr(), max_seq_len_, bb_hidden.data_ptr<float>(),
+                                     g0.data_ptr<int>(), bb_emb_.data_ptr(), reinterpret_cast<const void* const*>(d_heads_.data_ptr()),
+                                     reinterpret_cast<const void* const*>(d_embs_.data_ptr()), (int)groups, cp_vocab_, tr,
+                                     out_tokens.data_ptr<int>(), out_combined.data_ptr(), (int)eos_id, done.data_ptr<int>(), &smp,
+                                     (int)frame_step, cur_stream()),
+                "qtts_cp_frame_shared");
+      return;
+    }
+    if (!ws_streams_.defined()) {
+      ws_streams_ = torch::zeros({(int64_t)(kMaxStreams * qtts_workspace_bytes())}, torch::dtype(torch::kUInt8).device(dev_));
+      hip_check(qtts_workspace_init(ws_streams_.data_ptr(), dev_.index()), "qtts_workspace_init");
+    }
     hip_check(qtts_cp_frame_streams((int)n, ws_streams_.data_ptr(), reinterpret_cast<const CPLayerWeights*>(d_layer_weights_.data_ptr()),
                                     num_layers_, final_norm_weight_.data_ptr(), cos_table_.data_ptr(), sin_table_.data_ptr(),
                                     k_streams_.data_ptr(), v_streams_.data_ptr(), max_seq_len_, bb_hidden.data_ptr<float>(),
@@ -533,6 +576,7 @@ class MegakernelCodePredictorDecoder {
               "qtts_cp_frame_streams");
   }
   void check_error_streams() const {
+    check_shared_error(ws_shared_);
     if (!ws_streams_.defined()) return;
     for (int st = 0; st < kMaxStreams; ++st) {
       unsigned int code = 0;
@@ -577,6 +621,7 @@ class MegakernelCodePredictorDecoder {
   torch::Tensor bb_emb_, d_heads_, d_embs_;
   torch::Tensor k_cache_, v_cache_, hidden_buffer_, g_normalized_, ws_;
   torch::Tensor ws_streams_, k_streams_, v_streams_;   // frames_streams(): per-stream workspaces and KV caches
+  torch::Tensor ws_shared_;                            // frames_streams(shared=True): the weight-shared launches' workspace
 };
 
 }  // namespace
@@ -621,7 +666,7 @@ PYBIND11_MODULE(_qwentts_amd_C, m) {
            py::arg("out_tokens"), py::arg("hidden_out"), py::arg("history"), py::arg("n_history"),
            py::arg("repetition_penalty"), py::arg("eos_id"), py::arg("suppress_eos"), py::arg("do_sample"),
            py::arg("temperature"), py::arg("top_k"), py::arg("top_p"), py::arg("seed"), py::arg("frame_step"),
-           py::arg("skip") = py::none())
+           py::arg("skip") = py::none(), py::arg("shared") = false)
       .def("check_error_streams", &MegakernelTTSDecoder::check_error_streams)
       .def("check_error", &MegakernelTTSDecoder::check_error);
   py::class_<MegakernelCodePredictorDecoder>(m, "MegakernelCodePredictorDecoder")
@@ -631,7 +676,7 @@ PYBIND11_MODULE(_qwentts_amd_C, m) {
       .def("frames_streams", &MegakernelCodePredictorDecoder::frames_streams, py::arg("bb_hidden"), py::arg("g0"),
            py::arg("text_rows"), py::arg("out_tokens"), py::arg("out_combined"), py::arg("eos_id"), py::arg("done"),
            py::arg("do_sample"), py::arg("temperature"), py::arg("top_k"), py::arg("top_p"), py::arg("seed"),
-           py::arg("frame_step"))
+           py::arg("frame_step"), py::arg("shared") = false)
       .def("check_error_streams", &MegakernelCodePredictorDecoder::check_error_streams)
       .def("frame", &MegakernelCodePredictorDecoder::frame, py::arg("bb_hidden"), py::arg("g0"), py::arg("text_row"),
            py::arg("out_tokens"), py::arg("out_combined"), py::arg("eos_id"), py::arg("done"), py::arg("do_sample"),

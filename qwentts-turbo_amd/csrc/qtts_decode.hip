@@ -30,6 +30,8 @@
 #include <unordered_map>
 #include <utility>
 #include "qtts_common.h"
+#include "qtts_host.h"
+#include "qtts_poll.h"
 #include "qtts_select.h"
 #include "qwentts_amd.h"
 
@@ -305,105 +307,6 @@ __device__ __forceinline__ void unpack8(const TileKV<BB>& t, bool key, int jj, f
   }
 }
 
-// ---------------------------------------------------------------------------------------
-// Poller helpers
-// ---------------------------------------------------------------------------------------
-struct Poll {
-  __amdgpu_buffer_rsrc_t rs;   // covers the whole workspace
-  const Workspace* base;
-  ErrCtl ec;
-};
-
-__device__ __forceinline__ uint32_t ws_off(const Poll& P, const void* p) {
-  return (uint32_t)(reinterpret_cast<const char*>(p) - reinterpret_cast<const char*>(P.base));
-}
-
-// Poll npair 16-byte pairs (two tagged slots each) into registers: pair k of this lane, index
-// i = lane + 64 k (i < npair), lives at byte offset off(i) of the workspace and lands in
-// out[2 k], out[2 k + 1]. Returns false on timeout (error word set).
-template <int MAXP, typename OffF>
-__device__ bool poll_regs(const Poll& P, int npair, uint32_t tag, float (&out)[2 * MAXP], OffF off) {
-  const int lane = opaque((int)threadIdx.x & 63);   // keeps slot offsets from being hoisted and spilled
-  uint32_t valid = 0;
-#pragma unroll
-  for (int k = 0; k < MAXP; ++k)
-    if (lane + 64 * k < npair) valid |= 1u << k;
-  uint32_t pending = valid;
-  uint32_t spins = 0;
-  auto check = [&](const u32x4 (&v)[MAXP]) {
-#pragma unroll
-    for (int k = 0; k < MAXP; ++k) {
-      if ((pending & (1u << k)) && v[k].y == tag && v[k].w == tag) {
-        out[2 * k] = __uint_as_float(v[k].x);
-        out[2 * k + 1] = __uint_as_float(v[k].z);
-        pending &= ~(1u << k);
-      }
-    }
-    return __ballot(pending != 0u) == 0ull;
-  };
-  auto timed_out = [&]() {
-    ++spins;
-    if ((spins & 63u) == 0u && (spins > P.ec.spin_cap || err_set(P.ec))) {
-      if (lane == 0) atomicOr(P.ec.err, 1u);
-      return true;
-    }
-    return false;
-  };
-  if constexpr (MAXP <= 17) {
-    // NBAT batches in flight: the next batch is issued before the oldest one is checked, so a
-    // slot is seen about 1 / NBAT of a load latency after it lands instead of a whole one.
-    // Every batch has the same loads (lanes without a slot re-read slot 0), so the wait for
-    // the oldest batch is an exact vmcnt.
-    constexpr int NBAT = MAXP <= 2 ? 4 : (MAXP <= 4 ? 3 : 2);
-    u32x4 vb[NBAT][MAXP];
-    auto issue = [&](u32x4 (&v)[MAXP]) {
-#pragma unroll
-      for (int k = 0; k < MAXP; ++k)
-        v[k] = __builtin_amdgcn_raw_buffer_load_b128(P.rs, off((valid >> k) & 1u ? lane + 64 * k : 0), 0, 16);
-    };
-#pragma unroll
-    for (int b = 0; b < NBAT - 1; ++b) issue(vb[b]);
-    for (;;) {
-#pragma unroll
-      for (int b = 0; b < NBAT; ++b) {
-        issue(vb[(b + NBAT - 1) % NBAT]);
-        if (check(vb[b])) return true;
-      }
-      if (timed_out()) return false;
-    }
-  } else {
-    for (;;) {
-      u32x4 v[MAXP];
-#pragma unroll
-      for (int k = 0; k < MAXP; ++k)
-        if (pending & (1u << k)) v[k] = __builtin_amdgcn_raw_buffer_load_b128(P.rs, off(lane + 64 * k), 0, 16);
-      if (check(v)) return true;
-      if (timed_out()) return false;
-    }
-  }
-}
-// Poll npair pairs into LDS: pair i to dst[2 i], dst[2 i + 1].
-template <int MAXP, typename OffF>
-__device__ bool poll_pairs(const Poll& P, int npair, uint32_t tag, float* dst, OffF off) {
-  float v[2 * MAXP];
-  const bool ok = poll_regs<MAXP>(P, npair, tag, v, off);
-  const int lane = opaque((int)threadIdx.x & 63);
-#pragma unroll
-  for (int k = 0; k < MAXP; ++k)
-    if (lane + 64 * k < npair) *reinterpret_cast<float2*>(dst + 2 * (lane + 64 * k)) = make_float2(v[2 * k], v[2 * k + 1]);
-  return ok;
-}
-// contiguous n slots (n even) starting at p
-template <int MAXP>
-__device__ __forceinline__ bool poll_vec(const Poll& P, const uint64_t* p, int n, uint32_t tag, float* dst) {
-  const uint32_t o = ws_off(P, p);
-  return poll_pairs<MAXP>(P, n >> 1, tag, dst, [o](int i) { return o + 16u * (uint32_t)i; });
-}
-// contiguous 1024 slots into registers: this lane gets elements 2 (lane + 64 k) + {0, 1}
-__device__ __forceinline__ bool poll_vec_regs(const Poll& P, const uint64_t* p, uint32_t tag, float (&out)[16]) {
-  const uint32_t o = ws_off(P, p);
-  return poll_regs<8>(P, HID / 2, tag, out, [o](int i) { return o + 16u * (uint32_t)i; });
-}
 // Sum of the 8 XCD partials of rows r0 + 2 (lane & 15) + {0, 1}: lane group g = lane >> 4 polls
 // XCDs 2 g and 2 g + 1 and adds them; two exchanges (lane ^ 16, lane ^ 32) complete the sum as
 // ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7)), bit-identical in every lane and workgroup.
@@ -447,15 +350,6 @@ __device__ __forceinline__ bool poll_sum8_rows(const Poll& P, const uint64_t (*p
 // RMSNorm epsilon: the f32 constant 1e-6f of the reference, used in f64 arithmetic.
 constexpr double EPSD = (double)1e-6f;
 
-
-// Workgroup barrier: makes LDS data one wave wrote visible to the others. Used at every step
-// boundary and inside the attention steps; both roles reach it the same number of times (the
-// poller wave joins the math waves' internal barriers of a step before its own step work).
-__device__ __forceinline__ void step_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-}
 
 // ---------------------------------------------------------------------------------------
 // The kernel
@@ -1643,7 +1537,7 @@ namespace {
 using qtts::KArgs;
 using qtts::Workspace;
 
-constexpr uint32_t kSpinCap = 1u << 22;          // ~4 s of polling before a wait is declared failed
+using qtts_host::kSpinCap;
 constexpr uint32_t kSeqLimit = (1u << 20) - 1u;  // tag = (sequence << 12) | (layer pass * 8 + slot)
 
 struct DeviceCheck {
@@ -1736,28 +1630,47 @@ hipError_t check_device_locked(int device, DeviceCheck& dc) {
   return hipSuccess;
 }
 
-// Tag base of a launch over the n consecutive workspaces at ws. The launch takes the largest
-// sequence of its workspaces and moves all n past it, so its tags differ from every tag they
-// hold. When one of them is new, or the sequence space is used up, exactly these n workspaces
-// are zero-filled (a fill kernel on the launch stream) and the sequence restarts at 1.
+// Tag base of a launch over the n consecutive workspaces of `bytes` each at ws. The launch takes
+// the largest sequence of its workspaces and moves all n past it, so its tags differ from every
+// tag they hold. When one of them is new, or the sequence space is used up, exactly these n
+// workspaces are zero-filled (a fill kernel on the launch stream) and the sequence restarts at 1.
 // Called with g_mu held.
-uint32_t next_tag_base(void* ws, int n, hipStream_t stream, hipError_t* err) {
+uint32_t next_tag_base(void* ws, int n, size_t bytes, hipStream_t stream, hipError_t* err) {
   uint32_t seq = 0;
   bool fresh = false;
   for (int i = 0; i < n; ++i) {
-    const auto it = g_seq.find(reinterpret_cast<Workspace*>(ws) + i);
+    const auto it = g_seq.find(reinterpret_cast<char*>(ws) + (size_t)i * bytes);
     if (it == g_seq.end()) fresh = true;
     else seq = it->second > seq ? it->second : seq;
   }
   *err = hipSuccess;
   if (fresh || seq == 0 || seq >= kSeqLimit) {
     hipLaunchKernelGGL(zero_kernel, dim3(256), dim3(256), 0, stream, reinterpret_cast<uint4*>(ws),
-                       (size_t)n * sizeof(Workspace) / 16);
+                       (size_t)n * bytes / 16);
     *err = hipGetLastError();
     seq = 1;
   }
-  for (int i = 0; i < n; ++i) g_seq[reinterpret_cast<Workspace*>(ws) + i] = seq + 1;
+  for (int i = 0; i < n; ++i) g_seq[reinterpret_cast<char*>(ws) + (size_t)i * bytes] = seq + 1;
   return seq << 12;
+}
+
+// Ordered launch of a persistent kernel: a launch on another stream than the library's previous
+// one on this device first waits for it. Called with the device checked.
+hipError_t ordered_launch(int dev, const void* fn, int threads, void* kargs, uint32_t* tag_base, void* ws, int n_ws,
+                          size_t ws_bytes, hipStream_t stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  DeviceCheck& dc = g_dev[dev];
+  hipError_t e = hipSuccess;
+  if (dc.has_last && dc.last_stream != stream && (e = hipStreamWaitEvent(stream, dc.last, 0)) != hipSuccess) return e;
+  hipError_t ze = hipSuccess;
+  *tag_base = next_tag_base(ws, n_ws, ws_bytes, stream, &ze);
+  if (ze != hipSuccess) return ze;
+  void* args[] = {kargs};
+  if ((e = hipLaunchKernel(fn, dim3(qtts::NWG), dim3(threads), args, 0, stream)) != hipSuccess) return e;
+  if ((e = hipEventRecord(dc.last, stream)) != hipSuccess) return e;
+  dc.last_stream = stream;
+  dc.has_last = true;
+  return hipSuccess;
 }
 
 // xl: one stream per XCD, n_streams workspaces of one block starting at a.io[0].ws
@@ -1768,22 +1681,11 @@ hipError_t launch(bool bb, KArgs& a, hipStream_t stream, bool xl = false, int n_
   if ((e = check_device(dev)) != hipSuccess) return e;
   if (a.num_layers < 1 || a.n_pos < 1 || a.num_layers * a.n_pos > qtts::MAX_LAYER_PASSES) return hipErrorInvalidValue;
   if (a.io[0].pos0 < 0 || a.io[0].pos0 + a.n_pos > a.max_seq) return hipErrorInvalidValue;
-  std::lock_guard<std::mutex> lk(g_mu);
-  DeviceCheck& dc = g_dev[dev];
-  if (dc.has_last && dc.last_stream != stream && (e = hipStreamWaitEvent(stream, dc.last, 0)) != hipSuccess) return e;
-  hipError_t ze = hipSuccess;
-  a.tag_base = next_tag_base(a.io[0].ws, n_streams, stream, &ze);
-  if (ze != hipSuccess) return ze;
   a.spin_cap = kSpinCap;
   a.trace = g_trace;
-  void* args[] = {&a};
   const void* fn = bb ? (xl ? (const void*)qtts::qtts_decode_kernel<true, true> : (const void*)qtts::qtts_decode_kernel<true, false>)
                       : (xl ? (const void*)qtts::qtts_decode_kernel<false, true> : (const void*)qtts::qtts_decode_kernel<false, false>);
-  if ((e = hipLaunchKernel(fn, dim3(qtts::NWG), dim3(qtts::NTHR), args, 0, stream)) != hipSuccess) return e;
-  if ((e = hipEventRecord(dc.last, stream)) != hipSuccess) return e;
-  dc.last_stream = stream;
-  dc.has_last = true;
-  return hipSuccess;
+  return ordered_launch(dev, fn, qtts::NTHR, &a, &a.tag_base, a.io[0].ws, n_streams, sizeof(Workspace), stream);
 }
 
 void* lib_workspace(hipStream_t stream, hipError_t* err) {
@@ -1855,6 +1757,34 @@ hipError_t ref_launch(bool bb, int token, const void* embed, const void* emb, co
 }
 
 }  // namespace
+
+namespace qtts_host {
+
+hipError_t check_kernel(const void* fn, int threads, int* device) {
+  hipError_t e = hipGetDevice(device);
+  if (e != hipSuccess) return e;
+  if ((e = check_device(*device)) != hipSuccess) return e;
+  static std::map<std::pair<int, const void*>, hipError_t> checked;   // guarded by g_mu
+  std::lock_guard<std::mutex> lk(g_mu);
+  const auto key = std::make_pair(*device, fn);
+  const auto it = checked.find(key);
+  if (it != checked.end()) return it->second;
+  int occ = 0;
+  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, threads, 0);
+  if (e == hipSuccess && occ < 1) e = hipErrorInvalidDevice;
+  checked[key] = e;
+  return e;
+}
+
+hipError_t launch_persistent(const void* fn, int threads, void* kargs, uint32_t* tag_base, void* ws, int n_ws,
+                             size_t ws_bytes, hipStream_t stream) {
+  int dev = 0;
+  hipError_t e = check_kernel(fn, threads, &dev);
+  if (e != hipSuccess) return e;
+  return ordered_launch(dev, fn, threads, kargs, tag_base, ws, n_ws, ws_bytes, stream);
+}
+
+}  // namespace qtts_host
 
 extern "C" {
 

@@ -1,0 +1,113 @@
+// Exchange-slot polling shared by the decode kernels: a wave polls tagged {f32 value, u32 tag}
+// slots of a workspace through one buffer descriptor (L2-coherent sc1 loads) into registers or LDS.
+#pragma once
+#include "qtts_common.h"
+
+namespace qtts {
+
+struct Poll {
+  __amdgpu_buffer_rsrc_t rs;   // covers the whole workspace
+  const void* base;
+  ErrCtl ec;
+};
+
+__device__ __forceinline__ uint32_t ws_off(const Poll& P, const void* p) {
+  return (uint32_t)(reinterpret_cast<const char*>(p) - reinterpret_cast<const char*>(P.base));
+}
+
+// Poll npair 16-byte pairs (two tagged slots each) into registers: pair k of this lane, index
+// i = lane + 64 k (i < npair), lives at byte offset off(i) of the workspace and lands in
+// out[2 k], out[2 k + 1]. Returns false on timeout (error word set).
+template <int MAXP, typename OffF>
+__device__ bool poll_regs(const Poll& P, int npair, uint32_t tag, float (&out)[2 * MAXP], OffF off) {
+  const int lane = opaque((int)threadIdx.x & 63);   // keeps slot offsets from being hoisted and spilled
+  uint32_t valid = 0;
+#pragma unroll
+  for (int k = 0; k < MAXP; ++k)
+    if (lane + 64 * k < npair) valid |= 1u << k;
+  uint32_t pending = valid;
+  uint32_t spins = 0;
+  auto check = [&](const u32x4 (&v)[MAXP]) {
+#pragma unroll
+    for (int k = 0; k < MAXP; ++k) {
+      if ((pending & (1u << k)) && v[k].y == tag && v[k].w == tag) {
+        out[2 * k] = __uint_as_float(v[k].x);
+        out[2 * k + 1] = __uint_as_float(v[k].z);
+        pending &= ~(1u << k);
+      }
+    }
+    return __ballot(pending != 0u) == 0ull;
+  };
+  auto timed_out = [&]() {
+    ++spins;
+    if ((spins & 63u) == 0u && (spins > P.ec.spin_cap || err_set(P.ec))) {
+      if (lane == 0) atomicOr(P.ec.err, 1u);
+      return true;
+    }
+    return false;
+  };
+  if constexpr (MAXP <= 17) {
+    // NBAT batches in flight: the next batch is issued before the oldest one is checked, so a
+    // slot is seen about 1 / NBAT of a load latency after it lands instead of a whole one.
+    // Every batch has the same loads (lanes without a slot re-read slot 0), so the wait for
+    // the oldest batch is an exact vmcnt.
+    constexpr int NBAT = MAXP <= 2 ? 4 : (MAXP <= 4 ? 3 : 2);
+    u32x4 vb[NBAT][MAXP];
+    auto issue = [&](u32x4 (&v)[MAXP]) {
+#pragma unroll
+      for (int k = 0; k < MAXP; ++k)
+        v[k] = __builtin_amdgcn_raw_buffer_load_b128(P.rs, off((valid >> k) & 1u ? lane + 64 * k : 0), 0, 16);
+    };
+#pragma unroll
+    for (int b = 0; b < NBAT - 1; ++b) issue(vb[b]);
+    for (;;) {
+#pragma unroll
+      for (int b = 0; b < NBAT; ++b) {
+        issue(vb[(b + NBAT - 1) % NBAT]);
+        if (check(vb[b])) return true;
+      }
+      if (timed_out()) return false;
+    }
+  } else {
+    for (;;) {
+      u32x4 v[MAXP];
+#pragma unroll
+      for (int k = 0; k < MAXP; ++k)
+        if (pending & (1u << k)) v[k] = __builtin_amdgcn_raw_buffer_load_b128(P.rs, off(lane + 64 * k), 0, 16);
+      if (check(v)) return true;
+      if (timed_out()) return false;
+    }
+  }
+}
+// Poll npair pairs into LDS: pair i to dst[2 i], dst[2 i + 1].
+template <int MAXP, typename OffF>
+__device__ bool poll_pairs(const Poll& P, int npair, uint32_t tag, float* dst, OffF off) {
+  float v[2 * MAXP];
+  const bool ok = poll_regs<MAXP>(P, npair, tag, v, off);
+  const int lane = opaque((int)threadIdx.x & 63);
+#pragma unroll
+  for (int k = 0; k < MAXP; ++k)
+    if (lane + 64 * k < npair) *reinterpret_cast<float2*>(dst + 2 * (lane + 64 * k)) = make_float2(v[2 * k], v[2 * k + 1]);
+  return ok;
+}
+// contiguous n slots (n even) starting at p
+template <int MAXP>
+__device__ __forceinline__ bool poll_vec(const Poll& P, const uint64_t* p, int n, uint32_t tag, float* dst) {
+  const uint32_t o = ws_off(P, p);
+  return poll_pairs<MAXP>(P, n >> 1, tag, dst, [o](int i) { return o + 16u * (uint32_t)i; });
+}
+// contiguous 1024 slots into registers: this lane gets elements 2 (lane + 64 k) + {0, 1}
+__device__ __forceinline__ bool poll_vec_regs(const Poll& P, const uint64_t* p, uint32_t tag, float (&out)[16]) {
+  const uint32_t o = ws_off(P, p);
+  return poll_regs<8>(P, HID / 2, tag, out, [o](int i) { return o + 16u * (uint32_t)i; });
+}
+
+// Workgroup barrier: makes LDS data one wave wrote visible to the others. Every wave of the
+// workgroup must reach each barrier the same number of times.
+__device__ __forceinline__ void step_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+}  // namespace qtts

@@ -1,7 +1,23 @@
 """GPU: BASELINE config 4 -- a batch of 8 independent streams with ragged attended KV lengths
 in [128, 1024] (per-stream positions and attention lengths), one backbone step with codec head,
 suppress mask and greedy g0, then one code-predictor frame per stream, against the committed
-oracle fixture tests/golden/c4_batched.npz."""
+oracle fixture tests/golden/c4_batched.npz; and both multi-stream kernels against batch 1.
+
+Two kernels serve several streams (BatchedTTSDecoder ``mode``):
+* ``per_xcd``: stream s on XCD s, the batch-1 arithmetic; held bit-identical to batch 1.
+* ``shared``: one weight read for all streams, projections on bf16 MFMA with the f32 inputs split
+  exactly into three bf16 pieces and f32 sums (the reference kernels' f32 arithmetic). Its sums
+  differ from the f64 ones of batch 1 and the oracle by f32 rounding. The stored values hide most
+  of that (f32 q/k/v and partials, bf16 backbone residual and KV, bf16 logits): with BASELINE's
+  literal N(0, 0.02) norm gains all 8 streams of 28 layers come out bit-identical to batch 1.
+  Now and then the difference tips a bf16 rounding of the backbone residual by one ulp (0.4% of
+  one element); with N(1, 0.02) gains (the fixtures' non-inert layers) later layers spread such a
+  flip to ~5e-3 - 9e-3 rel-L2 of the final hidden, as they spread an f32-level perturbation of the
+  f64 oracle itself. So the shared backbone is held to rel-L2 1e-3 at literal gains and to
+  north_star's 1e-2 at N(1, 0.02), with the group-0 ids identical (their top-2 gaps logged) and the
+  code-predictor frame identical to batch 1's from the same backbone hidden. The code predictor
+  (f32 in both kernels) is held to identical ids and combine.
+"""
 import json
 
 import numpy as np
@@ -13,9 +29,20 @@ from oracle.qtts_oracle import rel_l2
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
+TOL_SHARED_BB = 2e-3      # 2-layer models: a flip has few layers to spread through
+TOL_SHARED_LITERAL = 1e-3  # 28 layers, N(0, 0.02) gains
+TOL_NORTH_STAR = 1e-2      # 28 layers, N(1, 0.02) gains
+MODES = ["per_xcd", "shared"]
 
 
-def test_c4_batch8_ragged(pkg):
+def _gap(logits: torch.Tensor) -> float:
+    """Top-2 gap of a logit vector (how far its greedy choice is from a tie)."""
+    v = torch.topk(logits[torch.isfinite(logits)].double(), 2)[0]
+    return float(v[0] - v[1])
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_c4_batch8_ragged(pkg, mode):
     manifest = json.loads((cases.HERE / "manifest.json").read_text())["cases"]["c4"]
     sd = cases.weights(pkg, "c4")
     assert cases.weight_digest(sd) == manifest["weights"], "seeded weight generator drifted"
@@ -24,8 +51,9 @@ def test_c4_batch8_ragged(pkg):
     lengths = cases.c4_lengths()
     assert lengths == fx["lengths"].tolist()
     n = len(lengths)
-    dec = pkg.BatchedTTSDecoder(dsd, n, max_seq_len=max(lengths) + 8)
+    dec = pkg.BatchedTTSDecoder(dsd, n, max_seq_len=max(lengths) + 8, mode=mode)
     xs, texts = [], []
+    print(f"c4 ({mode}): lengths {lengths}", flush=True)
     for s, L in enumerate(lengths):
         k, v, x, text = cases.c4_stream_inputs(s, L)
         dec.set_kv_cache(s, k.cuda(), v.cuda())
@@ -40,21 +68,80 @@ def test_c4_batch8_ragged(pkg):
     dec.cp_frames(hidden, g0, torch.stack(texts).cuda(), toks, comb)
     torch.cuda.synchronize()
     dec.check_error()
-    worst = max(rel_l2(hidden[s].cpu(), torch.from_numpy(fx["hidden"][s])) for s in range(n))
-    print(f"c4 batch {n}, lengths {lengths}: worst hidden rel_l2 {worst:.2e}", flush=True)
-    assert worst < TOL
-    assert np.array_equal(toks.cpu().numpy(), fx["tokens"])
-    assert np.array_equal(comb.float().cpu().numpy(), fx["combined"])
+    errs = [rel_l2(hidden[s].cpu(), torch.from_numpy(fx["hidden"][s])) for s in range(n)]
+    print(f"c4 batch {n} ({mode}), lengths {lengths}: hidden rel_l2 per stream {[f'{e:.1e}' for e in errs]}", flush=True)
     assert dec.positions() == lengths
+    if mode == "per_xcd":
+        assert max(errs) < TOL
+        assert np.array_equal(toks.cpu().numpy(), fx["tokens"])
+        assert np.array_equal(comb.float().cpu().numpy(), fx["combined"])
+        return
+    assert max(errs) < TOL_NORTH_STAR
+    gaps = [_gap(d.decoder.logits_buffer()) for d in dec.streams]
+    print(f"  g0 {toks[:, 0].tolist()}, top-2 gaps {[f'{g:.3f}' for g in gaps]}", flush=True)
+    assert np.array_equal(toks[:, 0].cpu().numpy(), fx["tokens"][:, 0])
+    # the code-predictor frame against batch 1's from the same (GPU) backbone hidden; where that
+    # hidden equals the oracle's, against the fixture as well
+    cp = dec.cp.decoder
+    tx = torch.stack(texts).cuda()
+    for s in range(n):
+        t1 = torch.full((16,), -1, **i32)
+        c1 = torch.empty(1024, dtype=torch.bfloat16, device="cuda")
+        cp.frame(hidden[s].contiguous(), g0[s:s + 1], tx[s].contiguous(), t1, c1, -1, torch.zeros(1, **i32), False,
+                 1.0, 0, 1.0, 0, 0)
+        torch.cuda.synchronize()
+        assert torch.equal(toks[s], t1), f"stream {s}: {toks[s].tolist()} vs batch 1 {t1.tolist()}"
+        assert torch.equal(comb[s], c1), f"stream {s}: combined input differs from batch 1"
+        if errs[s] == 0.0:
+            assert np.array_equal(toks[s].cpu().numpy(), fx["tokens"][s])
+            assert np.array_equal(comb[s].float().cpu().numpy(), fx["combined"][s])
 
 
-def _batched_pair(pkg, lengths, seed):
+def test_shared_28_layers_literal_gains(pkg):
+    """The weight-shared backbone step and code-predictor frame of 8 streams at the c4 lengths,
+    28 + 5 layers with BASELINE's literal N(0, 0.02) norm gains, against the per-XCD kernels
+    (bit-identical to batch 1): hidden and logits within TOL_SHARED_LITERAL (observed 0 and ~1e-7:
+    a logit can round to the next bf16 value), every id identical, top-2 gaps logged."""
+    sd = pkg.synthetic_state_dict(seed=cases.SEEDS["c4"], cfg=pkg.SyntheticConfig(norm_mean=0.0))
+    dsd = {k: v.cuda() for k, v in sd.items()}
+    lengths = cases.c4_lengths()
+    n = len(lengths)
+    i32 = dict(dtype=torch.int32, device="cuda")
+    out = {}
+    for mode in ("shared", "per_xcd"):
+        dec = pkg.BatchedTTSDecoder(dsd, n, max_seq_len=max(lengths) + 8, mode=mode)
+        xs, texts = [], []
+        for s, L in enumerate(lengths):
+            k, v, x, text = cases.c4_stream_inputs(s, L)
+            dec.set_kv_cache(s, k.cuda(), v.cuda())
+            xs.append(x)
+            texts.append(text)
+        print(f"literal gains ({mode}): launching", flush=True)
+        g0 = torch.zeros(n, **i32)
+        hidden = dec.step_select(torch.stack(xs).cuda(), g0, cases.EOS_ID)
+        toks = torch.full((n, 16), -1, **i32)
+        comb = torch.empty(n, 1024, dtype=torch.bfloat16, device="cuda")
+        dec.cp_frames(hidden, g0, torch.stack(texts).cuda(), toks, comb)
+        torch.cuda.synchronize()
+        dec.check_error()
+        out[mode] = (hidden.cpu(), [d.decoder.logits_buffer().cpu() for d in dec.streams], toks.cpu(), comb.cpu())
+    (hs, ls, ts, cs), (hp, lp, tp, cp_) = out["shared"], out["per_xcd"]
+    for s in range(n):
+        eh, el = rel_l2(hs[s], hp[s]), rel_l2(ls[s], lp[s])
+        print(f"  stream {s} (L={lengths[s]}): hidden {eh:.1e} logits {el:.1e} top-2 gap {_gap(lp[s]):.2e}", flush=True)
+        assert eh < TOL_SHARED_LITERAL and el < TOL_SHARED_LITERAL
+    assert torch.equal(ts, tp), f"ids differ: {ts.tolist()} vs {tp.tolist()}"
+    assert torch.equal(cs, cp_)
+
+
+def _batched_pair(pkg, lengths, seed, mode="per_xcd"):
     """Two BatchedTTSDecoders over one 2-layer synthetic model with identical per-stream KV
-    prefixes: stream s attends lengths[s] positions (its new entry at slot lengths[s] - 1)."""
+    prefixes: stream s attends lengths[s] positions (its new entry at slot lengths[s] - 1). The
+    first runs in `mode`; the second's streams serve as batch-1 references."""
     cfg = pkg.SyntheticConfig(n_bb_layers=2, n_cp_layers=1, n_groups=1)
     dsd = {k: v.cuda() for k, v in pkg.synthetic_state_dict(seed=seed, cfg=cfg).items()}
     n, S = len(lengths), max(lengths)
-    decs = [pkg.BatchedTTSDecoder(dsd, n, max_seq_len=S) for _ in range(2)]
+    decs = [pkg.BatchedTTSDecoder(dsd, n, max_seq_len=S, mode=m) for m in (mode, "per_xcd")]
     g = torch.Generator().manual_seed(seed)
     for s, L in enumerate(lengths):
         k = torch.randn(2, 8, L - 1, 128, generator=g).to(torch.bfloat16).cuda()
@@ -67,19 +154,22 @@ def _batched_pair(pkg, lengths, seed):
     return decs
 
 
+@pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("lengths,sample", [
     ([1, 33, 64, 65, 577, 4096, 200, 2, 1500], False),
     ([4096, 129, 1000], True),
 ], ids=["greedy9", "sampled3"])
-def test_backbone_streams_match_batch1(pkg, lengths, sample):
-    """One launch of up to 8 backbone streams (stream s on XCD s, decode_steps_streams) against
-    batch-1 decode_step_select on a copy of each stream: token, final-norm hidden, residual,
-    logits and the new KV entry bit-identical. Lengths mix the one-pass local attention (<= 64)
-    and the chunked split up to 32 (chunk, head) units (4096: 8 per workgroup); 9 streams take
-    two launches (8 + 1); the sampled case adds top-k / top-p, temperature and a repetition
-    penalty over per-stream histories of different lengths."""
+def test_backbone_streams_match_batch1(pkg, lengths, sample, mode):
+    """One launch of up to 8 backbone streams (decode_steps_streams) against batch-1
+    decode_step_select on a copy of each stream. per_xcd (stream s on XCD s): token, final-norm
+    hidden, residual, logits and the new KV entry bit-identical. shared: token identical, the
+    states within rel-L2 TOL_SHARED_BB. Lengths mix the batch-1 one-pass local attention (<= 64)
+    and its chunked split up to 32 (chunk, head) units (4096: 8 per workgroup), and give the
+    shared kernel's length-proportional units (1 .. 8 per stream); 9 streams take two launches
+    (8 + 1); the sampled case adds top-k / top-p, temperature and a repetition penalty over
+    per-stream histories of different lengths."""
     n = len(lengths)
-    xl, ref = _batched_pair(pkg, lengths, 70 + n)
+    xl, ref = _batched_pair(pkg, lengths, 70 + n, mode)
     g = torch.Generator().manual_seed(n)
     x = torch.randn(n, 1024, generator=g).to(torch.bfloat16).cuda()
     vocab = xl.vocab_size
@@ -89,7 +179,7 @@ def test_backbone_streams_match_batch1(pkg, lengths, sample):
               top_k=40, top_p=0.9, frame_step=3)
     i32 = dict(dtype=torch.int32, device="cuda")
     tok = torch.full((n,), -1, **i32)
-    print(f"backbone streams {lengths} sample={sample}: launching", flush=True)
+    print(f"backbone streams {lengths} sample={sample} ({mode}): launching", flush=True)
     hidden = xl.step_select(x, tok, cases.EOS_ID, history=hist if sample else None, n_history=n_hist, seed=5, **kw)
     for s, dec in enumerate(ref.streams):
         t1 = torch.full((1,), -1, **i32)
@@ -97,14 +187,24 @@ def test_backbone_streams_match_batch1(pkg, lengths, sample):
                                        cases.EOS_ID, False, sample, kw["temperature"], kw["top_k"], kw["top_p"], 5 + s,
                                        kw["frame_step"])
         torch.cuda.synchronize()
-        assert torch.equal(tok[s:s + 1], t1), f"stream {s} (L={lengths[s]}): token {tok[s].item()} vs {t1.item()}"
-        assert torch.equal(hidden[s], dec.decoder.hidden_state_buffer()), f"stream {s}: hidden differs"
         xd = xl.streams[s].decoder
-        assert torch.equal(xd.residual_buffer(), dec.decoder.residual_buffer()), f"stream {s}: residual differs"
-        assert torch.equal(xd.logits_buffer(), dec.decoder.logits_buffer()), f"stream {s}: logits differ"
         L = lengths[s]
-        assert torch.equal(xd.get_k_cache()[:, :, L - 1], dec.decoder.get_k_cache()[:, :, L - 1])
-        assert torch.equal(xd.get_v_cache()[:, :, L - 1], dec.decoder.get_v_cache()[:, :, L - 1])
+        if mode == "per_xcd":
+            assert torch.equal(tok[s:s + 1], t1), f"stream {s} (L={L}): token {tok[s].item()} vs {t1.item()}"
+            assert torch.equal(hidden[s], dec.decoder.hidden_state_buffer()), f"stream {s}: hidden differs"
+            assert torch.equal(xd.residual_buffer(), dec.decoder.residual_buffer()), f"stream {s}: residual differs"
+            assert torch.equal(xd.logits_buffer(), dec.decoder.logits_buffer()), f"stream {s}: logits differ"
+            assert torch.equal(xd.get_k_cache()[:, :, L - 1], dec.decoder.get_k_cache()[:, :, L - 1])
+            assert torch.equal(xd.get_v_cache()[:, :, L - 1], dec.decoder.get_v_cache()[:, :, L - 1])
+        else:
+            eh = rel_l2(hidden[s], dec.decoder.hidden_state_buffer())
+            el = rel_l2(xd.logits_buffer(), dec.decoder.logits_buffer())
+            ek = rel_l2(xd.get_k_cache()[:, :, L - 1].float(), dec.decoder.get_k_cache()[:, :, L - 1].float())
+            ev = rel_l2(xd.get_v_cache()[:, :, L - 1].float(), dec.decoder.get_v_cache()[:, :, L - 1].float())
+            print(f"  stream {s} (L={L}): hidden {eh:.1e} logits {el:.1e} K {ek:.1e} V {ev:.1e}, "
+                  f"top-2 gap {_gap(dec.decoder.logits_buffer()):.3e}", flush=True)
+            assert max(eh, el, ek, ev) < TOL_SHARED_BB, f"stream {s} (L={L})"
+            assert torch.equal(tok[s:s + 1], t1), f"stream {s} (L={L}): token {tok[s].item()} vs {t1.item()}"
     xl.check_error()
     ref.check_error()
     assert xl.positions() == ref.positions() == lengths
@@ -136,15 +236,17 @@ def test_backbone_streams_reject_bad_arguments(pkg):
     assert lead.position() == 0 and other.position() == 16
 
 
-@pytest.mark.parametrize("n,sample", [(3, False), (9, True)], ids=["greedy3", "sampled9"])
-def test_cp_frames_streams_match_batch1(pkg, n, sample):
-    """Code-predictor frames of n streams through BatchedTTSDecoder.cp_frames (up to 8 per launch,
-    stream s on XCD s) against the batch-1 frame() of each stream with the same key (seed + s):
-    the 15 group ids and the combined next input bit-identical; 9 streams take two launches; the
-    sampled case draws every group with temperature and top-k."""
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("n,sample", [(3, False), (9, True), (8, False)], ids=["greedy3", "sampled9", "greedy8"])
+def test_cp_frames_streams_match_batch1(pkg, n, sample, mode):
+    """Code-predictor frames of n streams through BatchedTTSDecoder.cp_frames (up to 8 per launch)
+    against the batch-1 frame() of each stream with the same key (seed + s): the 15 group ids and
+    the combined next input identical (in both modes: the code predictor accumulates in f32 in
+    either kernel, and the combine is a bf16 sum of the rows the ids select); 9 streams take two
+    launches; the sampled case draws every group with temperature and top-k."""
     cfg = pkg.SyntheticConfig(n_bb_layers=1, n_cp_layers=2, n_groups=15)
     dsd = {k: v.cuda() for k, v in pkg.synthetic_state_dict(seed=40 + n, cfg=cfg).items()}
-    dec = pkg.BatchedTTSDecoder(dsd, n, max_seq_len=16)
+    dec = pkg.BatchedTTSDecoder(dsd, n, max_seq_len=16, mode=mode)
     g = torch.Generator().manual_seed(n)
     hid = torch.randn(n, 1024, generator=g).cuda()
     i32 = dict(dtype=torch.int32, device="cuda")
@@ -153,7 +255,7 @@ def test_cp_frames_streams_match_batch1(pkg, n, sample):
     toks = torch.full((n, 16), -1, **i32)
     comb = torch.empty(n, 1024, dtype=torch.bfloat16, device="cuda")
     kw = dict(do_sample=sample, temperature=0.8, top_k=30, seed=11, frame_step=5)
-    print(f"cp frames {n} streams sample={sample}: launching", flush=True)
+    print(f"cp frames {n} streams sample={sample} ({mode}): launching", flush=True)
     dec.cp_frames(hid, g0, text, toks, comb, **kw)
     cp = dec.cp.decoder
     for s in range(n):
@@ -168,16 +270,19 @@ def test_cp_frames_streams_match_batch1(pkg, n, sample):
     print(f"cp frames {n} streams: first stream groups {toks[0, 1:6].tolist()}...", flush=True)
 
 
+@pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("sample", [False, True], ids=["greedy", "sampled"])
-def test_batched_generate_matches_single_stream(pkg, sample):
+def test_batched_generate_matches_single_stream(pkg, sample, mode):
     """BatchedTTSDecoder.generate() -- per-stream prefill, then one code-predictor launch and one
     backbone launch per frame for all streams -- against NativeTTSGenerator.generate() of each
     stream with key seed + s, frame for frame and id for id: 3 streams with ragged prompts (40,
     97, 160 tokens) and trailing texts (5, 1, 30 rows). The EOS id is a group-0 token that
     stream 0 first chooses at a frame k >= 5 (not a multiple of sync_every) in a run with EOS
     suppressed, so stream 0 ends there while the others may run on; suppressing that id earlier
-    changes no earlier choice, since it was never chosen before."""
-    cfg = pkg.SyntheticConfig(n_bb_layers=4, n_cp_layers=2, n_groups=15)
+    changes no earlier choice, since it was never chosen before. The shared mode runs at BASELINE's
+    literal N(0, 0.02) gains (see the module docstring)."""
+    # shared mode: BASELINE's literal gains, where the f32 sums tip no stored rounding
+    cfg = pkg.SyntheticConfig(n_bb_layers=4, n_cp_layers=2, n_groups=15, norm_mean=1.0 if mode == "per_xcd" else 0.0)
     dsd = {k: v.cuda() for k, v in pkg.synthetic_state_dict(seed=77, cfg=cfg).items()}
     g = torch.Generator().manual_seed(78)
     prompts = [torch.randn(1, S, 1024, generator=g).to(torch.bfloat16) for S in (40, 97, 160)]
@@ -186,8 +291,8 @@ def test_batched_generate_matches_single_stream(pkg, sample):
     n, frames_max = 3, 24
     kw = dict(do_sample=sample, temperature=0.9, top_k=40, top_p=0.9, cp_do_sample=sample, cp_temperature=0.8,
               cp_top_k=30, repetition_penalty=1.1, seed=5)
-    dec = pkg.BatchedTTSDecoder(dsd, n, max_seq_len=256)
-    print(f"batched generate sample={sample}: EOS suppressed run", flush=True)
+    dec = pkg.BatchedTTSDecoder(dsd, n, max_seq_len=256, mode=mode)
+    print(f"batched generate sample={sample} ({mode}): EOS suppressed run", flush=True)
     free = dec.generate(prompts, texts, pad, 3000, max_tokens=frames_max, min_new_tokens=frames_max, **kw)
     assert [len(f) for f in free] == [frames_max] * n
     g0 = [f[0] for f in free[0]]
@@ -212,6 +317,8 @@ def test_batched_generate_rejects_bad_arguments(pkg):
     cfg = pkg.SyntheticConfig(n_bb_layers=1, n_cp_layers=1, n_groups=15)
     dsd = {k: v.cuda() for k, v in pkg.synthetic_state_dict(seed=5, cfg=cfg).items()}
     dec = pkg.BatchedTTSDecoder(dsd, 2, max_seq_len=64)
+    with pytest.raises(ValueError, match="mode"):
+        pkg.BatchedTTSDecoder(dsd, 2, max_seq_len=64, mode="xcd")
     for s in range(2):
         dec.streams[s].set_position(7)
     ok = torch.zeros(1, 10, 1024, dtype=torch.bfloat16)
