@@ -636,6 +636,11 @@ PYBIND11_MODULE(_qwentts_amd_C, m) {
     TORCH_CHECK(buf->is_cuda() && buf->is_contiguous(), "trace buffer must be a contiguous GPU tensor");
     hip_check(qtts_debug_trace(buf->data_ptr(), (size_t)buf->numel() * buf->element_size()), "qtts_debug_trace");
   }, py::arg("buffer") = py::none());
+  m.def("set_trace_shared", [](c10::optional<torch::Tensor> buf) {
+    if (!buf.has_value()) { hip_check(qtts_debug_trace_shared(nullptr, 0), "qtts_debug_trace_shared"); return; }
+    TORCH_CHECK(buf->is_cuda() && buf->is_contiguous(), "trace buffer must be a contiguous GPU tensor");
+    hip_check(qtts_debug_trace_shared(buf->data_ptr(), (size_t)buf->numel() * buf->element_size()), "qtts_debug_trace_shared");
+  }, py::arg("buffer") = py::none());
   py::class_<MegakernelTTSDecoder>(m, "MegakernelTTSDecoder")
       .def(py::init<torch::Tensor, std::vector<torch::Tensor>, torch::Tensor, torch::Tensor, torch::Tensor, torch::Tensor,
                     int64_t, int64_t>())

@@ -43,6 +43,10 @@
 namespace qtts {
 namespace sh {
 
+// Forced inlining for the kernel's lambdas: a real call passes the by-value launch arguments and
+// the captured state by address, through scratch memory.
+#define SH_INLINE __attribute__((always_inline))
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -132,8 +136,13 @@ struct SArgs {
   int cp_vocab;
   SelParams sel;
   int unit_stream[NUNIT];  // stream of attention unit u, -1 for none
+  uint64_t* trace;         // optional step timeline: [wg][step][TRACE_SLOTS] s_memrealtime stamps
   SStream io[NS];
 };
+// timeline slots of a step: 0 after the entry barrier, 1 after the partials barrier, 2 + w the
+// end of wave w's vector work, 10 .. 15 points inside the step (wave 0)
+constexpr int TRACE_SLOTS = 16;
+constexpr int TRACE_STEPS = 1024;
 
 struct SLds {
   union {
@@ -180,6 +189,38 @@ __device__ __forceinline__ void split3(float x, bf16_t& h, bf16_t& m, bf16_t& l)
   l = f2bf(r1 - bf2f(m));
 }
 
+// Read npair 16-byte pairs into registers (pair k of this lane: i = lane + 64 k < npair) until
+// every tag matches, one round of loads in flight, re-issuing only the pairs still pending: for
+// data that has (nearly all) arrived, which a batched poll would fetch several times over.
+template <int MAXP, typename OffF>
+__device__ __forceinline__ bool read_pairs(const Poll& P, int npair, uint32_t tag, float (&out)[2 * MAXP], OffF off) {
+  const int lane = opaque((int)threadIdx.x & 63);
+  uint32_t pending = 0;
+#pragma unroll
+  for (int k = 0; k < MAXP; ++k)
+    if (lane + 64 * k < npair) pending |= 1u << k;
+  uint32_t spins = 0;
+  for (;;) {
+    u32x4 v[MAXP];
+#pragma unroll
+    for (int k = 0; k < MAXP; ++k)
+      if (pending & (1u << k)) v[k] = __builtin_amdgcn_raw_buffer_load_b128(P.rs, off(lane + 64 * k), 0, 16);
+#pragma unroll
+    for (int k = 0; k < MAXP; ++k) {
+      if ((pending & (1u << k)) && v[k].y == tag && v[k].w == tag) {
+        out[2 * k] = __uint_as_float(v[k].x);
+        out[2 * k + 1] = __uint_as_float(v[k].z);
+        pending &= ~(1u << k);
+      }
+    }
+    if (__ballot(pending != 0u) == 0ull) return true;
+    ++spins;
+    if ((spins & 63u) == 0u && (spins > P.ec.spin_cap || err_set(P.ec))) {
+      if (lane == 0) atomicOr(P.ec.err, 1u);
+      return false;
+    }
+  }
+}
 // Sum of the 8 XCD partials of rows r0 + 2 (lane & 15) + {0, 1} of one stream: lane group
 // g = lane >> 4 polls XCDs 2 g and 2 g + 1; two exchanges complete the sum as
 // ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7)), the same in every lane and workgroup.
@@ -200,12 +241,34 @@ __device__ __forceinline__ bool poll_sum8s(const Poll& P, const uint64_t* p0, ui
   return ok;
 }
 
+// A 1024-vector published by the 32 workgroups of an XCD, workgroup j writing rows
+// [32 j, 32 j + 32) as 16 pairs from one store instruction: lanes 0..31 poll the last pair of
+// producer `lane` until all 32 have landed, then every pair is read once (lane gets elements
+// 2 (lane + 64 k) + {0, 1}). Polling one pair per producer instead of all 512 keeps the eight
+// waves' polls from filling the CU's memory pipeline.
+__device__ __forceinline__ bool gather1024(const Poll& P, const uint64_t* p, uint32_t tag, float (&out)[16]) {
+  const uint32_t o = ws_off(P, p);
+  float pr[2];
+  if (!poll_regs<1>(P, WPX, tag, pr, [o](int i) { return o + 16u * (16u * (uint32_t)i + 15u); })) return false;
+  return read_pairs<8>(P, HID / 2, tag, out, [o](int i) { return o + 16u * (uint32_t)i; });
+}
+
+// Token selection over an LDS logit vector, kept out of line: inlined, the loop-invariant parts of
+// its sampler would be hoisted out of the step loops and hold registers (or spill) for the whole
+// launch; it runs at most once per head.
+__device__ __attribute__((noinline)) int sh_wave_select(const float* lg, int n, SelParams sp, SelScratch* sc) {
+  return wave_select(lg, n, sp, sc);
+}
+
 template <bool BB>
 __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
   __shared__ SLds s;
   // norm statistics in f64 for the backbone (its bf16 residual), f32 in the code predictor
   using A = std::conditional_t<BB, double, float>;
+  // lane and thread index, re-derived opaquely at every step so that offsets computed from them
+  // are recomputed where used instead of being hoisted out of the step loop and spilled
   int lane = threadIdx.x & 63;
+  int tid = threadIdx.x;
   const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));   // wave = stream slot
   const int xcd = (int)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15u);   // HW_REG_XCC_ID
   const int li = blockIdx.x >> 3;
@@ -264,6 +327,11 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
     __builtin_amdgcn_raw_buffer_store_b128(d, P.rs, (int)ws_off(P, p), 0, 0);
   };
   auto tag_of = [&](int lp, int slot) -> uint32_t { return a.tag_base + (uint32_t)(lp * T_NSLOT + slot); };
+  int nstep = 0;
+  auto stamp = [&](int slot) {
+    if (a.trace != nullptr && lane == 0 && nstep < TRACE_STEPS && ((slot >= 2 && slot < 2 + SWAV) || wv == 0))
+      a.trace[((size_t)wg * TRACE_STEPS + nstep) * TRACE_SLOTS + slot] = __builtin_amdgcn_s_memrealtime();
+  };
   auto has_head = [&](int pi) -> bool { return cp ? pi >= 1 : (a.head != nullptr && pi == a.n_pos - 1); };
 
   // ---- per-wave vectors of its stream: RMSNorm gains of the lane's 16 hidden elements
@@ -324,14 +392,15 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
   // the workgroup's 32 rows 32 li + m of a lane-distributed vector: lanes 16 (li & 3) .. + 15
   // hold them at k = li >> 2
   auto keep_rows = [&](float* dst, const float (&xv)[16]) {
-    if ((lane >> 4) == (li & 3)) {
+    // a select chain over k (a uniform index into the register array would go through scratch)
+    const int kk = li >> 2;
+    float v0 = xv[0], v1 = xv[1];
 #pragma unroll
-      for (int k = 0; k < 8; ++k)
-        if (k == (li >> 2)) {
-          dst[2 * (lane & 15)] = xv[2 * k];
-          dst[2 * (lane & 15) + 1] = xv[2 * k + 1];
-        }
+    for (int k = 1; k < 8; ++k) {
+      v0 = k == kk ? xv[2 * k] : v0;
+      v1 = k == kk ? xv[2 * k + 1] : v1;
     }
+    if ((lane >> 4) == (li & 3)) *reinterpret_cast<float2*>(&dst[2 * (lane & 15)]) = make_float2(v0, v1);
   };
 
   // ---- vector work of this wave's stream --------------------------------------------------
@@ -420,34 +489,43 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
     }
   };
   // the stream's O-projection input: merge of its attention units (backbone). Lane (h, dq):
-  // head h = lane >> 5, dims dq .. dq + 3 (dq = 4 (lane & 31)); per unit it polls two pairs of
-  // acc and the (m, l) pair of head h: w_c = exp(m_c - M), out = (sum_c w_c acc_c) / (sum_c w_c l_c)
-  auto prep_o = [&](int lp) {
+  // head h = lane >> 5, dims dq .. dq + 3 (dq = 4 (lane & 31)). First the (m, l) pair of head h
+  // of every unit: w_c = exp(m_c - M), Z = sum_c w_c l_c; then two acc pairs per unit:
+  // out = (sum_c w_c acc_c) / Z. (Two polls keep fewer registers live than one.)
+  auto prep_o = [&](int lp) SH_INLINE {
     const int u0 = IO->u0, nu = IO->nu;
     const int h = lane >> 5, dq = 4 * (lane & 31);
-    float v[2 * 3 * UMAX];
+    const uint32_t o = ws_off(P, &ws->attp[xcd][lp & 1][0][0][0]);
+    const uint32_t tg = tag_of(lp, T_ATT);
+    float w[UMAX];
+    float Z = 0.0f;
     {
-      const uint32_t o = ws_off(P, &ws->attp[xcd][lp & 1][0][0][0]);
-      poll_regs<3 * UMAX>(P, 64 * 3 * nu, tag_of(lp, T_ATT), v, [o, u0](int i) {
-        const uint32_t k = (uint32_t)i >> 6, l = (uint32_t)i & 63u, c = k / 3u, w = k - 3u * c;
-        const uint32_t slot = (((uint32_t)u0 + c) * 2u + (l >> 5)) * (uint32_t)UPH + (w == 2u ? 128u : 4u * (l & 31u) + 2u * w);
-        return o + 8u * slot;
+      float ml[2 * UMAX];
+      poll_regs<UMAX>(P, 64 * nu, tg, ml, [o, u0](int i) {
+        const uint32_t c = (uint32_t)i >> 6, l = (uint32_t)i & 63u;
+        return o + 8u * ((((uint32_t)u0 + c) * 2u + (l >> 5)) * (uint32_t)UPH + 128u);
       });
-    }
-    float M = -INFINITY;
+      float M = -INFINITY;
 #pragma unroll
-    for (int c = 0; c < UMAX; ++c)
-      if (c < nu) M = fmaxf(M, v[2 * (3 * c + 2)]);
-    float Z = 0.0f, o4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int c = 0; c < UMAX; ++c)
+        if (c < nu) M = fmaxf(M, ml[2 * c]);
 #pragma unroll
-    for (int c = 0; c < UMAX; ++c) {
-      if (c < nu) {
-        const float w = __expf(v[2 * (3 * c + 2)] - M);
-        Z = fmaf(v[2 * (3 * c + 2) + 1], w, Z);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) o4[j] = fmaf(v[2 * (3 * c + (j >> 1)) + (j & 1)], w, o4[j]);
+      for (int c = 0; c < UMAX; ++c) {
+        // slots c >= nu were never polled: their registers are not read (garbage times 0 can be NaN)
+        w[c] = c < nu ? __expf(ml[2 * c] - M) : 0.0f;
+        Z = fmaf(c < nu ? ml[2 * c + 1] : 0.0f, w[c], Z);
       }
     }
+    float acc[2 * 2 * UMAX];
+    read_pairs<2 * UMAX>(P, 64 * 2 * nu, tg, acc, [o, u0](int i) {
+      const uint32_t k = (uint32_t)i >> 6, l = (uint32_t)i & 63u, c = k >> 1;
+      return o + 8u * ((((uint32_t)u0 + c) * 2u + (l >> 5)) * (uint32_t)UPH + 4u * (l & 31u) + 2u * (k & 1u));
+    });
+    float o4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < UMAX; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o4[j] = fmaf(c < nu ? acc[4 * c + j] : 0.0f, w[c], o4[j]);
     const float rz = rcp_f(Z);
     put_pair(128 * h + dq, o4[0] * rz, o4[1] * rz);
     put_pair(128 * h + dq + 2, o4[2] * rz, o4[3] * rz);
@@ -471,7 +549,8 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
   auto prep_gu = [&](int lp, int layer) {
     load_gains(lw(LW, layer, W_LNPOST));
     float xv[16], y[16];
-    poll_vec_regs(P, &ws->h1[xcd][lp & 1][wv][0], tag_of(lp, T_H1), xv);
+    gather1024(P, &ws->h1[xcd][lp & 1][wv][0], tag_of(lp, T_H1), xv);
+    stamp(12);
     keep_rows(s.h1res[wv], xv);
     normed(xv, y);
     put_vec(y);
@@ -498,7 +577,7 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
   auto prep_input_next = [&](int lp, int nlayer) {
     load_gains(lw(LW, nlayer, W_LNIN));
     float xv[16], y[16];
-    poll_vec_regs(P, &ws->xl[xcd][lp & 1][wv][0], tag_of(lp, T_XL), xv);
+    gather1024(P, &ws->xl[xcd][lp & 1][wv][0], tag_of(lp, T_XL), xv);
     keep_rows(s.xres[wv], xv);
     normed(xv, y);
     put_vec(y);
@@ -507,7 +586,7 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
   auto prep_final = [&](int lp) {
     load_gains(a.final_norm);
     float xv[16], y[16];
-    poll_vec_regs(P, &ws->xl[xcd][lp & 1][wv][0], tag_of(lp, T_XL), xv);
+    gather1024(P, &ws->xl[xcd][lp & 1][wv][0], tag_of(lp, T_XL), xv);
     normed(xv, y);
     if (wg == wv) {
 #pragma unroll
@@ -634,10 +713,11 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
     for (int jj = 0; jj < AJJ; ++jj) {
       const int pos = b0 + 4 * AJJ * wv + 4 * jj + g;
       const bool ok = pos < lim;
-      const size_t off = (head_base + (size_t)(ok ? pos : 0)) * HDIM + d0;   // every address inside the cache
-      const u32x4 k = ldw(kc + off), v = ldw(vc + off);
-      t.k[jj] = ok ? k : u32x4{0u, 0u, 0u, 0u};
-      t.v[jj] = ok ? v : u32x4{0u, 0u, 0u, 0u};
+      // positions past lim read slot 0 (finite cache data): their scores are masked to -inf and
+      // their V weighs 0, so no select on the loaded value (it would wait for the load here)
+      const size_t off = (head_base + (size_t)(ok ? pos : 0)) * HDIM + d0;
+      t.k[jj] = ldw(kc + off);
+      t.v[jj] = ldw(vc + off);
     }
   };
   struct Unit { int us, L, c0, c1; };
@@ -740,8 +820,8 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
       if (lane == 0) { s.wpart[wv][h][HDIM] = m[h]; s.wpart[wv][h][HDIM + 1] = l[h]; }
     }
     step_barrier();
-    if (u.us >= 0 && threadIdx.x < 2 * HDIM) {
-      const int h = threadIdx.x >> 7, d = threadIdx.x & 127;
+    if (u.us >= 0 && tid < 2 * HDIM) {
+      const int h = tid >> 7, d = tid & 127;
       float M = -INFINITY;
 #pragma unroll
       for (int w = 0; w < SWAV; ++w) M = fmaxf(M, s.wpart[w][h][HDIM]);
@@ -762,8 +842,9 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
 
   // ---- projections on MFMA ------------------------------------------------------------------
   // Weight fragments: lane l holds 8 consecutive bf16 of row (l & 15) of a 16-row block at
-  // columns 32 kb + 8 (l >> 4) (the v_mfma_f32_16x16x32_bf16 A layout); rows past the tile's
-  // valid count are read from a valid row and zeroed (no load under a branch).
+  // columns 32 kb + 8 (l >> 4) (the v_mfma_f32_16x16x32_bf16 A layout). Rows past the tile's
+  // valid count are read from a valid row (no load under a branch, no select on the loaded
+  // value, which would wait for it); their output rows are never summed or published.
   auto wld = [&](const bf16_t* p) -> u32x4 {
     if constexpr (BB) return ldw_nt(p); else return ldw(p);
   };
@@ -787,10 +868,7 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
     const int i = lane & 15, kg = lane >> 4, tile = wv >> 2;
     const bf16_t* row = lw(LW, layer, tile ? W_UP : W_GATE) + (size_t)(XI * xcd + 12 * li + (i < 12 ? i : 0)) * HID;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const u32x4 v = wld(row + 32 * (8 * (wv & 3) + j) + 8 * kg);
-      t.p[j] = i < 12 ? v : u32x4{0u, 0u, 0u, 0u};
-    }
+    for (int j = 0; j < 8; ++j) t.p[j] = wld(row + 32 * (8 * (wv & 3) + j) + 8 * kg);
   };
   auto load_d = [&](TD& t, int layer) {
     const int i = lane & 15, kg = lane >> 4, tile = wv >> 2;
@@ -804,10 +882,7 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
     const int i = lane & 15, kg = lane >> 4;
     const bf16_t* row = W + (size_t)(wg * head_rows + (i < head_rows ? i : 0)) * HID;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const u32x4 v = wld(row + 32 * (4 * wv + j) + 8 * kg);
-      t.p[j] = i < head_rows ? v : u32x4{0u, 0u, 0u, 0u};
-    }
+    for (int j = 0; j < 4; ++j) t.p[j] = wld(row + 32 * (4 * wv + j) + 8 * kg);
   };
   // The wave's K-blocks kb0 .. kb0 + NB - 1 of its tile against the 16 input columns (hi and mid
   // pieces of the 8 streams) and the 8 lo columns; the partial of (row, stream) goes to
@@ -907,7 +982,7 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
       sp.group = 0;
     }
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    return wave_select(s.z.stage, n, sp, &s.z.sel);
+    return sh_wave_select(s.z.stage, n, sp, &s.z.sel);
   };
 
   // =========================================================================================
@@ -928,84 +1003,115 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
     const bool head = has_head(pi);
     for (int layer = 0; layer < NL; ++layer) {
       lane = opaque(lane);
+      tid = opaque(tid);
       const int lp = pi * NL + layer;
       const int par = lp & 1;
       const bool last_layer = layer == NL - 1;
       // ---- QKV
       step_barrier();
+      stamp(0);
       gemv(tq.p, 4 * wv);
-      if constexpr (BB) load_kv_first(tkv, layer);
-      load_o(to, layer);
       step_barrier();
-      if (threadIdx.x < 16 * NS) {
-        const int st = threadIdx.x >> 4, r = threadIdx.x & 15;
+      stamp(1);
+      if (tid < 16 * NS) {
+        const int st = tid >> 4, r = tid & 15;
         const float v = red_sum(0, SWAV, r, st);
         // slot order pairs the rotate_half partners: channel c' of head block h goes to slot
         // 128 h + 2 (c' mod 64) + c' / 64, so one 16-byte pair holds channels c and c + 64
         const int lr = 16 * li + r, cc = lr & 127;
         if (is_live(st)) pub_local(&ws->qkv[xcd][par][st][(lr & ~127) + 2 * (cc & 63) + (cc >> 6)], v, tag_of(lp, T_QKV));
       }
+      stamp(14);
+      // the next tiles go out after the publish: a wave's vector-memory results return in issue
+      // order, so a poll issued behind a tile load would wait for the tile
+      if constexpr (BB) load_kv_first(tkv, layer);
+      load_o(to, layer);
       if (me) prep_att(lp, layer, pos);
+      stamp(2 + wv);
+      ++nstep;
       // ---- attention (backbone: its own step; code predictor: local, before the O projection)
       if constexpr (BB) {
         step_barrier();
+        stamp(0);
         attention_unit(lp, layer, tkv);
+        stamp(1);
         if (me) prep_o(lp);
+        stamp(2 + wv);
+        ++nstep;
       } else {
         if (me) attention_cp(layer, pi + 1);
+        stamp(13);
       }
       // ---- O projection (cross-XCD partials)
       step_barrier();
+      stamp(0);
       gemv(to.p, 2 * (wv & 3));
-      load_g(tgu, layer);
       step_barrier();
-      if (threadIdx.x < 32 * NS) {
-        const int st = threadIdx.x >> 5, tile = (threadIdx.x >> 4) & 1, r = threadIdx.x & 15;
+      stamp(1);
+      if (tid < 32 * NS) {
+        const int st = tid >> 5, tile = (tid >> 4) & 1, r = tid & 15;
         const float v = red_sum(4 * tile, 4, r, st);
         if (is_live(st)) pub_cross(&ws->opart[par][xcd][st][32 * li + 16 * tile + r], v, tag_of(lp, T_OPART));
       }
-      if (me) { ar1(lp); prep_gu(lp, layer); }
+      stamp(14);
+      load_g(tgu, layer);
+      if (me) { ar1(lp); stamp(11); prep_gu(lp, layer); }
+      stamp(2 + wv);
+      ++nstep;
       // ---- gate / up + SiLU
       step_barrier();
+      stamp(0);
       gemv(tgu.p, 8 * (wv & 3));
-      load_d(td, layer);
       step_barrier();
-      if (threadIdx.x < 12 * NS) {
-        const int st = threadIdx.x / 12, r = threadIdx.x - 12 * st;
+      stamp(1);
+      if (tid < 12 * NS) {
+        const int st = tid / 12, r = tid - 12 * st;
         const float gt = red_sum(0, 4, r, st), up = red_sum(4, 4, r, st);
         const float act = gt / (1.0f + __expf(-gt)) * up;
         if (is_live(st)) pub_local(&ws->inter[xcd][par][st][12 * li + r], act, tag_of(lp, T_INTER));
       }
+      stamp(14);
+      load_d(td, layer);
       if (me) prep_down(lp);
+      stamp(2 + wv);
+      ++nstep;
       // ---- down projection (cross-XCD partials)
       step_barrier();
+      stamp(0);
       gemv(td.p, 3 * (wv & 3));
-      if (!last_layer) load_q(tq, layer + 1);
-      else if (head) load_h(tq, head_w(pi));
-      else if (!last_pos) load_q(tq, 0);
       step_barrier();
-      if (threadIdx.x < 32 * NS) {
-        const int st = threadIdx.x >> 5, tile = (threadIdx.x >> 4) & 1, r = threadIdx.x & 15;
+      stamp(1);
+      if (tid < 32 * NS) {
+        const int st = tid >> 5, tile = (tid >> 4) & 1, r = tid & 15;
         const float v = red_sum(4 * tile, 4, r, st);
         if (is_live(st)) pub_cross(&ws->dpart[par][xcd][st][32 * li + 16 * tile + r], v, tag_of(lp, T_DPART));
       }
+      stamp(14);
+      if (!last_layer) load_q(tq, layer + 1);
+      else if (head) load_h(tq, head_w(pi));
+      else if (!last_pos) load_q(tq, 0);
       if (me) {
         if (!last_layer) { ar2(lp); prep_input_next(lp, layer + 1); }
         else if (head || last_pos) { ar2(lp); prep_final(lp); }
         else prep_input0(pi + 1);   // code-predictor position 0: its output feeds no head
       }
+      stamp(2 + wv);
+      ++nstep;
     }
     if (head) {
+      lane = opaque(lane);
+      tid = opaque(tid);
       step_barrier();
+      stamp(0);
       gemv(tq.p, 4 * wv);
-      if (!last_pos) load_q(tq, 0);
       step_barrier();
+      stamp(1);
       const uint32_t tg = a.tag_base + TAG_HEAD + (uint32_t)pi;
       const int row0 = wg * head_rows;
-      if (threadIdx.x < 16 * NS) {
+      if (tid < 16 * NS) {
         // logits are bf16 values, as the reference's torch.mv over bf16 operands returns them
         // (generator.py:158, :351); ties go to the lowest id, as torch.argmax
-        const int st = threadIdx.x >> 4, r = threadIdx.x & 15;
+        const int st = tid >> 4, r = tid & 15;
         const float lv = rbf(red_sum(0, SWAV, r, st));
         const bool ok = r < head_rows && is_live(st);
         if (cp_greedy) {
@@ -1024,6 +1130,8 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
           if (!cp && (IO0 + st)->out_logits) (IO0 + st)->out_logits[row0 + r] = lv;
         }
       }
+      stamp(14);
+      if (!last_pos) load_q(tq, 0);
       if (cp) {
         int tok = 0;
         if (cp_greedy) {
@@ -1042,7 +1150,7 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
           if (me) {
             float cv[2];
             const uint32_t o = ws_off(P, &ws->tok[pi & 1][wv][0]);
-            poll_regs<1>(P, 1, tg, cv, [o](int) { return o; });
+            [[clang::always_inline]] poll_regs<1>(P, 1, tg, cv, [o](int) { return o; });
             const int t = __builtin_amdgcn_readfirstlane((int)__float_as_uint(cv[0]));
             tok = (t >= 0 && t < a.cp_vocab) ? t : 0;
           }
@@ -1056,6 +1164,8 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
         const int t = select_full(pi);
         if (lane == 0 && IO->out_token) *IO->out_token = t;
       }
+      stamp(2 + wv);
+      ++nstep;
     }
   }
 
@@ -1098,6 +1208,8 @@ template __global__ void qtts_shared_kernel<false>(const SArgs a);
 // =========================================================================================
 namespace {
 
+uint64_t* g_strace = nullptr;   // optional step timeline buffer of the weight-shared kernels
+
 using qtts::sh::SArgs;
 using qtts::sh::SStream;
 using qtts::sh::SWorkspace;
@@ -1119,6 +1231,7 @@ void base_sargs(SArgs& a, void* ws, int n_streams, const TTSLayerWeights* layers
   a.sel.temperature = 1.0f;
   a.sel.top_p = 1.0f;
   a.spin_cap = qtts_host::kSpinCap;
+  a.trace = g_strace;
   for (int u = 0; u < qtts::sh::NUNIT; ++u) a.unit_stream[u] = -1;
 }
 
@@ -1166,6 +1279,14 @@ void assign_units(SArgs& a) {
 extern "C" {
 
 size_t qtts_shared_workspace_bytes(void) { return sizeof(SWorkspace); }
+
+hipError_t qtts_debug_trace_shared(void* device_buffer, size_t bytes) {
+  if (device_buffer != nullptr &&
+      bytes < (size_t)qtts::NWG * qtts::sh::TRACE_STEPS * qtts::sh::TRACE_SLOTS * sizeof(uint64_t))
+    return hipErrorInvalidValue;
+  g_strace = reinterpret_cast<uint64_t*>(device_buffer);
+  return hipSuccess;
+}
 
 hipError_t qtts_shared_workspace_check(void* workspace, unsigned int* error_code, hipStream_t stream) {
   if (workspace == nullptr || error_code == nullptr) return hipErrorInvalidValue;
