@@ -303,11 +303,6 @@ hipError_t qtts_cp_frame_streams(
  * Code predictor: n_groups + 1 <= 16, cp_vocab / 256 <= 16. qtts_shared_workspace_check reads
  * and clears the workspace's wait-timeout error word (synchronises the stream). */
 size_t qtts_shared_workspace_bytes(void);
-/* Debugging aid (no reference counterpart): record the weight-shared kernels' step timeline
- * (s_memrealtime stamps, [256 workgroups][1024 steps][16]: after the entry barrier, after the
- * partials barrier, the end of each of the 8 waves' vector work, 6 points inside a step) into
- * device_buffer (>= 33,554,432 bytes); NULL turns it off. */
-hipError_t qtts_debug_trace_shared(void* device_buffer, size_t bytes);
 hipError_t qtts_shared_workspace_check(void* workspace, unsigned int* error_code, hipStream_t stream);
 hipError_t qtts_backbone_step_shared(
     int n_streams, void* workspace, const TTSLayerWeights* layer_weights, int num_layers,
@@ -323,6 +318,12 @@ hipError_t qtts_cp_frame_shared(
     const void* const* lm_heads, const void* const* cp_embeddings, int n_groups, int cp_vocab,
     const void* text_rows, int* out_tokens, void* out_combined,
     int eos_id, int* done, const QttsSampling* sampling, int frame_step, hipStream_t stream);
+
+/* Debugging aid (no reference counterpart): record the weight-shared kernels' step timeline
+ * (s_memrealtime stamps, [256 workgroups][1024 steps][16]: after the entry barrier, after the
+ * partials barrier, the end of each of the 8 waves' vector work, 6 points inside a step) into
+ * device_buffer (>= 33,554,432 bytes); NULL turns it off. */
+hipError_t qtts_debug_trace_shared(void* device_buffer, size_t bytes);
 
 #ifdef __cplusplus
 }
