@@ -607,6 +607,118 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
     put_vec(y);
   };
 
+  // The code predictor's vector phases take the issue of the next step's weight tile as an
+  // argument and make it right after their last poll: a wave's vector-memory results return in
+  // issue order, so a poll issued behind a tile load waits for the tile's HBM round trip. (The
+  // backbone issues its tiles right after the publish: its kernel has no registers left to hold
+  // the polled values across the issue, and a spill reload after the issue would wait for the
+  // tile.) Generic lambdas: only the code-predictor instantiation creates them.
+  auto cp_prep_input0 = [&](int pi, auto&& issue) SH_INLINE {
+    load_gains(lw(LW, 0, W_LNIN));
+    float xv[16];
+    if (pi == 0) {
+      const auto* p = gmem(reinterpret_cast<const u32x2*>(IO->bb_hidden));
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const u32x2 v = p[lane + 64 * k];
+        xv[2 * k] = rbf(__uint_as_float(v.x));
+        xv[2 * k + 1] = rbf(__uint_as_float(v.y));
+      }
+    } else {
+      const bf16_t* src = pi == 1 ? a.bb_emb + (size_t)(*IO->g0) * HID : s.embp[pi - 2] + (size_t)s.tok[wv][pi - 2] * HID;
+      const auto* p = gmem(reinterpret_cast<const uint32_t*>(src));
+#pragma unroll
+      for (int k = 0; k < 8; ++k) { const uint32_t w = p[lane + 64 * k]; xv[2 * k] = bflo(w); xv[2 * k + 1] = bfhi(w); }
+    }
+    issue();
+    keep_rows(s.xres[wv], xv);
+    if (pi >= 1 && wg == wv) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int e = 2 * (lane + 64 * k);
+        const float2 c = *reinterpret_cast<const float2*>(&s.comb[e]);
+        *reinterpret_cast<float2*>(&s.comb[e]) = pi == 1 ? make_float2(xv[2 * k], xv[2 * k + 1])
+                                                         : make_float2(rbf(c.x + xv[2 * k]), rbf(c.y + xv[2 * k + 1]));
+      }
+    }
+    float y[16];
+    normed(xv, y);
+    put_vec(y);
+  };
+  auto cp_prep_att = [&](int lp, int layer, int pos, auto&& issue) SH_INLINE {
+    load_qk(layer, pos);
+    float v[8];
+    {
+      const uint32_t o = ws_off(P, &ws->qkv[xcd][lp & 1][wv][0]);
+      poll_regs<4>(P, LROWS / 2, tag_of(lp, T_QKV), v, [o](int i) { return o + 16u * (uint32_t)i; });
+    }
+    issue();
+    float ss[3];
+#pragma unroll
+    for (int h = 0; h < 3; ++h) ss[h] = fmaf(v[2 * h], v[2 * h], v[2 * h + 1] * v[2 * h + 1]);
+    group_sum_n<64, 3>(ss);
+    float outl[3], outh[3];
+#pragma unroll
+    for (int h = 0; h < 3; ++h) {
+      const float r = rsqrt_a(ss[h] / (float)HDIM + (float)EPSD);
+      const float gl = h < 2 ? qn[0] : kn[0], gh = h < 2 ? qn[1] : kn[1];
+      const float nl = (v[2 * h] * r) * gl, nh = (v[2 * h + 1] * r) * gh;
+      outl[h] = nl * rc[0] - nh * rsn[0];
+      outh[h] = nl * rsn[1] + nh * rc[1];
+    }
+    const int c = lane;
+    s.q[wv][0][c] = outl[0]; s.q[wv][0][c + 64] = outh[0];
+    s.q[wv][1][c] = outl[1]; s.q[wv][1][c + 64] = outh[1];
+    s.knew[wv][c] = outl[2]; s.knew[wv][c + 64] = outh[2];
+    s.vnew[wv][c] = v[6]; s.vnew[wv][c + 64] = v[7];
+    if (li == 0) {
+      float* kc = reinterpret_cast<float*>(IO->kc) + (((size_t)layer * NKVH + xcd) * (size_t)a.max_seq + pos) * HDIM + c;
+      float* vc = reinterpret_cast<float*>(IO->vc) + (((size_t)layer * NKVH + xcd) * (size_t)a.max_seq + pos) * HDIM + c;
+      gput(kc, outl[2]); gput(kc + 64, outh[2]);
+      gput(vc, v[6]); gput(vc + 64, v[7]);
+      kv_pending = true;   // ordered before this wave's next slot publish (ar1)
+    }
+  };
+  // a gathered 1024-vector (h1 or the residual after the down projection): its norm into the
+  // projection input, the workgroup's rows kept in `keep`
+  auto cp_prep_vec = [&](const uint64_t* base, uint32_t tag, const bf16_t* gains, float* keep, auto&& issue) SH_INLINE {
+    load_gains(gains);
+    float xv[16], y[16];
+    gather1024(P, base, tag, xv);
+    issue();
+    keep_rows(keep, xv);
+    normed(xv, y);
+    put_vec(y);
+  };
+  auto cp_prep_down = [&](int lp, auto&& issue) SH_INLINE {
+    float v[6];
+    const uint32_t o = ws_off(P, &ws->inter[xcd][lp & 1][wv][0]);
+    poll_regs<3>(P, XI / 2, tag_of(lp, T_INTER), v, [o](int i) { return o + 16u * (uint32_t)i; });
+    issue();
+#pragma unroll
+    for (int k = 0; k < 3; ++k) put_pair(2 * (lane + 64 * k), v[2 * k], v[2 * k + 1]);
+  };
+  auto cp_prep_final = [&](int lp, auto&& issue) SH_INLINE {
+    load_gains(a.final_norm);
+    float xv[16];
+    gather1024(P, &ws->xl[xcd][lp & 1][wv][0], tag_of(lp, T_XL), xv);
+    issue();
+    float y[16];
+    normed(xv, y);
+    if (wg == wv) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int e = 2 * (lane + 64 * k);
+        if (IO->out_hidden) *reinterpret_cast<float2*>(IO->out_hidden + e) = make_float2(y[2 * k], y[2 * k + 1]);
+        if (IO->out_residual)
+          *reinterpret_cast<float2*>(reinterpret_cast<float*>(IO->out_residual) + e) = make_float2(xv[2 * k], xv[2 * k + 1]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) y[j] = rbf(y[j]);
+    put_vec(y);
+  };
+
   // ---- attention ---------------------------------------------------------------------------
   // code predictor, wave s over stream s at length L <= 16 (f32, as the reference CP kernel):
   // lane group g takes positions j = g + 4 jj; the scores, the maximum and the sums run over
@@ -1024,9 +1136,15 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
       stamp(14);
       // the next tiles go out after the publish: a wave's vector-memory results return in issue
       // order, so a poll issued behind a tile load would wait for the tile
-      if constexpr (BB) load_kv_first(tkv, layer);
-      load_o(to, layer);
-      if (me) prep_att(lp, layer, pos);
+      if constexpr (BB) {
+        load_kv_first(tkv, layer);
+        load_o(to, layer);
+        if (me) prep_att(lp, layer, pos);
+      } else {
+        auto iss = [&]() SH_INLINE { load_o(to, layer); };
+        if (me) cp_prep_att(lp, layer, pos, iss);
+        else iss();
+      }
       stamp(2 + wv);
       ++nstep;
       // ---- attention (backbone: its own step; code predictor: local, before the O projection)
@@ -1054,8 +1172,19 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
         if (is_live(st)) pub_cross(&ws->opart[par][xcd][st][32 * li + 16 * tile + r], v, tag_of(lp, T_OPART));
       }
       stamp(14);
-      load_g(tgu, layer);
-      if (me) { ar1(lp); stamp(11); prep_gu(lp, layer); }
+      if constexpr (BB) {
+        load_g(tgu, layer);
+        if (me) { ar1(lp); stamp(11); prep_gu(lp, layer); }
+      } else {
+        auto iss = [&]() SH_INLINE { stamp(12); load_g(tgu, layer); };
+        if (me) {
+          ar1(lp);
+          stamp(11);
+          cp_prep_vec(&ws->h1[xcd][par][wv][0], tag_of(lp, T_H1), lw(LW, layer, W_LNPOST), s.h1res[wv], iss);
+        } else {
+          iss();
+        }
+      }
       stamp(2 + wv);
       ++nstep;
       // ---- gate / up + SiLU
@@ -1071,8 +1200,14 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
         if (is_live(st)) pub_local(&ws->inter[xcd][par][st][12 * li + r], act, tag_of(lp, T_INTER));
       }
       stamp(14);
-      load_d(td, layer);
-      if (me) prep_down(lp);
+      if constexpr (BB) {
+        load_d(td, layer);
+        if (me) prep_down(lp);
+      } else {
+        auto iss = [&]() SH_INLINE { load_d(td, layer); };
+        if (me) cp_prep_down(lp, iss);
+        else iss();
+      }
       stamp(2 + wv);
       ++nstep;
       // ---- down projection (cross-XCD partials)
@@ -1087,13 +1222,36 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
         if (is_live(st)) pub_cross(&ws->dpart[par][xcd][st][32 * li + 16 * tile + r], v, tag_of(lp, T_DPART));
       }
       stamp(14);
-      if (!last_layer) load_q(tq, layer + 1);
-      else if (head) load_h(tq, head_w(pi));
-      else if (!last_pos) load_q(tq, 0);
-      if (me) {
-        if (!last_layer) { ar2(lp); prep_input_next(lp, layer + 1); }
-        else if (head || last_pos) { ar2(lp); prep_final(lp); }
-        else prep_input0(pi + 1);   // code-predictor position 0: its output feeds no head
+      if constexpr (BB) {
+        if (!last_layer) load_q(tq, layer + 1);
+        else if (head) load_h(tq, head_w(pi));
+        else if (!last_pos) load_q(tq, 0);
+        if (me) {
+          if (!last_layer) { ar2(lp); prep_input_next(lp, layer + 1); }
+          else if (head || last_pos) { ar2(lp); prep_final(lp); }
+          else prep_input0(pi + 1);
+        }
+      } else {
+        // next: the following layer's input, the final norm (a head follows every position
+        // from 1 on), or, after position 0 (whose output feeds no head), position 1's input
+        auto iss = [&]() SH_INLINE {
+          if (!last_layer) load_q(tq, layer + 1);
+          else if (head) load_h(tq, head_w(pi));
+          else if (!last_pos) load_q(tq, 0);
+        };
+        if (me) {
+          if (!last_layer) {
+            ar2(lp);
+            cp_prep_vec(&ws->xl[xcd][par][wv][0], tag_of(lp, T_XL), lw(LW, layer + 1, W_LNIN), s.xres[wv], iss);
+          } else if (head || last_pos) {
+            ar2(lp);
+            cp_prep_final(lp, iss);
+          } else {
+            cp_prep_input0(pi + 1, iss);
+          }
+        } else {
+          iss();
+        }
       }
       stamp(2 + wv);
       ++nstep;
@@ -1131,7 +1289,9 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
         }
       }
       stamp(14);
-      if (!last_pos) load_q(tq, 0);
+      if constexpr (BB) {
+        if (!last_pos) load_q(tq, 0);
+      }
       if (cp) {
         int tok = 0;
         if (cp_greedy) {
@@ -1158,7 +1318,14 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
         if (me) {
           if (lane == 0) s.tok[wv][pi - 1] = tok;
           __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-          if (!last_pos) prep_input0(pi + 1);
+          if constexpr (BB) {
+            if (!last_pos) prep_input0(pi + 1);
+          }
+        }
+        if constexpr (!BB) {
+          auto iss = [&]() SH_INLINE { if (!last_pos) load_q(tq, 0); };
+          if (me && !last_pos) cp_prep_input0(pi + 1, iss);
+          else iss();
         }
       } else if (me && wg == wv) {
         const int t = select_full(pi);
