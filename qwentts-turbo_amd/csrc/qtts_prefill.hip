@@ -11,7 +11,10 @@
 //   xn  = bf16(w * bf16(x * (1 / sqrt(mean(x^2) + eps))))              RMSNorm (:59-64)
 //   q,k,v = bf16(W xn); q,k per head through RMSNorm, then
 //   rope = bf16(bf16(q * cos) + bf16(rotate_half(q) * sin))            bf16 cos/sin tables
-//   s   = bf16(bf16(q . k) * scale), p = bf16(softmax_f32(s)), att = bf16(p V)   (:185-208)
+//   s   = bf16(bf16(q . k) * scale); att = bf16((sum_j bf16(e^(s_j - m)) v_j) / sum_j e^(s_j - m))
+//         with the running max m: the softmax as flash-style attention kernels (torch's sdpa on
+//         bf16) round it, normalised after the P V product (eager torch rounds p = bf16(e / l)
+//         before it; :185-208)
 //   h1  = bf16(h + bf16(W_o att)); a = bf16(bf16(silu(bf16(W_g xn))) * bf16(W_u xn))
 //   h   = bf16(h1 + bf16(W_d a)); hidden = RMSNorm_final(h[S-1]); logits = bf16(W_head hidden)
 // The f32 sums run in MFMA order rather than the CPU's, so an f32 result can land on the other
@@ -31,9 +34,9 @@
 //   reduce_resid_norm_kernel  split-K O / down: sums, residual add and the next RMSNorm per token
 //   attn_kernel      causal GQA, 4 waves per (32-query block, query head) splitting the key
 //                    blocks: S^T = K Q^T on MFMA (each lane then holds one query's scores, so
-//                    the row max and sum stay in the lane and its partner half-wave), two passes
-//                    (row max / sum, then p = bf16(e * (1 / l)) and O^T = V^T P^T on MFMA with V^T
-//                    staged in LDS), partials merged in wave order
+//                    the row max and sum stay in the lane and its partner half-wave), one pass
+//                    with a running max, O^T += V^T P^T on MFMA with V^T read from the row-major
+//                    V block through LDS transpose reads, partials merged in wave order
 //   select_kernel    suppress mask + EOS suppression + the decode kernels' wave_select
 #include <hip/hip_runtime.h>
 #include <algorithm>
@@ -57,8 +60,6 @@ constexpr int GT = 256;                      // GEMM threads (4 waves)
 template <int TN> constexpr int bk_of() { return TN == 64 ? 128 : 64; }
 constexpr int QKVW = 4096;                   // q | k | v row of one token
 constexpr int QROW = 136;                    // LDS row of the query block: 128 dims + 16-byte pad
-constexpr int VTROW = 36;                    // LDS row of V^T: 32 keys + pad; 72 B keeps the 8-byte
-                                             // reads aligned and puts rows 8 apart 16 banks apart
 constexpr int MAX_SPLIT = 16;
 
 enum WMode { W_DIRECT, W_QKV, W_O, W_GU, W_DOWN };
@@ -501,26 +502,43 @@ __global__ void __launch_bounds__(256) reduce_resid_norm_kernel(const GemmArgs g
 
 // Causal GQA attention of S queries (positions p0 .. p0 + S - 1) over cache positions
 // 0 .. p0 + S - 1, one workgroup of AW waves per (32-query block, query head); wave w takes the
-// 32-key blocks kb = w, w + AW, ... The block's queries sit in LDS; each wave stages its K
-// block in its own LDS rows from coalesced loads. MFMA 32x32x16 with A = K rows and B = Q^T gives S^T: lane
-// (half hf, column c) holds query 32 qb + c's scores for keys 8 (r >> 2) + 4 hf + (r & 3), r < 16,
-// of each block, so a query's row max and sum stay in the lane and its partner half-wave. The
-// waves' (max, sum) pairs merge through LDS in wave order; pass 2 forms p = bf16(e * (1 / l)) and
-// O^T = V^T P^T, reusing the score registers as the B operand in place (k-index 8 hf + j of step
-// kk2 is key 16 kk2 + 8 (j >> 2) + 4 hf + (j & 3); each wave's V^T block is staged in its own LDS
-// rows [d][key] and read in that order). The AW partial O^T are added in wave order by wave 0.
-// Grid: 16 x (query blocks) workgroups, KV head = linear id mod 8 (one head per XCD's L2), the
-// longest query blocks first.
+// 32-key blocks kb = w, w + AW, ... in one pass with a running (online) softmax:
+//   * S^T = K Q^T on MFMA 32x32x16 (A = the K block staged in the wave's LDS rows, B = Q^T from
+//     the block's queries in LDS): lane (half hf, column c) holds query 32 qb + c's scores for
+//     keys 8 (r >> 2) + 4 hf + (r & 3), r < 16, so a query's row max and sum stay in the lane and
+//     its partner half-wave; s = bf16(bf16(q . k) * scale) as the reference rounds them.
+//   * The running max m moves to m' = max(m, block max); O^T and the sum l scale by e^(m - m')
+//     (skipped when no query of the wave moved); p = e^(s - m') rounded to bf16 is the B operand
+//     of O^T += V^T P^T, reusing the score registers in place (k-index 8 hf + j of step kk2 is key
+//     16 kk2 + 8 (j >> 2) + 4 hf + (j & 3)); l sums the f32 e^(s - m').
+//   * V^T comes from the V block staged row-major (16-byte writes) through the LDS transpose read
+//     ds_read_b64_tr_b16: in each 16-lane group, with M[l][j] = the 4 bf16 at lane l's address,
+//     lane i receives M[4 j + (i >> 2)][i & 3], j < 4. Lane i of group g (hf = g >> 1) passes
+//     row 16 kk2 + 4 hf (+ 8) + (i >> 2), columns 32 mb + 16 (g & 1) + 4 (i & 3): it receives
+//     dims 32 mb + 16 (g & 1) + i, keys 16 kk2 + 4 hf (+ 8) + 0..3, the A operand of O^T.
+// The softmax normalisation comes last (att = bf16(O / l)), as in flash-style kernels; the waves'
+// (m, l, O^T) merge through LDS in wave order. Grid: 16 x (query blocks) workgroups, KV head =
+// linear id mod 8 (one head per XCD's L2), the longest query blocks first.
 constexpr int AW = 4;
-constexpr int ATT_SMEM = std::max(AW * HDIM * VTROW * 2, (AW - 1) * HDIM * 32 * 4);
-static_assert(32 * QROW <= HDIM * VTROW, "a wave's LDS region holds its staged K block");
+constexpr int VROW = 160;     // LDS row of a staged V block (bf16): 320 B puts the 4 rows one
+                              // transpose read touches 16 banks apart
+constexpr int WST = 32 * VROW;                      // a wave's staging region (K block, then V)
+constexpr int ATT_Q = 32 * QROW;                    // the query block
+constexpr int ATT_SMEM = std::max((ATT_Q + AW * WST) * 2, (AW - 1) * HDIM * 32 * 4 + AW * 2 * 32 * 4);
+static_assert(32 * QROW <= WST, "a wave's LDS region holds its staged K block");
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x2 lds_tr16(const bf16_t* p) {
+  const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4s*)((__attribute__((address_space(3))) void*)p));
+  return __builtin_bit_cast(u32x2, r);
+}
 
 __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, const bf16_t* kc, const bf16_t* vc,
                                                        int layer, int max_seq, int p0, int S, bf16_t* att,
                                                        float scale) {
   __shared__ __attribute__((aligned(16))) char smem[ATT_SMEM];
-  __shared__ float sml[AW][2][32];
-  __shared__ __attribute__((aligned(16))) bf16_t sq[32 * QROW];
+  bf16_t* sq = reinterpret_cast<bf16_t*>(smem);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hf = lane >> 5, c = lane & 31;
   // XCD-aware order: workgroups go to the XCDs round-robin by linear id, so id & 7 picks the KV
   // head and each XCD's L2 holds one head's K and V; within it, the longest query blocks first
@@ -532,10 +550,9 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
   const int qpos = p0 + i;
   const int last = p0 + min(S, 32 * qb + 32) - 1;   // last key any query of the block sees
   const int nkb = last / 32 + 1;
-  bf16_t* vt = reinterpret_cast<bf16_t*>(smem) + w * HDIM * VTROW;
+  bf16_t* st = sq + ATT_Q + w * WST;   // the wave's K block, then its V block
 
-  // the block's 32 query rows go to LDS once (two 16-byte chunks per thread); every wave reads
-  // its B operands from there, which keeps 32 VGPRs free for the V prefetch
+  // the block's 32 query rows go to LDS once (two 16-byte chunks per thread)
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int ch = threadIdx.x + 64 * AW * j, qrow = ch >> 4, qcol = 8 * (ch & 15);
@@ -548,46 +565,41 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
   const bf16_t* kb_ = kc + hbase;
   const bf16_t* vb_ = vc + hbase;
 
-  // K block kb (32 keys x 128 dims) in 8 coalesced 1 KB rounds, issued a block ahead: round i,
-  // lane j loads key 32 kb + 4 i + (j >> 4), dims 8 (j & 15) .. + 7 (four whole rows per
-  // instruction; a row-per-lane load touches 32 cache lines per instruction and kept the address
-  // unit busy). Loads are unconditional from a clamped row and zeroed when staged: a load under a
-  // branch would make the compiler wait for every outstanding load, the prefetch included.
-  bf16_t* kt = vt;   // the wave's LDS region holds the K block, then (pass 2) the V^T block
-  auto loadk = [&](int kb, u32x4 (&kr)[8]) {
+  // K and V blocks (32 keys x 128 dims each) in 8 coalesced 1 KB rounds, issued a block ahead:
+  // round r, lane j loads key 32 kb + 4 r + (j >> 4), dims 8 (j & 15) .. + 7. Loads are
+  // unconditional from a clamped row and zeroed when staged: a load under a branch would make the
+  // compiler wait for every outstanding load, the prefetch included.
+  auto load = [&](const bf16_t* base, int kb, u32x4 (&rr)[8]) {
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
       const int key = 32 * kb + 4 * r + (lane >> 4);
-      kr[r] = ldw(kb_ + (size_t)(key <= last ? key : 0) * HDIM + 8 * (lane & 15));
+      rr[r] = ldw(base + (size_t)(key <= last ? key : 0) * HDIM + 8 * (lane & 15));
     }
   };
-  auto stagek = [&](int kb, const u32x4 (&kr)[8]) {
+  auto stage = [&](int kb, const u32x4 (&rr)[8], int pitch) {
     if (32 * kb + 31 <= last) {   // wave-uniform: a whole block needs no zeroing
 #pragma unroll
-      for (int r = 0; r < 8; ++r)
-        *reinterpret_cast<u32x4*>(&kt[(4 * r + (lane >> 4)) * QROW + 8 * (lane & 15)]) = kr[r];
+      for (int r = 0; r < 8; ++r) *reinterpret_cast<u32x4*>(&st[(4 * r + (lane >> 4)) * pitch + 8 * (lane & 15)]) = rr[r];
     } else {
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
         const int row = 4 * r + (lane >> 4);
-        *reinterpret_cast<u32x4*>(&kt[row * QROW + 8 * (lane & 15)]) =
-            32 * kb + row <= last ? kr[r] : u32x4{0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4*>(&st[row * pitch + 8 * (lane & 15)]) = 32 * kb + row <= last ? rr[r] : u32x4{0u, 0u, 0u, 0u};
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   };
   auto scores = [&](int kb, float (&sc)[16]) {
-    // two independent 4-step MFMA chains (even and odd 16-dim steps), added at the end
+    // two independent 4-step MFMA chains (even and odd 16-dim steps), added at the end; Q^T
+    // (query c, dims 16 kk + 8 hf ..) and K (key c, the same dims) from LDS, both with row pitch
+    // QROW; the offset is opaque so the reads stay in the loop instead of being hoisted
     f32x16 acc, acc2;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = acc2[r] = 0.0f;
-    // Q^T operand (query c, dims 16 kk + 8 hf ..) from LDS; the offset is made opaque so the
-    // reads stay in the loop instead of being hoisted into 32 live registers
-    // and the K operand (key c, the same dims) from the staged block; both row pitches are QROW
     int qo = c * QROW + 8 * hf;
     asm volatile("" : "+v"(qo));
     const bf16_t* qp = &sq[qo];
-    const bf16_t* kp = &kt[qo];
+    const bf16_t* kp = &st[qo];
 #pragma unroll
     for (int kk = 0; kk < 8; kk += 2) {
       const u32x4 q0 = *reinterpret_cast<const u32x4*>(qp + 16 * kk);
@@ -616,138 +628,104 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
   constexpr float L2E = 1.4426950408889634f;
   auto ex = [](float s, float nm) { return __builtin_amdgcn_exp2f(fmaf(s, L2E, nm)); };
 
-  // pass 1: this wave's row maximum and softmax denominator
   float m = -INFINITY, l = 0.0f;
-  u32x4 kq[8];
-  loadk(w, kq);
-  auto pass1 = [&](int kb) {
-    stagek(kb, kq);
-    loadk(kb + AW, kq);
-    float sc[16];
-    scores(kb, sc);
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");   // K reads before the next staging
-    float bm = sc[0];
-#pragma unroll
-    for (int r = 1; r < 16; ++r) bm = fmaxf(bm, sc[r]);
-    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-    // (no branch around the MFMAs: a fully masked block leaves m and l unchanged; masked scores
-    // are -inf, whose exp is 0, and a still fully masked row subtracts 0 instead of -inf)
-    const float mn = fmaxf(m, bm);
-    const float nm = mn == -INFINITY ? 0.0f : -mn * L2E;
-    float add = 0.0f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) add += ex(sc[r], nm);
-    l = m == -INFINITY ? add : l * __expf(m - mn) + add;
-    m = mn;
-  };
-  for (int kb = w; kb < nkb; kb += AW) pass1(kb);
-  l += __shfl_xor(l, 32, 64);
-  if (hf == 0) {
-    sml[w][0][c] = m;
-    sml[w][1][c] = l;
-  }
-  __syncthreads();
-  {
-    float M = -INFINITY;
-#pragma unroll
-    for (int v = 0; v < AW; ++v) M = fmaxf(M, sml[v][0][c]);
-    float L = 0.0f;
-#pragma unroll
-    for (int v = 0; v < AW; ++v) {
-      const float mv = sml[v][0][c];
-      L += mv == -INFINITY ? 0.0f : sml[v][1][c] * __expf(mv - M);
-    }
-    m = M;
-    l = L;
-  }
-  const float rl = l > 0.0f ? 1.0f / l : 0.0f;   // softmax scale (torch multiplies by 1 / sum too)
-  const float nm = m == -INFINITY ? 0.0f : -m * L2E;
-
-  // pass 2: p = bf16(e * (1 / l)), O^T += V^T P^T over this wave's blocks
   f32x16 o[4];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[mb][r] = 0.0f;
-  // staging: lane (group dgr = lane >> 4, pair kp2 = lane & 15) moves keys 2 kp2, 2 kp2 + 1 of dims
-  // 32 dd + 8 dgr + 0..7: the four groups write rows 8 apart, i.e. different banks
-  const int kp2 = lane & 15, dgr = lane >> 4;
-  // V rows 2 kp2, 2 kp2 + 1 of block kb, dims 32 dd + 8 dgr .. + 7, issued a block ahead into vr
-  // (unconditional loads from clamped rows, zeroed when staged: see loadk)
-  u32x4 vr[8];
-  auto loadv = [&](int kb) {
-    const int k0 = 32 * kb + 2 * kp2;
-    const bf16_t* v0 = vb_ + (size_t)(k0 <= last ? k0 : 0) * HDIM + 8 * dgr;
-    const bf16_t* v1 = vb_ + (size_t)(k0 + 1 <= last ? k0 + 1 : 0) * HDIM + 8 * dgr;
-#pragma unroll
-    for (int dd = 0; dd < 4; ++dd) {
-      vr[dd] = ldw(v0 + 32 * dd);
-      vr[4 + dd] = ldw(v1 + 32 * dd);
-    }
-  };
-  loadk(w, kq);
-  loadv(w);
-  auto pass2 = [&](int kb) {
-    stagek(kb, kq);
-    loadk(kb + AW, kq);
+  // transpose-read addresses of this lane (see above), relative to the staged V block
+  const int gi = lane & 15, g = lane >> 4;
+  const int tr_off = (4 * (g >> 1) + (gi >> 2)) * VROW + 16 * (g & 1) + 4 * (gi & 3);
+  u32x4 kr[8], vr[8];
+  load(kb_, w, kr);
+  load(vb_, w, vr);
+  for (int kb = w; kb < nkb; kb += AW) {
+    stage(kb, kr, QROW);
+    load(kb_, kb + AW, kr);
     float sc[16];
     scores(kb, sc);
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");   // K reads before the V^T staging
-    // stage the prefetched V rows of this block transposed into vt[d][key], then issue the next
-    {
-      const int k0 = 32 * kb + 2 * kp2;
-      const bool whole = 32 * kb + 31 <= last;   // wave-uniform: a whole block needs no zeroing
-      const bool ok0 = whole || k0 <= last, ok1 = whole || k0 + 1 <= last;
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");   // K reads before the V staging
+    stage(kb, vr, VROW);
+    load(vb_, kb + AW, vr);
+    // running max; a fully masked row so far keeps m = -inf and adds nothing
+    float bm = sc[0];
 #pragma unroll
-      for (int dd = 0; dd < 4; ++dd) {
-        const u32x4 a = ok0 ? vr[dd] : u32x4{0u, 0u, 0u, 0u};
-        const u32x4 b = ok1 ? vr[4 + dd] : u32x4{0u, 0u, 0u, 0u};
+    for (int r = 1; r < 16; ++r) bm = fmaxf(bm, sc[r]);
+    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    const float mn = fmaxf(m, bm);
+    const float nm = mn == -INFINITY ? 0.0f : -mn * L2E;
+    if (__builtin_amdgcn_ballot_w64(mn != m) != 0ull) {
+      const float al = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m - mn) * L2E);
+      l *= al;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int d = 32 * dd + 8 * dgr + 2 * e;
-          *reinterpret_cast<uint32_t*>(&vt[d * VTROW + 2 * kp2]) = (a[e] & 0xffffu) | (b[e] << 16);
-          *reinterpret_cast<uint32_t*>(&vt[(d + 1) * VTROW + 2 * kp2]) = (a[e] >> 16) | (b[e] & 0xffff0000u);
-        }
-      }
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[mb][r] *= al;
     }
-    loadv(kb + AW);
-    // the rows are this wave's own: order the writes before the reads within the wave
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    m = mn;
+    float e[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      e[r] = ex(sc[r], nm);
+      l += e[r];
+    }
 #pragma unroll
     for (int kk2 = 0; kk2 < 2; ++kk2) {
       u32x4 pb;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        pb[j] = pack_bh(ex(sc[8 * kk2 + 2 * j], nm) * rl, ex(sc[8 * kk2 + 2 * j + 1], nm) * rl);
+      for (int j = 0; j < 4; ++j) pb[j] = pack_bh(e[8 * kk2 + 2 * j], e[8 * kk2 + 2 * j + 1]);
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
-        const bf16_t* vr = &vt[(32 * mb + c) * VTROW + 16 * kk2 + 4 * hf];
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(vr);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(vr + 8);
+        const bf16_t* vp = &st[16 * kk2 * VROW + 32 * mb + tr_off];
+        const u32x2 lo = lds_tr16(vp);
+        const u32x2 hi = lds_tr16(vp + 8 * VROW);
         const u32x4 av = {lo[0], lo[1], hi[0], hi[1]};
         o[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(av), as_bf8(pb), o[mb], 0, 0, 0);
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  };
-  for (int kb = w; kb < nkb; kb += AW) pass2(kb);
-  // partial O^T of waves 1.. to LDS (the V^T rows are dead), added in wave order by wave 0
-  __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");   // V reads before the next K staging
+  }
+  l += __shfl_xor(l, 32, 64);
+
+  // merge the waves: M = max m_w, L = sum l_w e^(m_w - M), O = sum O_w e^(m_w - M) (wave order)
+  __syncthreads();   // every wave's staging region is dead
   float* ob = reinterpret_cast<float*>(smem);
+  float* sml = ob + (AW - 1) * HDIM * 32;   // [AW][2][32]
+  if (hf == 0) {
+    sml[(w * 2) * 32 + c] = m;
+    sml[(w * 2 + 1) * 32 + c] = l;
+  }
+  __syncthreads();
+  float M = -INFINITY;
+#pragma unroll
+  for (int v = 0; v < AW; ++v) M = fmaxf(M, sml[(v * 2) * 32 + c]);
+  const float sw = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m - M) * L2E);
   if (w > 0) {
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) ob[((w - 1) * 64 + mb * 16 + r) * 64 + lane] = o[mb][r];
+      for (int r = 0; r < 16; ++r) ob[((w - 1) * 64 + mb * 16 + r) * 64 + lane] = o[mb][r] * sw;
   }
   __syncthreads();
   if (w > 0 || !qok) return;
+  float L = 0.0f;
+#pragma unroll
+  for (int v = 0; v < AW; ++v) {
+    const float mv = sml[(v * 2) * 32 + c];
+    L += mv == -INFINITY ? 0.0f : sml[(v * 2 + 1) * 32 + c] * __builtin_amdgcn_exp2f((mv - M) * L2E);
+  }
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[mb][r] *= sw;
 #pragma unroll 1
   for (int v = 1; v < AW; ++v)
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) o[mb][r] += ob[((v - 1) * 64 + mb * 16 + r) * 64 + lane];
+  const float rl = L > 0.0f ? 1.0f / L : 0.0f;
   // O^T layout: column = query c, register r of block mb = dim 32 mb + 8 (r >> 2) + 4 hf + (r & 3)
   bf16_t* op = att + (size_t)i * (NQH * HDIM) + hq * HDIM;
 #pragma unroll
@@ -756,8 +734,8 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
     for (int rq = 0; rq < 4; ++rq) {
       const int d0 = 32 * mb + 8 * rq + 4 * hf;
       u32x2 pk;
-      pk[0] = pack_bh(o[mb][4 * rq], o[mb][4 * rq + 1]);
-      pk[1] = pack_bh(o[mb][4 * rq + 2], o[mb][4 * rq + 3]);
+      pk[0] = pack_bh(o[mb][4 * rq] * rl, o[mb][4 * rq + 1] * rl);
+      pk[1] = pack_bh(o[mb][4 * rq + 2] * rl, o[mb][4 * rq + 3] * rl);
       *reinterpret_cast<u32x2*>(op + d0) = pk;
     }
 }
