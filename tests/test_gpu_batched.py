@@ -14,18 +14,20 @@ Two kernels serve several streams (BatchedTTSDecoder ``mode``):
   one element); with N(1, 0.02) gains (the fixtures' non-inert layers) later layers spread such a
   flip to ~5e-3 - 9e-3 rel-L2 of the final hidden, as they spread an f32-level perturbation of the
   f64 oracle itself. So the shared backbone is held to rel-L2 1e-3 at literal gains and to
-  north_star's 1e-2 at N(1, 0.02), with the group-0 ids identical (their top-2 gaps logged) and the
-  code-predictor frame identical to batch 1's from the same backbone hidden. The code predictor
-  (f32 in both kernels) is held to identical ids and combine.
+  north_star's 1e-2 at N(1, 0.02), with the group-0 ids identical (their top-2 gaps logged). The
+  code predictor (f32 in both kernels, summed in different orders) is held to identical ids and
+  combine, except where a decision is tipped by a last-bit difference (the oracle's own choice
+  under a one-ulp move of one logit, checked when it occurs).
 """
 import json
+import math
 
 import numpy as np
 import pytest
 import torch
 
 from golden import cases
-from oracle.qtts_oracle import rel_l2
+from oracle.qtts_oracle import TalkerOracle, TalkerWeights, head_logits, rb, rel_l2, sample_token
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
@@ -236,16 +238,56 @@ def test_backbone_streams_reject_bad_arguments(pkg):
     assert lead.position() == 0 and other.position() == 16
 
 
+def _bf16_step(v: float, up: bool) -> float:
+    """The neighbouring bf16 value of the bf16 value v (towards +inf when up)."""
+    b = int(torch.tensor([v], dtype=torch.bfloat16).view(torch.int16)[0]) & 0xFFFF
+    b = b + (1 if (up == (b < 0x8000)) else -1) if v != 0.0 else (0x0001 if up else 0x8001)
+    return float(torch.tensor([b if b < 0x8000 else b - 0x10000], dtype=torch.int16).view(torch.bfloat16)[0])
+
+
+def _cp_last_bit_choice(sd, hid, g0, ids_ref, ids_got, j, sample, kw, seed):
+    """Group j (1..15) of a code-predictor frame, where two kernels chose ids_ref[j] and ids_got[j]
+    after agreeing on groups 1..j-1. The oracle (kernel policy, f64 sums), teacher-forced with the
+    agreed ids, must choose ids_ref[j] from its bf16 logits, and ids_got[j] once one logit moves by
+    one bf16 ulp (ids_got[j] up or ids_ref[j] down): a decision that a last-bit difference of one
+    sum tips, through the top-2 order, the top-k boundary or a greedy tie. Returns the move."""
+    tw = TalkerWeights.from_state_dict(sd, 1, 2)
+    orc = TalkerOracle(tw, max_seq=64, policy="kernel")
+    orc.cp.reset()
+    orc.cp.step(rb(hid.float().cpu()).to(torch.bfloat16), pos=0)
+    h, _ = orc.cp.step(orc.bb_emb[g0], pos=1)
+    for g in range(j - 1):
+        h, _ = orc.cp.step(orc.cp_emb[g][ids_ref[g + 1]], pos=g + 2)
+    lg = head_logits(tw.cp_heads[j - 1], h).float()
+
+    def pick(x):
+        return sample_token(x, sample, kw["temperature"], kw["top_k"], 1.0, None, seed=seed,
+                            frame_step=kw["frame_step"], group=j)
+
+    assert pick(lg) == ids_ref[j], f"group {j}: the oracle picks {pick(lg)}, batch 1 {ids_ref[j]}"
+    for idx, up, label in ((ids_got[j], True, "kernel's id one ulp up"), (ids_ref[j], False, "batch 1's id one ulp down")):
+        moved = lg.clone()
+        moved[idx] = _bf16_step(float(lg[idx]), up)
+        if pick(moved) == ids_got[j]:
+            return label
+    raise AssertionError(f"group {j}: {ids_got[j]} is not the oracle's choice under a one-ulp move of either logit")
+
+
 @pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("n,sample", [(3, False), (9, True), (8, False)], ids=["greedy3", "sampled9", "greedy8"])
 def test_cp_frames_streams_match_batch1(pkg, n, sample, mode):
     """Code-predictor frames of n streams through BatchedTTSDecoder.cp_frames (up to 8 per launch)
-    against the batch-1 frame() of each stream with the same key (seed + s): the 15 group ids and
-    the combined next input identical (in both modes: the code predictor accumulates in f32 in
-    either kernel, and the combine is a bf16 sum of the rows the ids select); 9 streams take two
-    launches; the sampled case draws every group with temperature and top-k."""
+    against the batch-1 frame() of each stream with the same key (seed + s); 9 streams take two
+    launches; the sampled case draws every group with temperature and top-k.
+
+    per_xcd: the 15 group ids and the combined next input identical (the batch-1 arithmetic).
+    shared: the same, except where the two kernels' f32 sums (different summation orders) tip a
+    last-bit decision: at the first differing group the oracle, teacher-forced with the agreed
+    earlier ids, must choose batch 1's id, and the shared kernel's once one bf16 logit moves by one
+    ulp (every later group of that frame starts from different inputs and is not compared)."""
     cfg = pkg.SyntheticConfig(n_bb_layers=1, n_cp_layers=2, n_groups=15)
-    dsd = {k: v.cuda() for k, v in pkg.synthetic_state_dict(seed=40 + n, cfg=cfg).items()}
+    sd = pkg.synthetic_state_dict(seed=40 + n, cfg=cfg)
+    dsd = {k: v.cuda() for k, v in sd.items()}
     dec = pkg.BatchedTTSDecoder(dsd, n, max_seq_len=16, mode=mode)
     g = torch.Generator().manual_seed(n)
     hid = torch.randn(n, 1024, generator=g).cuda()
@@ -264,6 +306,14 @@ def test_cp_frames_streams_match_batch1(pkg, n, sample, mode):
         cp.frame(hid[s].contiguous(), g0[s:s + 1], text[s].contiguous(), t1, c1, -1, torch.zeros(1, **i32), sample,
                  kw["temperature"], kw["top_k"], 1.0, kw["seed"] + s, kw["frame_step"])
         torch.cuda.synchronize()
+        if mode == "shared" and not torch.equal(toks[s], t1):
+            ref, got = t1.tolist(), toks[s].tolist()
+            j = next(k for k in range(16) if ref[k] != got[k])
+            assert j >= 1, f"stream {s}: group 0 id is the input and must be equal"
+            how = _cp_last_bit_choice(sd, hid[s], int(g0[s]), ref, got, j, sample, kw, kw["seed"] + s)
+            print(f"stream {s}: first difference at group {j} ({ref[j]} vs {got[j]}): the oracle's choice "
+                  f"with the {how}", flush=True)
+            continue
         assert torch.equal(toks[s], t1), f"stream {s}: {toks[s].tolist()} vs {t1.tolist()}"
         assert torch.equal(comb[s], c1), f"stream {s}: combined input differs"
     dec.check_error()
