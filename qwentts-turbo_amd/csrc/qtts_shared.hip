@@ -264,7 +264,9 @@ template <bool BB>
 __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
   __shared__ SLds s;
   // norm statistics in f64 for the backbone (its bf16 residual), f32 in the code predictor
-  using A = std::conditional_t<BB, double, float>;
+  // norms and their sums in f32 for both models: the projections already sum in f32 (MFMA), so
+  // the batch-1 backbone's f64 norms would buy no accuracy here, only VALU time and registers
+  using A = float;
   // lane and thread index, re-derived opaquely at every step so that offsets computed from them
   // are recomputed where used instead of being hoisted out of the step loop and spilled
   int lane = threadIdx.x & 63;
