@@ -1205,12 +1205,16 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   // attention over the whole context in every workgroup when it fits one pass of the math
   // waves (attention and O projection then share a step); split into chunks otherwise
   auto att_local = [&](int pi) { return SIO(pos0) + pi + 1 <= KVGeo<BB>::SUB; };
+  // the code-predictor frame's position 0 feeds no head: of its last layer only the K/V entry
+  // (the QKV step) is read later, so its attention, MLP and final norm are not computed
+  auto kv_only = [&](int pi, int layer) { return a.cp_frame && pi == 0 && layer == NL - 1 && a.n_pos > 1; };
   auto walk = [&](auto&& act) {
     act(S_PRO, 0, 0); stamp();
     step_barrier();
     for (int pi = 0; pi < a.n_pos; ++pi) {
       for (int layer = 0; layer < NL; ++layer) {
         act(S_QKV, pi, layer); stamp(); step_barrier();
+        if (kv_only(pi, layer)) continue;
         act(S_ATT, pi, layer); stamp(); step_barrier();
         if (!att_local(pi)) { act(S_O, pi, layer); stamp(); step_barrier(); }
         act(S_GU, pi, layer); stamp(); step_barrier();
@@ -1263,6 +1267,14 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           prep_att(lp, layer, q.pos, q.C);
           load_qk_gains(nl);
           if (layer == NL - 1 && !q.last_pos) load_rope(q.pos + 1);
+          if (kv_only(pi, layer)) {
+            // position 1's input, in place of this position's DOWN step; the math waves read
+            // xn before publishing the QKV rows prep_att has waited for, so xn is free
+            prep_input0(pi + 1);
+            if (lead) comb_add(true);
+            load_gain_pairs(g_in, lw(LW, NL > 1 ? 1 : 0, W_LNIN));
+            load_gain_pairs(g_post, lw(LW, 0, W_LNPOST));
+          }
           break;
         case S_ATT:
           // the math waves' attention synchronises the whole workgroup (passes + 2 times);
@@ -1430,6 +1442,12 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           break;
         case S_QKV:
           qkv_stage(layer);
+          if (kv_only(pi, layer)) {
+            // the next step is position 1's layer-0 QKV
+            tk = TileKV<BB>{};
+            load_qkv<BB>(tq, LW, 0, xcd, li, mw, lane);
+            break;
+          }
           if (q.has_chunk) load_kv<BB>(tk, a, SIO(kc), SIO(vc), layer, xcd, q.c0, min(q.c1, q.L - 1), mw, lane);
           else tk = TileKV<BB>{};
           if (q.local) load_o<BB>(to, LW, layer, xcd, li, mw, lane);
