@@ -53,6 +53,13 @@ __device__ __forceinline__ bf16_t f2bf(float f) {
   return (bf16_t)((u & 0x7fffffffu) > 0x7f800000u ? qnan : rne);
 }
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+// two values packed as one bf16 pair (lo in bits 0..15) with gfx950's conversion instruction
+// (v_cvt_pk_bf16_f32, round to nearest even as f2bf, one VALU op for both)
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t f2bf2(float lo, float hi) {
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
 
 // 8 bf16 weights (one 16-byte piece) dot 8 activations, accumulated in f64 (each product is
 // exact in f64; only the accumulation rounds, at ~1e-16 relative).

@@ -188,6 +188,14 @@ __device__ __forceinline__ void split3(float x, bf16_t& h, bf16_t& m, bf16_t& l)
   m = f2bf(r1);
   l = f2bf(r1 - bf2f(m));
 }
+// the same split of two values as packed pairs with the conversion instruction (three per pair
+// instead of about forty); each residual is exact in f32, so the pieces equal split3's
+__device__ __forceinline__ void split3x2(float x0, float x1, uint32_t& h, uint32_t& m, uint32_t& l) {
+  h = f2bf2(x0, x1);
+  const float r0 = x0 - bflo(h), r1 = x1 - bfhi(h);
+  m = f2bf2(r0, r1);
+  l = f2bf2(r0 - bflo(m), r1 - bfhi(m));
+}
 
 // Read npair 16-byte pairs into registers (pair k of this lane: i = lane + 64 k < npair) until
 // every tag matches, one round of loads in flight, re-issuing only the pairs still pending: for
@@ -380,12 +388,22 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
   };
   // projection input of this wave's stream: element e of piece p at xb[p][wv][e]
   auto put_pair = [&](int e, float v0, float v1) {
-    bf16_t h0, m0, l0, h1, m1, l1;
-    split3(v0, h0, m0, l0);
-    split3(v1, h1, m1, l1);
-    *reinterpret_cast<uint32_t*>(&s.xb[0][wv][e]) = (uint32_t)h0 | ((uint32_t)h1 << 16);
-    *reinterpret_cast<uint32_t*>(&s.xb[1][wv][e]) = (uint32_t)m0 | ((uint32_t)m1 << 16);
-    *reinterpret_cast<uint32_t*>(&s.xb[2][wv][e]) = (uint32_t)l0 | ((uint32_t)l1 << 16);
+    uint32_t h, m, l;
+    if constexpr (BB) {
+      // the backbone instantiation keeps the bit-manipulation rounding: its register allocation
+      // spills with the shorter sequence (a spill reload waits behind the in-flight weight tile)
+      bf16_t h0, m0, l0, h1, m1, l1;
+      split3(v0, h0, m0, l0);
+      split3(v1, h1, m1, l1);
+      h = (uint32_t)h0 | ((uint32_t)h1 << 16);
+      m = (uint32_t)m0 | ((uint32_t)m1 << 16);
+      l = (uint32_t)l0 | ((uint32_t)l1 << 16);
+    } else {
+      split3x2(v0, v1, h, m, l);
+    }
+    *reinterpret_cast<uint32_t*>(&s.xb[0][wv][e]) = h;
+    *reinterpret_cast<uint32_t*>(&s.xb[1][wv][e]) = m;
+    *reinterpret_cast<uint32_t*>(&s.xb[2][wv][e]) = l;
   };
   auto put_vec = [&](const float (&y)[16]) {
 #pragma unroll
