@@ -136,7 +136,18 @@ constexpr int TRACE_STEPS = 1024;
 struct Lds {
   union {
     double red[NMATH][2][8][64];   // chunked attention partials [wave][head][dim % 8][lane group * 16 + dim / 8]
-    float vst[16][HDIM];           // code-predictor local attention: V of the context positions
+    struct {
+      float vst[16][HDIM];         // code-predictor local attention: V of the context positions
+      // code-predictor frame, two-column pass: the operands of position 1 (column 1; position
+      // 0 uses the arrays below)
+      alignas(16) float xn_1[HID];
+      alignas(16) float hn_1[HID];
+      alignas(16) float inter_1[XI];
+      alignas(16) float q_1[2][HDIM];
+      alignas(16) float knew_1[HDIM];
+      alignas(16) float vnew_1[HDIM];
+      alignas(16) float attn_1[2 * HDIM];
+    };
   };
   double pl[2][16];                // (unused by the f32 code-predictor attention; kept for layout)
   alignas(16) float plf[2][16];    // code-predictor local attention: p_j = exp(s_j - M) per head
@@ -158,6 +169,8 @@ struct Lds {
   // poller-only from here
   alignas(16) float xres[HID];
   alignas(16) float h1res[HID];
+  alignas(16) float xres_1[HID];   // two-column pass: position 1's residual stream
+  alignas(16) float h1res_1[HID];
   alignas(16) float comb[HID];   // code-predictor frame (workgroup 0): running embedding combine
   alignas(16) float stage[MAXC * APS > MAXV ? MAXC * APS : MAXV];
   uint32_t pen_bits[MAXV / 32];
@@ -189,6 +202,11 @@ __device__ __forceinline__ const bf16_t* lw(const TTSLayerWeights* layers, int l
 template <bool BB> struct KVGeo;
 template <> struct KVGeo<true> { static constexpr int JJ = 4, PPP = 1, SUB = 64, CSUB = 64; };
 template <> struct KVGeo<false> { static constexpr int JJ = 1, PPP = 2, SUB = 16, CSUB = 2; };
+// Column of the code-predictor frame's two-column pass (positions 0 and 1 share one pass over
+// the weights): Col0 = position 0 (and every single-column step), Col1 = position 1.
+using Col0 = std::integral_constant<int, 0>;
+using Col1 = std::integral_constant<int, 1>;
+
 template <bool BB> struct TileKV {
   u32x4 k[KVGeo<BB>::JJ * KVGeo<BB>::PPP];
   u32x4 v[KVGeo<BB>::JJ * KVGeo<BB>::PPP];
@@ -449,6 +467,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   //   qn / kn: q/k-norm gains of head channels lane, lane + 64; rc / rsn: their cos / sin
   uint32_t g_in[8], g_post[8], g_fin[8];
   float qn[2], kn[2], rc[2], rsn[2];
+  float rc1[2], rsn1[2];   // two-column pass: rotary of position 1
   auto load_gain_pairs = [&](uint32_t (&g)[8], const bf16_t* src) {
     const auto* p = gmem(reinterpret_cast<const uint32_t*>(src));
 #pragma unroll
@@ -460,13 +479,28 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     qn[0] = ldbf(q + lane); qn[1] = ldbf(q + lane + 64);
     kn[0] = ldbf(k + lane); kn[1] = ldbf(k + lane + 64);
   };
-  auto load_rope = [&](int pos) {
+  auto load_rope_to = [&](int pos, float (&c)[2], float (&sn)[2]) QTTS_INLINE {
     const size_t row = (size_t)rot_row(lane, pos) * HDIM;   // channel lane + 64 shares the row
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      rc[j] = ldbf(a.cos_t + row + lane + 64 * j);
-      rsn[j] = ldbf(a.sin_t + row + lane + 64 * j);
+      c[j] = ldbf(a.cos_t + row + lane + 64 * j);
+      sn[j] = ldbf(a.sin_t + row + lane + 64 * j);
     }
+  };
+  auto load_rope = [&](int pos) { load_rope_to(pos, rc, rsn); };
+  // LDS operands of a column (Col0: the single-column arrays) and its exchange-buffer parity:
+  // column 1 publishes with position 1's layer-pass tags into the parity buffer column 0 does
+  // not use in the same step (by the exchange chain, every reader of a buffer is done before
+  // the next step's writers reach it)
+  constexpr bool DUO_OK = !BB && !XL;
+  auto cxres = [&](auto c) QTTS_INLINE -> float* { if constexpr (decltype(c)::value == 1) return s.xres_1; else return s.xres; };
+  auto cxn = [&](auto c) QTTS_INLINE -> float* { if constexpr (decltype(c)::value == 1) return s.xn_1; else return s.xn; };
+  auto ch1res = [&](auto c) QTTS_INLINE -> float* { if constexpr (decltype(c)::value == 1) return s.h1res_1; else return s.h1res; };
+  auto chn = [&](auto c) QTTS_INLINE -> float* { if constexpr (decltype(c)::value == 1) return s.hn_1; else return s.hn; };
+  auto cinter = [&](auto c) QTTS_INLINE -> float* { if constexpr (decltype(c)::value == 1) return s.inter_1; else return s.inter; };
+  auto cattn = [&](auto c) QTTS_INLINE -> float* { if constexpr (decltype(c)::value == 1) return s.attn_1; else return s.attn; };
+  auto cpar = [&](int lp, auto c) QTTS_INLINE -> int {
+    if constexpr (decltype(c)::value == 1) return ((lp - NL) & 1) ^ 1; else return lp & 1;
   };
   // RMSNorm statistic of the lane-distributed 1024-vector: 1 / sqrt(mean(x^2) + eps) in f64
   auto rstd_of = [&](const float (&xv)[16]) -> A {
@@ -498,7 +532,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   };
 
   // ---- poller: input of layer 0 of position pi (embedding source) -> xres, xn
-  auto prep_input0 = [&](int pi) {
+  auto prep_input0 = [&](int pi, auto col) QTTS_INLINE {
     A gd[16];
     gains_d(g_in, gd);
     float xv[16];
@@ -518,35 +552,37 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) { const uint32_t w = p[lane + 64 * k]; xv[2 * k] = bflo(w); xv[2 * k + 1] = bfhi(w); }
     }
-    store_pairs(s.xres, xv);
+    store_pairs(cxres(col), xv);
     float y[16];
     normed(xv, gd, y);
-    store_pairs(s.xn, y);
+    store_pairs(cxn(col), y);
   };
 
   // ---- poller (code-predictor frame, workgroup 0): the embedding combine, accumulated as each
   // position's input row arrives in xres (bf16 rounding after each add, in the order
   // emb_bb[g0] + emb_0[t_0] + emb_1[t_1] + ...; generator.py:356-362)
-  auto comb_add = [&](bool first) {
+  auto comb_add = [&](bool first, auto col) QTTS_INLINE {
+    const float* xr = cxres(col);
     for (int k = 0; k < 8; ++k) {
       const int e = 2 * (lane + 64 * k);
-      const float2 x = *reinterpret_cast<const float2*>(&s.xres[e]);
+      const float2 x = *reinterpret_cast<const float2*>(&xr[e]);
       const float2 c = *reinterpret_cast<const float2*>(&s.comb[e]);
       *reinterpret_cast<float2*>(&s.comb[e]) = first ? x : make_float2(rbf(c.x + x.x), rbf(c.y + x.y));
     }
   };
 
   // ---- poller: AR2 of layer pass lp (down partials + residual) -> xl slots
-  auto ar2 = [&](int lp) QTTS_INLINE {
-    const int par = lp & 1;
+  auto ar2 = [&](int lp, auto col) QTTS_INLINE {
+    const int par = cpar(lp, col);
+    const float* h1r = ch1res(col);
     if constexpr (XL) {
       // the workgroup's 8 row groups: rows 32 li + 2 (lane + 64 k) + {0, 1}
       double sm[4];
       float r[4];
 #pragma unroll
       for (int k = 0; k < 2; ++k) {
-        r[2 * k] = s.h1res[32 * li + 2 * (lane + 64 * k)];
-        r[2 * k + 1] = s.h1res[32 * li + 2 * (lane + 64 * k) + 1];
+        r[2 * k] = h1r[32 * li + 2 * (lane + 64 * k)];
+        r[2 * k + 1] = h1r[32 * li + 2 * (lane + 64 * k) + 1];
       }
       poll_sum8_rows(P, ws->dpart[par], 32 * li, tag_of(lp, T_DPART), sm);
 #pragma unroll
@@ -558,7 +594,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       return;
     }
     const int row = 32 * li + 2 * (lane & 15);
-    const float r0 = s.h1res[row], r1 = s.h1res[row + 1];
+    const float r0 = h1r[row], r1 = h1r[row + 1];
     double s0, s1;
     poll_sum8(P, ws->dpart[par], 32 * li, tag_of(lp, T_DPART), s0, s1);
     if (lane < 16) {
@@ -569,21 +605,21 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     }
   };
   // ---- poller: next layer input (after ar2 of lp) -> xres, xn
-  auto prep_input_next = [&](int lp) {
+  auto prep_input_next = [&](int lp, auto col) QTTS_INLINE {
     float xv[16], y[16];
     A gd[16];
     gains_d(g_in, gd);
-    poll_vec_regs(P, ws->xl[xcd][lp & 1], tag_of(lp, T_XL), xv);
-    store_pairs(s.xres, xv);
+    poll_vec_regs(P, ws->xl[xcd][cpar(lp, col)], tag_of(lp, T_XL), xv);
+    store_pairs(cxres(col), xv);
     normed(xv, gd, y);
-    store_pairs(s.xn, y);
+    store_pairs(cxn(col), y);
   };
   // ---- poller: final norm (after ar2 of lp) -> hb (bf16-rounded), outputs
-  auto prep_final = [&](int lp) {
+  auto prep_final = [&](int lp, auto col) QTTS_INLINE {
     float xv[16], y[16];
     A gd[16];
     gains_d(g_fin, gd);
-    poll_vec_regs(P, ws->xl[xcd][lp & 1], tag_of(lp, T_XL), xv);
+    poll_vec_regs(P, ws->xl[xcd][cpar(lp, col)], tag_of(lp, T_XL), xv);
     store_pairs(s.xres, xv);
     normed(xv, gd, y);
     if (lead) {
@@ -618,9 +654,13 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
   };
-  auto prep_att = [&](int lp, int layer, int pos, int C) {
-    const int par = lp & 1;
-    const A cl = rc[0], ch = rc[1], sl = rsn[0], sh = rsn[1];
+  auto prep_att = [&](int lp, int layer, int pos, int C, auto col) QTTS_INLINE {
+    constexpr bool c1 = decltype(col)::value == 1;
+    const int par = cpar(lp, col);
+    const A cl = c1 ? rc1[0] : rc[0], ch = c1 ? rc1[1] : rc[1], sl = c1 ? rsn1[0] : rsn[0], sh = c1 ? rsn1[1] : rsn[1];
+    float (&sq)[2][HDIM] = c1 ? s.q_1 : s.q;
+    float* skn = c1 ? s.knew_1 : s.knew;
+    float* svn = c1 ? s.vnew_1 : s.vnew;
     float v[8];   // [head][j]: head 0, 1 = q, 2 = k, 3 = v; j = 0: channel c, 1: channel c + 64
     {
       const uint32_t o = ws_off(P, ws->qkv[xcd][par]);
@@ -640,12 +680,12 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       outh[h] = (float)(nl * sh + nh * ch);
     }
     const int c = lane;
-    s.q[0][c] = outl[0]; s.q[0][c + 64] = outh[0];
-    s.q[1][c] = outl[1]; s.q[1][c + 64] = outh[1];
+    sq[0][c] = outl[0]; sq[0][c + 64] = outh[0];
+    sq[1][c] = outl[1]; sq[1][c + 64] = outh[1];
     float kl = outl[2], kh = outh[2], vl = v[6], vh = v[7];
     if constexpr (BB) { kl = rbf(kl); kh = rbf(kh); vl = rbf(vl); vh = rbf(vh); }
-    s.knew[c] = kl; s.knew[c + 64] = kh;
-    s.vnew[c] = vl; s.vnew[c + 64] = vh;
+    skn[c] = kl; skn[c + 64] = kh;
+    svn[c] = vl; svn[c + 64] = vh;
     if (C - 1 >= li && C - 1 < li + NSUB) {
       const size_t off = (((size_t)layer * NKVH + xcd) * (size_t)a.max_seq + pos) * HDIM + c;
       if constexpr (BB) {
@@ -690,16 +730,17 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     if (c == 0) s.wts[h][MAXC] = 1.0 / Z;
   };
   // ---- poller: AR1 (O partials + residual) -> h1 slots; then h1 -> h1res, hn
-  auto prep_gu = [&](int lp, int layer) QTTS_INLINE {
-    const int par = lp & 1;
+  auto ar1 = [&](int lp, auto col) QTTS_INLINE {
+    const int par = cpar(lp, col);
+    const float* xr = cxres(col);
     // h1 = x + the sum of the 8 XCD partials, in f64
     if constexpr (XL) {
       double sm[4];
       float r[4];
 #pragma unroll
       for (int k = 0; k < 2; ++k) {
-        r[2 * k] = s.xres[32 * li + 2 * (lane + 64 * k)];
-        r[2 * k + 1] = s.xres[32 * li + 2 * (lane + 64 * k) + 1];
+        r[2 * k] = xr[32 * li + 2 * (lane + 64 * k)];
+        r[2 * k + 1] = xr[32 * li + 2 * (lane + 64 * k) + 1];
       }
       poll_sum8_rows(P, ws->opart[par], 32 * li, tag_of(lp, T_OPART), sm);
       if (kv_pending) {
@@ -712,7 +753,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
                    (float)((double)r[2 * k + 1] + sm[2 * k + 1]), tag_of(lp, T_H1));
     } else {
       const int row = 32 * li + 2 * (lane & 15);
-      const float r0 = s.xres[row], r1 = s.xres[row + 1];
+      const float r0 = xr[row], r1 = xr[row + 1];
       double s0, s1;
       poll_sum8(P, ws->opart[par], 32 * li, tag_of(lp, T_OPART), s0, s1);
       if (kv_pending) {
@@ -721,16 +762,23 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       }
       if (lane < 16) pub_local2(&ws->h1[xcd][par][row], (float)((double)r0 + s0), (float)((double)r1 + s1), tag_of(lp, T_H1));
     }
+  };
+  // h1 gathered -> h1res, hn
+  auto gather_h1 = [&](int lp, auto col) QTTS_INLINE {
     float xv[16], y[16];
     A gd[16];
     gains_d(g_post, gd);
-    poll_vec_regs(P, ws->h1[xcd][par], tag_of(lp, T_H1), xv);
-    store_pairs(s.h1res, xv);
+    poll_vec_regs(P, ws->h1[xcd][cpar(lp, col)], tag_of(lp, T_H1), xv);
+    store_pairs(ch1res(col), xv);
     normed(xv, gd, y);
-    store_pairs(s.hn, y);
+    store_pairs(chn(col), y);
   };
-  auto prep_down = [&](int lp) {
-    poll_vec<3>(P, ws->inter[xcd][lp & 1], XI, tag_of(lp, T_INTER), s.inter);
+  auto prep_gu = [&](int lp, int layer, auto col) QTTS_INLINE {
+    ar1(lp, col);
+    gather_h1(lp, col);
+  };
+  auto prep_down = [&](int lp, auto col) QTTS_INLINE {
+    poll_vec<3>(P, ws->inter[xcd][cpar(lp, col)], XI, tag_of(lp, T_INTER), cinter(col));
   };
 
   // ---- math: attention over this workgroup's chunk [c0, c1) at KV length L, for NH query
@@ -890,14 +938,30 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   // p_j = exp(s_j - M); p and V_j go to LDS and, after a second barrier, thread (h, d) forms
   // (sum_j p_j V_j[d]) / (sum_j p_j) from operands it loads all at once. Positions j >= L carry
   // p = 0 and V = 0 (the tile's out-of-range lanes read zeros), so the sums run over all 16.
-  auto attention_cp_local = [&](int L) {
+  // duo (two-column pass, L = 2): position 1 (column 1) attends to positions 0 and 1, both new
+  // entries in LDS; position 0 (column 0) attends to itself alone, whose result is its V exactly
+  // (p = exp(0) = 1, Z = 1), stored directly.
+  auto attention_cp_local = [&](int L, auto duo_c) QTTS_INLINE {
+    constexpr bool duo = decltype(duo_c)::value;
     const int Lold = L - 1;
     const int d0 = 8 * (lane & 15), g = lane >> 4;
     const int j = 4 * mw + g;
     float kv[8], vv[8];
-    const float4 qa0 = *reinterpret_cast<const float4*>(&s.q[0][d0]), qb0 = *reinterpret_cast<const float4*>(&s.q[0][d0 + 4]);
-    const float4 qa1 = *reinterpret_cast<const float4*>(&s.q[1][d0]), qb1 = *reinterpret_cast<const float4*>(&s.q[1][d0 + 4]);
-    if (j == Lold) {
+    const float (&sq)[2][HDIM] = duo ? s.q_1 : s.q;
+    const float4 qa0 = *reinterpret_cast<const float4*>(&sq[0][d0]), qb0 = *reinterpret_cast<const float4*>(&sq[0][d0 + 4]);
+    const float4 qa1 = *reinterpret_cast<const float4*>(&sq[1][d0]), qb1 = *reinterpret_cast<const float4*>(&sq[1][d0 + 4]);
+    if (duo) {
+      // j = 0: position 0's entry; j = 1: position 1's; positions past L carry zeros
+      const float* ks = j == 0 ? s.knew : s.knew_1;
+      const float* vs = j == 0 ? s.vnew : s.vnew_1;
+      const bool ok = j < 2;
+      const float4 ka = ok ? *reinterpret_cast<const float4*>(&ks[d0]) : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 kb = ok ? *reinterpret_cast<const float4*>(&ks[d0 + 4]) : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 va = ok ? *reinterpret_cast<const float4*>(&vs[d0]) : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 vb = ok ? *reinterpret_cast<const float4*>(&vs[d0 + 4]) : make_float4(0.f, 0.f, 0.f, 0.f);
+      kv[0] = ka.x; kv[1] = ka.y; kv[2] = ka.z; kv[3] = ka.w; kv[4] = kb.x; kv[5] = kb.y; kv[6] = kb.z; kv[7] = kb.w;
+      vv[0] = va.x; vv[1] = va.y; vv[2] = va.z; vv[3] = va.w; vv[4] = vb.x; vv[5] = vb.y; vv[6] = vb.z; vv[7] = vb.w;
+    } else if (j == Lold) {
       const float4 ka = *reinterpret_cast<const float4*>(&s.knew[d0]), kb = *reinterpret_cast<const float4*>(&s.knew[d0 + 4]);
       const float4 va = *reinterpret_cast<const float4*>(&s.vnew[d0]), vb = *reinterpret_cast<const float4*>(&s.vnew[d0 + 4]);
       kv[0] = ka.x; kv[1] = ka.y; kv[2] = ka.z; kv[3] = ka.w; kv[4] = kb.x; kv[5] = kb.y; kv[6] = kb.z; kv[7] = kb.w;
@@ -953,7 +1017,12 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       A4[jj & 3] = fmaf(pj[jj], vj[jj], A4[jj & 3]);
     }
     const float As = (A4[0] + A4[1]) + (A4[2] + A4[3]), Z = (Z4[0] + Z4[1]) + (Z4[2] + Z4[3]);
-    s.attn[t] = As * rcp_f(Z);
+    if (duo) {
+      s.attn_1[t] = As * rcp_f(Z);
+      s.attn[t] = s.vnew[d];
+    } else {
+      s.attn[t] = As * rcp_f(Z);
+    }
     step_barrier();   // s.attn complete; vst / plf are reused by the next attention
   };
 
@@ -962,9 +1031,9 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) { xv[i] = x[8 * lane + i]; xv[8 + i] = x[512 + 8 * lane + i]; }
   };
-  auto math_qkv = [&](int lp, int lg, const TileQKV& tq) {
+  auto math_qkv = [&](int lp, int lg, const TileQKV& tq, auto col) QTTS_INLINE {
     A xv[16];
-    load_x16(s.xn, xv);
+    load_x16(cxn(col), xv);
     const uint32_t tg = tag_of(lp, T_QKV);
     A v[4];
 #pragma unroll
@@ -973,7 +1042,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     // slot order pairs the rotate_half partners: channel c' of head h goes to slot
     // 128 h + 2 (c' mod 64) + c' / 64, so one 16-byte pair holds channels c and c + 64
     const int lr = 16 * lg + 4 * mw + (lane >> 4), cc = lr & 127;
-    if ((lane & 15) == 0) pub_local(&ws->qkv[xcd][lp & 1][(lr & ~127) + 2 * (cc & 63) + (cc >> 6)], (float)t, tg);
+    if ((lane & 15) == 0) pub_local(&ws->qkv[xcd][cpar(lp, col)][(lr & ~127) + 2 * (cc & 63) + (cc >> 6)], (float)t, tg);
   };
   // chunked attention: merge, one column per thread: f32((sum_c acc_c w_c) * (1 / Z)); chunks
   // c >= C carry weight 0 (their partials are finite: zero-initialised or older)
@@ -990,11 +1059,12 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       step_barrier();
     }
   };
-  auto math_o = [&](int lp, int lg, const TileO& to) {
+  auto math_o = [&](int lp, int lg, const TileO& to, auto colc) QTTS_INLINE {
     const int col = 8 * (lane & 31);
+    const float* at = cattn(colc);
     A xv[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) xv[i] = s.attn[col + i];
+    for (int i = 0; i < 8; ++i) xv[i] = at[col + i];
     const uint32_t tg = tag_of(lp, T_OPART);
     A v[4];
 #pragma unroll
@@ -1002,11 +1072,11 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     // per half-wave: row pair j = (lane >> 3) & 3 ends in lanes 0, 8, 16, 24 (+32)
     const A t = rs_sum<4, 4>(v, lane);
     if ((lane & 7) == 0)
-      pub_cross(&ws->opart[lp & 1][xcd][32 * lg + 8 * mw + 2 * ((lane >> 3) & 3) + (lane >> 5)], (float)t, tg);
+      pub_cross(&ws->opart[cpar(lp, colc)][xcd][32 * lg + 8 * mw + 2 * ((lane >> 3) & 3) + (lane >> 5)], (float)t, tg);
   };
-  auto math_gu = [&](int lp, int lg, const TileGU& tgu) {
+  auto math_gu = [&](int lp, int lg, const TileGU& tgu, auto col) QTTS_INLINE {
     A xv[16];
-    load_x16(s.hn, xv);
+    load_x16(chn(col), xv);
     const uint32_t tg = tag_of(lp, T_INTER);
     using P2 = pair2<A>;
     P2 c[4];
@@ -1019,15 +1089,16 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     const int r = lane >> 4;
     if ((lane & 15) == 0 && r < 3) {
       const A act = t.a / (A(1) + exp_a(-t.a)) * t.b;
-      pub_local(&ws->inter[xcd][lp & 1][12 * lg + 3 * mw + r], (float)act, tg);
+      pub_local(&ws->inter[xcd][cpar(lp, col)][12 * lg + 3 * mw + r], (float)act, tg);
     }
   };
-  auto math_down = [&](int lp, int lg, const TileD& td) {
+  auto math_down = [&](int lp, int lg, const TileD& td, auto col) QTTS_INLINE {
+    const float* it = cinter(col);
     A xv[24];
 #pragma unroll
     for (int j = 0; j < 3; ++j)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) xv[8 * j + i] = s.inter[8 * ((lane & 15) + 16 * j) + i];
+      for (int i = 0; i < 8; ++i) xv[8 * j + i] = it[8 * ((lane & 15) + 16 * j) + i];
     const uint32_t tg = tag_of(lp, T_DPART);
     A v[2];
 #pragma unroll
@@ -1039,7 +1110,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     // per 16-lane group: row set g = (lane >> 3) & 1 ends in lanes 0 and 8
     const A t = rs_sum<3, 2>(v, lane);
     if ((lane & 7) == 0)
-      pub_cross(&ws->dpart[lp & 1][xcd][32 * lg + 8 * mw + 4 * ((lane >> 3) & 1) + (lane >> 4)], (float)t, tg);
+      pub_cross(&ws->dpart[cpar(lp, col)][xcd][32 * lg + 8 * mw + 4 * ((lane >> 3) & 1) + (lane >> 4)], (float)t, tg);
   };
   // head rows of a workgroup (of its row group sub in XL): backbone codec head 12 rows (3 per
   // wave), CP head 8 (2 per wave)
@@ -1195,7 +1266,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   // the compute of step k on operands the poller prepared during step k-1 and issue the
   // weight loads needed two steps later.
   // =====================================================================================
-  enum Step { S_PRO, S_QKV, S_ATT, S_O, S_GU, S_DOWN, S_HEAD };
+  enum Step { S_PRO, S_QKV, S_ATT, S_O, S_GU, S_DOWN, S_HEAD, S_QKV2, S_ATT2, S_GU2, S_DOWN2 };
   int nstep = 0;
   auto stamp = [&]() {
     if (a.trace != nullptr && lane == 0 && (poller || mw == 0) && nstep < TRACE_STEPS)
@@ -1208,10 +1279,26 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   // the code-predictor frame's position 0 feeds no head: of its last layer only the K/V entry
   // (the QKV step) is read later, so its attention, MLP and final norm are not computed
   auto kv_only = [&](int pi, int layer) { return a.cp_frame && pi == 0 && layer == NL - 1 && a.n_pos > 1; };
+  // The code-predictor frame (batch 1) runs positions 0 and 1 as one two-column pass: both
+  // inputs are known at launch (bf16(h) and emb_bb[g0]), position 1's layer l attends to
+  // position 0's layer-l entry, and every weight tile serves both columns. Its steps: the
+  // *2 variants, indexed by position 1; a head follows, then positions 2.. one by one.
+  const bool duo_frame = DUO_OK && a.cp_frame && a.n_pos >= 2;
   auto walk = [&](auto&& act) {
     act(S_PRO, 0, 0); stamp();
     step_barrier();
-    for (int pi = 0; pi < a.n_pos; ++pi) {
+    int pi_first = 0;
+    if (duo_frame) {
+      for (int layer = 0; layer < NL; ++layer) {
+        act(S_QKV2, 1, layer); stamp(); step_barrier();
+        act(S_ATT2, 1, layer); stamp(); step_barrier();
+        act(S_GU2, 1, layer); stamp(); step_barrier();
+        act(S_DOWN2, 1, layer); stamp(); step_barrier();
+      }
+      act(S_HEAD, 1, NL - 1); stamp(); step_barrier();
+      pi_first = 2;
+    }
+    for (int pi = pi_first; pi < a.n_pos; ++pi) {
       for (int layer = 0; layer < NL; ++layer) {
         act(S_QKV, pi, layer); stamp(); step_barrier();
         if (kv_only(pi, layer)) continue;
@@ -1260,18 +1347,25 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           load_gain_pairs(g_fin, a.final_norm);
           load_qk_gains(0);
           load_rope(q.pos);
-          prep_input0(0);
+          prep_input0(0, Col0{});
+          if constexpr (DUO_OK) {
+            if (duo_frame) {
+              prep_input0(1, Col1{});
+              if (lead) comb_add(true, Col1{});   // emb_bb[g0] opens the combine
+              load_rope_to(q.pos + 1, rc1, rsn1);
+            }
+          }
           load_gain_pairs(g_in, lw(LW, NL > 1 ? 1 : 0, W_LNIN));
           break;
         case S_QKV:
-          prep_att(lp, layer, q.pos, q.C);
+          prep_att(lp, layer, q.pos, q.C, Col0{});
           load_qk_gains(nl);
           if (layer == NL - 1 && !q.last_pos) load_rope(q.pos + 1);
           if (kv_only(pi, layer)) {
             // position 1's input, in place of this position's DOWN step; the math waves read
             // xn before publishing the QKV rows prep_att has waited for, so xn is free
-            prep_input0(pi + 1);
-            if (lead) comb_add(true);
+            prep_input0(pi + 1, Col0{});
+            if (lead) comb_add(true, Col0{});
             load_gain_pairs(g_in, lw(LW, NL > 1 ? 1 : 0, W_LNIN));
             load_gain_pairs(g_post, lw(LW, 0, W_LNPOST));
           }
@@ -1291,7 +1385,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
             for (int b = 0; b < nb; ++b) step_barrier();
           }
           if (q.local) {
-            prep_gu(lp, layer);
+            prep_gu(lp, layer, Col0{});
             load_gain_pairs(g_post, lw(LW, nl, W_LNPOST));
           } else {
             prep_o(lp, q.C);
@@ -1299,19 +1393,59 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           break;
         case S_O:
           step_barrier();   // joins the barrier after the math waves' attention merge
-          prep_gu(lp, layer);
+          prep_gu(lp, layer, Col0{});
           load_gain_pairs(g_post, lw(LW, nl, W_LNPOST));
           break;
-        case S_GU: prep_down(lp); break;
+        case S_GU: prep_down(lp, Col0{}); break;
         case S_DOWN:
-          if (layer < NL - 1) { ar2(lp); prep_input_next(lp); }
-          else if (q.head || q.last_pos) { ar2(lp); prep_final(lp); }
+          if (layer < NL - 1) { ar2(lp, Col0{}); prep_input_next(lp, Col0{}); }
+          else if (q.head || q.last_pos) { ar2(lp, Col0{}); prep_final(lp, Col0{}); }
           else {
-            prep_input0(pi + 1);
-            if (a.cp_frame && lead) comb_add(pi == 0);
+            prep_input0(pi + 1, Col0{});
+            if (a.cp_frame && lead) comb_add(pi == 0, Col0{});
           }
           // g_in now serves the layer after next
           if (layer < NL - 1 || !(q.head || q.last_pos)) load_gain_pairs(g_in, lw(LW, (nl + 1) % NL, W_LNIN));
+          break;
+        case S_QKV2:
+          if constexpr (DUO_OK) {
+            prep_att(lp - NL, layer, q.pos - 1, q.C, Col0{});
+            prep_att(lp, layer, q.pos, q.C, Col1{});
+            load_qk_gains(nl);
+            if (layer == NL - 1) load_rope(q.pos + 1);
+          }
+          break;
+        case S_ATT2:
+          if constexpr (DUO_OK) {
+            for (int b = 0; b < 3; ++b) step_barrier();   // the local attention's three barriers
+            // position 0's last layer feeds nothing beyond its K/V entry; both columns' sums are
+            // published before either gather, so neither gather waits behind the other's
+            if (layer < NL - 1) ar1(lp - NL, Col0{});
+            ar1(lp, Col1{});
+            if (layer < NL - 1) gather_h1(lp - NL, Col0{});
+            gather_h1(lp, Col1{});
+            load_gain_pairs(g_post, lw(LW, nl, W_LNPOST));
+          }
+          break;
+        case S_GU2:
+          if constexpr (DUO_OK) {
+            if (layer < NL - 1) prep_down(lp - NL, Col0{});
+            prep_down(lp, Col1{});
+          }
+          break;
+        case S_DOWN2:
+          if constexpr (DUO_OK) {
+            if (layer < NL - 1) {
+              ar2(lp - NL, Col0{});
+              ar2(lp, Col1{});
+              prep_input_next(lp - NL, Col0{});
+              prep_input_next(lp, Col1{});
+              load_gain_pairs(g_in, lw(LW, (nl + 1) % NL, W_LNIN));
+            } else {
+              ar2(lp, Col1{});
+              prep_final(lp, Col1{});
+            }
+          }
           break;
         case S_HEAD:
           if (cp_greedy) step_barrier();   // joins the math waves' head barrier
@@ -1321,8 +1455,8 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
               if (lane == 0) s.tok[pi - 1] = tok;
               __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
               if (!q.last_pos) {
-                prep_input0(pi + 1);
-                if (lead) comb_add(false);
+                prep_input0(pi + 1, Col0{});
+                if (lead) comb_add(false, Col0{});
                 load_gain_pairs(g_in, lw(LW, NL > 1 ? 1 : 0, W_LNIN));
               }
             } else if (lane == 0 && SIO(out_token)) {
@@ -1350,15 +1484,15 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
 #pragma unroll 1
           for (int sub = 0; sub < NSUB - 2; sub += 2) {
             load_qkv<BB>(t1, LW, layer_, xcd, li + sub + 1, mw, lane);
-            math_qkv(lp, li + sub, tq);
+            math_qkv(lp, li + sub, tq, Col0{});
             load_qkv<BB>(tq, LW, layer_, xcd, li + sub + 2, mw, lane);
-            math_qkv(lp, li + sub + 1, t1);
+            math_qkv(lp, li + sub + 1, t1, Col0{});
           }
           load_qkv<BB>(t1, LW, layer_, xcd, li + NSUB - 1, mw, lane);
-          math_qkv(lp, li + NSUB - 2, tq);
-          math_qkv(lp, li + NSUB - 1, t1);
+          math_qkv(lp, li + NSUB - 2, tq, Col0{});
+          math_qkv(lp, li + NSUB - 1, t1, Col0{});
         } else {
-          math_qkv(lp, li, tq);
+          math_qkv(lp, li, tq, Col0{});
         }
       };
       auto o_stage = [&](int layer_) {
@@ -1367,15 +1501,15 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
 #pragma unroll 1
           for (int sub = 0; sub < NSUB - 2; sub += 2) {
             load_o<BB>(t1, LW, layer_, xcd, li + sub + 1, mw, lane);
-            math_o(lp, li + sub, to);
+            math_o(lp, li + sub, to, Col0{});
             load_o<BB>(to, LW, layer_, xcd, li + sub + 2, mw, lane);
-            math_o(lp, li + sub + 1, t1);
+            math_o(lp, li + sub + 1, t1, Col0{});
           }
           load_o<BB>(t1, LW, layer_, xcd, li + NSUB - 1, mw, lane);
-          math_o(lp, li + NSUB - 2, to);
-          math_o(lp, li + NSUB - 1, t1);
+          math_o(lp, li + NSUB - 2, to, Col0{});
+          math_o(lp, li + NSUB - 1, t1, Col0{});
         } else {
-          math_o(lp, li, to);
+          math_o(lp, li, to, Col0{});
         }
       };
       auto gu_stage = [&](int layer_) {
@@ -1384,15 +1518,15 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
 #pragma unroll 1
           for (int sub = 0; sub < NSUB - 2; sub += 2) {
             load_gu<BB>(t1, LW, layer_, xcd, li + sub + 1, mw, lane);
-            math_gu(lp, li + sub, tgu);
+            math_gu(lp, li + sub, tgu, Col0{});
             load_gu<BB>(tgu, LW, layer_, xcd, li + sub + 2, mw, lane);
-            math_gu(lp, li + sub + 1, t1);
+            math_gu(lp, li + sub + 1, t1, Col0{});
           }
           load_gu<BB>(t1, LW, layer_, xcd, li + NSUB - 1, mw, lane);
-          math_gu(lp, li + NSUB - 2, tgu);
-          math_gu(lp, li + NSUB - 1, t1);
+          math_gu(lp, li + NSUB - 2, tgu, Col0{});
+          math_gu(lp, li + NSUB - 1, t1, Col0{});
         } else {
-          math_gu(lp, li, tgu);
+          math_gu(lp, li, tgu, Col0{});
         }
       };
       auto down_stage = [&](int layer_) {
@@ -1401,15 +1535,15 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
 #pragma unroll 1
           for (int sub = 0; sub < NSUB - 2; sub += 2) {
             load_d<BB>(t1, LW, layer_, xcd, li + sub + 1, mw, lane);
-            math_down(lp, li + sub, td);
+            math_down(lp, li + sub, td, Col0{});
             load_d<BB>(td, LW, layer_, xcd, li + sub + 2, mw, lane);
-            math_down(lp, li + sub + 1, t1);
+            math_down(lp, li + sub + 1, t1, Col0{});
           }
           load_d<BB>(t1, LW, layer_, xcd, li + NSUB - 1, mw, lane);
-          math_down(lp, li + NSUB - 2, td);
-          math_down(lp, li + NSUB - 1, t1);
+          math_down(lp, li + NSUB - 2, td, Col0{});
+          math_down(lp, li + NSUB - 1, t1, Col0{});
         } else {
-          math_down(lp, li, td);
+          math_down(lp, li, td, Col0{});
         }
       };
       auto head_stage = [&]() {
@@ -1454,7 +1588,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           break;
         case S_ATT:
           if constexpr (!BB) {
-            if (q.local) attention_cp_local(q.L);
+            if (q.local) attention_cp_local(q.L, std::false_type{});
             else if (q.has_chunk) attention(std::integral_constant<int, 1>{}, lp, layer, q.L, q.c0, q.c1, false, li & 1, li);
           } else if (q.has_chunk) {
             if (q.local) {
@@ -1504,6 +1638,42 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           head_stage();
           if (!q.last_pos) load_qkv<BB>(tq, LW, 0, xcd, li, mw, lane);
           else tq = TileQKV{};
+          break;
+        case S_QKV2:
+          if constexpr (DUO_OK) {
+            math_qkv(lp - NL, li, tq, Col0{});
+            math_qkv(lp, li, tq, Col1{});
+            tk = TileKV<BB>{};
+            load_o<BB>(to, LW, layer, xcd, li, mw, lane);
+          }
+          break;
+        case S_ATT2:
+          if constexpr (DUO_OK) {
+            attention_cp_local(2, std::true_type{});
+            math_o(lp - NL, li, to, Col0{});
+            math_o(lp, li, to, Col1{});
+            load_gu<BB>(tgu, LW, layer, xcd, li, mw, lane);
+          }
+          break;
+        case S_GU2:
+          if constexpr (DUO_OK) {
+            math_gu(lp - NL, li, tgu, Col0{});
+            math_gu(lp, li, tgu, Col1{});
+            load_d<BB>(td, LW, layer, xcd, li, mw, lane);
+          }
+          break;
+        case S_DOWN2:
+          if constexpr (DUO_OK) {
+            math_down(lp - NL, li, td, Col0{});
+            math_down(lp, li, td, Col1{});
+            if (!last_layer) {
+              load_qkv<BB>(tq, LW, layer + 1, xcd, li, mw, lane);
+            } else {
+              int row0, nrows;
+              head_rows(0, row0, nrows);
+              load_head<BB>(tq, head_weights(pi), row0, nrows, lane);
+            }
+          }
           break;
       }
     });
