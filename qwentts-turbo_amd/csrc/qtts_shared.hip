@@ -462,13 +462,14 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
   // q/k norm, RoPE and the KV write of layer `layer` at cache slot pos. The lane holds channels
   // c = lane and c + 64 (the rotate_half partners) of q head 0, q head 1, k and v.
   bool kv_pending = false;
-  auto prep_att = [&](int lp, int layer, int pos) {
+  auto prep_att = [&](int lp, int layer, int pos, auto&& issue) SH_INLINE {
     load_qk(layer, pos);
     float v[8];
     {
       const uint32_t o = ws_off(P, &ws->qkv[xcd][lp & 1][wv][0]);
       poll_regs<4>(P, LROWS / 2, tag_of(lp, T_QKV), v, [o](int i) { return o + 16u * (uint32_t)i; });
     }
+    issue();
     A ss[3];
 #pragma unroll
     for (int h = 0; h < 3; ++h) ss[h] = fma((A)v[2 * h], (A)v[2 * h], (A)v[2 * h + 1] * (A)v[2 * h + 1]);
@@ -1157,9 +1158,9 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
       // the next tiles go out after the publish: a wave's vector-memory results return in issue
       // order, so a poll issued behind a tile load would wait for the tile
       if constexpr (BB) {
-        load_kv_first(tkv, layer);
-        load_o(to, layer);
-        if (me) prep_att(lp, layer, pos);
+        auto iss = [&]() SH_INLINE { load_kv_first(tkv, layer); load_o(to, layer); };
+        if (me) prep_att(lp, layer, pos, iss);
+        else iss();
       } else {
         auto iss = [&]() SH_INLINE { load_o(to, layer); };
         if (me) cp_prep_att(lp, layer, pos, iss);
