@@ -567,22 +567,6 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
     if (lane < 16)
       pub_local2(&ws->h1[xcd][par][wv][32 * li + r2], (float)((double)r0 + s0), (float)((double)r1 + s1), tag_of(lp, T_H1));
   };
-  auto prep_gu = [&](int lp, int layer) {
-    load_gains(lw(LW, layer, W_LNPOST));
-    float xv[16], y[16];
-    gather1024(P, &ws->h1[xcd][lp & 1][wv][0], tag_of(lp, T_H1), xv);
-    stamp(12);
-    keep_rows(s.h1res[wv], xv);
-    normed(xv, y);
-    put_vec(y);
-  };
-  auto prep_down = [&](int lp) {
-    float v[6];
-    const uint32_t o = ws_off(P, &ws->inter[xcd][lp & 1][wv][0]);
-    poll_regs<3>(P, XI / 2, tag_of(lp, T_INTER), v, [o](int i) { return o + 16u * (uint32_t)i; });
-#pragma unroll
-    for (int k = 0; k < 3; ++k) put_pair(2 * (lane + 64 * k), v[2 * k], v[2 * k + 1]);
-  };
   // AR2: x' = h1 + the sum of the 8 XCD down partials (bf16 residual in the backbone)
   auto ar2 = [&](int lp) {
     const int par = lp & 1, r2 = 2 * (lane & 15);
@@ -594,14 +578,6 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
       if constexpr (BB) { x0 = rbf(x0); x1 = rbf(x1); }
       pub_local2(&ws->xl[xcd][par][wv][32 * li + r2], x0, x1, tag_of(lp, T_XL));
     }
-  };
-  auto prep_input_next = [&](int lp, int nlayer) {
-    load_gains(lw(LW, nlayer, W_LNIN));
-    float xv[16], y[16];
-    gather1024(P, &ws->xl[xcd][lp & 1][wv][0], tag_of(lp, T_XL), xv);
-    keep_rows(s.xres[wv], xv);
-    normed(xv, y);
-    put_vec(y);
   };
   // final norm: outputs (the stream's own workgroup) and the head input bf16(h)
   auto prep_final = [&](int lp) {
@@ -628,12 +604,11 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
     put_vec(y);
   };
 
-  // The code predictor's vector phases take the issue of the next step's weight tile as an
-  // argument and make it right after their last poll: a wave's vector-memory results return in
-  // issue order, so a poll issued behind a tile load waits for the tile's HBM round trip. (The
-  // backbone issues its tiles right after the publish: its kernel has no registers left to hold
-  // the polled values across the issue, and a spill reload after the issue would wait for the
-  // tile.) Generic lambdas: only the code-predictor instantiation creates them.
+  // These vector phases take the issue of the next step's weight tile as an argument and make it
+  // right after their last poll: a wave's vector-memory results return in issue order, so a poll
+  // issued behind a tile load waits for the tile's HBM round trip. Both models use them for the
+  // QKV, O, gate/up and (except after the last layer) down steps; the code predictor also for
+  // its inputs and final norm.
   auto cp_prep_input0 = [&](int pi, auto&& issue) SH_INLINE {
     load_gains(lw(LW, 0, W_LNIN));
     float xv[16];
@@ -1193,10 +1168,7 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
         if (is_live(st)) pub_cross(&ws->opart[par][xcd][st][32 * li + 16 * tile + r], v, tag_of(lp, T_OPART));
       }
       stamp(14);
-      if constexpr (BB) {
-        load_g(tgu, layer);
-        if (me) { ar1(lp); stamp(11); prep_gu(lp, layer); }
-      } else {
+      {
         auto iss = [&]() SH_INLINE { stamp(12); load_g(tgu, layer); };
         if (me) {
           ar1(lp);
@@ -1221,10 +1193,7 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
         if (is_live(st)) pub_local(&ws->inter[xcd][par][st][12 * li + r], act, tag_of(lp, T_INTER));
       }
       stamp(14);
-      if constexpr (BB) {
-        load_d(td, layer);
-        if (me) prep_down(lp);
-      } else {
+      {
         auto iss = [&]() SH_INLINE { load_d(td, layer); };
         if (me) cp_prep_down(lp, iss);
         else iss();
@@ -1244,13 +1213,22 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
       }
       stamp(14);
       if constexpr (BB) {
-        if (!last_layer) load_q(tq, layer + 1);
-        else if (head) load_h(tq, head_w(pi));
-        else if (!last_pos) load_q(tq, 0);
-        if (me) {
-          if (!last_layer) { ar2(lp); prep_input_next(lp, layer + 1); }
-          else if (head || last_pos) { ar2(lp); prep_final(lp); }
-          else prep_input0(pi + 1);
+        if (!last_layer) {
+          // the next layer's QKV tile goes out after the gather's last poll
+          auto iss = [&]() SH_INLINE { load_q(tq, layer + 1); };
+          if (me) {
+            ar2(lp);
+            cp_prep_vec(&ws->xl[xcd][par][wv][0], tag_of(lp, T_XL), lw(LW, layer + 1, W_LNIN), s.xres[wv], iss);
+          } else {
+            iss();
+          }
+        } else {
+          if (head) load_h(tq, head_w(pi));
+          else if (!last_pos) load_q(tq, 0);
+          if (me) {
+            if (head || last_pos) { ar2(lp); prep_final(lp); }
+            else prep_input0(pi + 1);
+          }
         }
       } else {
         // next: the following layer's input, the final norm (a head follows every position
