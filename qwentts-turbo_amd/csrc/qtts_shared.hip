@@ -747,22 +747,29 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
     float kn8[8], vn8[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) { kn8[i] = s.knew[wv][d0 + i]; vn8[i] = s.vnew[wv][d0 + i]; }
+    // position blocks jj (positions 4 jj .. 4 jj + 3, one per lane group) wholly past L are skipped
+    // (uniform branches; their scores are -inf, their weights 0, as the masks below give them)
     float sc[8];   // [h * 4 + jj]
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       const int j = g + 4 * jj;
-      float kv[8];
+      float sj[2] = {0.0f, 0.0f};
+      if (4 * jj < L) {
+        float kv[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) kv[i] = j == Lold ? kn8[i] : __uint_as_float(kt[jj][i >> 2][i & 3]);
+        for (int i = 0; i < 8; ++i) kv[i] = j == Lold ? kn8[i] : __uint_as_float(kt[jj][i >> 2][i & 3]);
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        float d = 0.0f;
+        for (int h = 0; h < 2; ++h) {
+          float d = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) d = fmaf(qv[h][i], kv[i], d);
-        sc[4 * h + jj] = d;
+          for (int i = 0; i < 8; ++i) d = fmaf(qv[h][i], kv[i], d);
+          sj[h] = d;
+        }
+        group_sum_n<16>(sj);
       }
+      sc[jj] = sj[0];
+      sc[4 + jj] = sj[1];
     }
-    group_sum_n<16>(sc);
     float acc[2][8], Z[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -780,32 +787,43 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
       for (int i = 0; i < 8; ++i) acc[h][i] = 0.0f;
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
-        const int j = g + 4 * jj;
-        const float p = j < L ? __expf(sc[4 * h + jj] - M) : 0.0f;
-        Z[h] += p;
+        if (4 * jj < L) {
+          const int j = g + 4 * jj;
+          const float p = j < L ? __expf(sc[4 * h + jj] - M) : 0.0f;
+          Z[h] += p;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[h][i] = fmaf(p, j == Lold ? vn8[i] : __uint_as_float(vt[jj][i >> 2][i & 3]), acc[h][i]);
+          for (int i = 0; i < 8; ++i) acc[h][i] = fmaf(p, j == Lold ? vn8[i] : __uint_as_float(vt[jj][i >> 2][i & 3]), acc[h][i]);
+        }
       }
     }
-    // lane groups hold different positions: sum over the lanes l, l ^ 16, l ^ 32, l ^ 48
+    // lane groups hold different positions: sum over the lanes l, l ^ 16, l ^ 32, l ^ 48 as
+    // (a_g + a_g^1) + (a_g^2 + a_g^3), scattered: after the two exchanges lane group g holds the 4
+    // values k = n + 4 ((g >> 1) & 1) + 8 (g & 1) (head k >> 3, dims d0 + (k & 7)), each summed in
+    // the order a full butterfly gives (the two halves' sums commute exactly)
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       Z[h] += xlane_f<4>(Z[h]);
       Z[h] += xlane_f<5>(Z[h]);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        acc[h][i] += xlane_f<4>(acc[h][i]);
-        acc[h][i] += xlane_f<5>(acc[h][i]);
-      }
     }
-    if (lane < 16) {
+    const bool hi1 = (g & 1) != 0, hi2 = (g & 2) != 0;
+    float k8[8];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const float rz = rcp_f(Z[h]);
-#pragma unroll
-        for (int i = 0; i < 8; i += 2) put_pair(128 * h + d0 + i, acc[h][i] * rz, acc[h][i + 1] * rz);
-      }
+    for (int m = 0; m < 8; ++m) {
+      const float send = hi1 ? acc[0][m] : acc[1][m];
+      const float keep = hi1 ? acc[1][m] : acc[0][m];
+      k8[m] = keep + xlane_f<4>(send);
     }
+    float k4[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      const float send = hi2 ? k8[n] : k8[n + 4];
+      const float keep = hi2 ? k8[n + 4] : k8[n];
+      k4[n] = keep + xlane_f<5>(send);
+    }
+    const float rz = rcp_f(hi1 ? Z[1] : Z[0]);
+    const int e = 128 * (hi1 ? 1 : 0) + d0 + (hi2 ? 4 : 0);
+    put_pair(e, k4[0] * rz, k4[1] * rz);
+    put_pair(e + 2, k4[2] * rz, k4[3] * rz);
   };
   // backbone: unit li of this XCD's KV head (stream us, positions [c0, c1)), f32 softmax. Wave w
   // takes positions c0 + APASS * pass + 32 w + 4 jj + g (lane group g, jj < AJJ) with its own
