@@ -190,6 +190,45 @@ def test_cp_frame_greedy_tokens(full, pkg, seed):
     assert torch.equal(comb.cpu(), comb_ref)
 
 
+@pytest.mark.parametrize("n_cp_layers", [1, 2, 3])
+def test_cp_frame_two_column_pass_layer_counts(pkg, n_cp_layers):
+    """The frame's positions 0 and 1 run as one two-column pass whose second column publishes into
+    the exchange buffers of the other parity; with an even layer count both columns' layer-pass
+    numbers have the same parity, with one layer the pass's only layer is position 0's last. Ids,
+    combine and the cache entries of positions 0 and 1 against the oracle at 1, 2 and 3 layers."""
+    cfg = pkg.SyntheticConfig(n_bb_layers=1, n_cp_layers=n_cp_layers, n_groups=15)
+    sd = pkg.synthetic_state_dict(seed=77 + n_cp_layers, cfg=cfg)
+    dsd = {k: v.to("cuda") for k, v in sd.items()}
+    tw = TalkerWeights.from_state_dict(sd, 1, n_cp_layers)
+    cp = pkg.CodePredictorMegakernelGenerator(model=dsd, max_seq_len=32)
+    talker = TalkerOracle(tw, max_seq=64)
+    g = torch.Generator().manual_seed(500 + n_cp_layers)
+    i32 = dict(dtype=torch.int32, device="cuda")
+    for rep in range(2):
+        hid = torch.randn(1024, generator=g)
+        g0 = int(torch.randint(0, 3072, (1,), generator=g))
+        text = torch.randn(1024, generator=g).to(torch.bfloat16)
+        ref = talker.cp_frame(hid, g0)
+        out = torch.full((16,), -1, **i32)
+        comb = torch.empty(1024, dtype=torch.bfloat16, device="cuda")
+        cp.decoder.frame(hid.cuda(), torch.tensor([g0], **i32), text.cuda(), out, comb, -1, torch.zeros(1, **i32),
+                         False, 1.0, 0, 1.0, 0, rep)
+        torch.cuda.synchronize()
+        cp.check_error()
+        toks = out.cpu().tolist()
+        _print(f"CP {n_cp_layers} layers, frame {rep}: gpu {toks[1:]} oracle {ref}")
+        assert toks[0] == g0
+        assert toks[1:] == ref
+        assert torch.equal(comb.cpu(), talker.combine([g0] + ref, text))
+        # the K/V entries the pass wrote for positions 0 and 1, every layer
+        kc, vc = cp.decoder.get_k_cache(), cp.decoder.get_v_cache()
+        okk, ovv = talker.cp.k, talker.cp.v
+        for l in range(n_cp_layers):
+            for pos in (0, 1):
+                assert rel_l2(kc[l, :, pos].float().cpu(), okk[l, :, pos].float()) < TOL
+                assert rel_l2(vc[l, :, pos].float().cpu(), ovv[l, :, pos].float()) < TOL
+
+
 def test_backbone_head_select_greedy_and_penalty(full, pkg):
     sd, dsd, tw = full
     n = 2
