@@ -880,23 +880,31 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
       for (int i = 0; i < 8; ++i) { kn8[i] = s.knew[u.us][d0 + i]; vn8[i] = s.vnew[u.us][d0 + i]; }
       for (int b0 = u.c0; b0 < u.c1; b0 += APASS) {
         if (b0 > u.c0) load_kv(t, layer, u.us, b0, min(u.c1, Lold));
+        // blocks of 4 positions (one per lane group) wholly past the unit's end are skipped
+        // (wave-uniform branches); their scores are -inf and their weights 0, as the masks give them
+        const int wb0 = b0 + 4 * AJJ * wv;   // the wave's first position of this pass
         float sc[2 * AJJ];   // [h * AJJ + jj]
 #pragma unroll
         for (int jj = 0; jj < AJJ; ++jj) {
-          const int pos = b0 + 4 * AJJ * wv + 4 * jj + g;
-          const u32x4 w = t.k[jj];
-          float kv[8] = {bflo(w.x), bfhi(w.x), bflo(w.y), bfhi(w.y), bflo(w.z), bfhi(w.z), bflo(w.w), bfhi(w.w)};
+          const int pos = wb0 + 4 * jj + g;
+          float sj[2] = {0.0f, 0.0f};
+          if (wb0 + 4 * jj < u.c1) {
+            const u32x4 w = t.k[jj];
+            float kv[8] = {bflo(w.x), bfhi(w.x), bflo(w.y), bfhi(w.y), bflo(w.z), bfhi(w.z), bflo(w.w), bfhi(w.w)};
 #pragma unroll
-          for (int i = 0; i < 8; ++i) kv[i] = pos == Lold ? kn8[i] : kv[i];
+            for (int i = 0; i < 8; ++i) kv[i] = pos == Lold ? kn8[i] : kv[i];
 #pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            float d = 0.0f;
+            for (int h = 0; h < 2; ++h) {
+              float d = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) d = fmaf(qv[h][i], kv[i], d);
-            sc[h * AJJ + jj] = d;
+              for (int i = 0; i < 8; ++i) d = fmaf(qv[h][i], kv[i], d);
+              sj[h] = d;
+            }
+            group_sum_n<16>(sj);
           }
+          sc[jj] = sj[0];
+          sc[AJJ + jj] = sj[1];
         }
-        group_sum_n<16>(sc);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           float mx = -INFINITY;
@@ -916,34 +924,46 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
             for (int i = 0; i < 8; ++i) acc[h][i] *= alpha;
 #pragma unroll
             for (int jj = 0; jj < AJJ; ++jj) {
-              const float p = sc[h * AJJ + jj] == -INFINITY ? 0.0f : __expf(sc[h * AJJ + jj] - mn);
-              const int pos = b0 + 4 * AJJ * wv + 4 * jj + g;
-              const u32x4 w = t.v[jj];
-              float vv[8] = {bflo(w.x), bfhi(w.x), bflo(w.y), bfhi(w.y), bflo(w.z), bfhi(w.z), bflo(w.w), bfhi(w.w)};
-              l[h] += p;
+              if (wb0 + 4 * jj < u.c1) {
+                const float p = sc[h * AJJ + jj] == -INFINITY ? 0.0f : __expf(sc[h * AJJ + jj] - mn);
+                const int pos = wb0 + 4 * jj + g;
+                const u32x4 w = t.v[jj];
+                float vv[8] = {bflo(w.x), bfhi(w.x), bflo(w.y), bfhi(w.y), bflo(w.z), bfhi(w.z), bflo(w.w), bfhi(w.w)};
+                l[h] += p;
 #pragma unroll
-              for (int i = 0; i < 8; ++i) acc[h][i] = fmaf(p, pos == Lold ? vn8[i] : vv[i], acc[h][i]);
+                for (int i = 0; i < 8; ++i) acc[h][i] = fmaf(p, pos == Lold ? vn8[i] : vv[i], acc[h][i]);
+              }
             }
             m[h] = mn;
           }
         }
       }
     }
-    // the wave's totals over its 4 lane groups
+    // the wave's totals over its 4 lane groups, (a_g + a_g^1) + (a_g^2 + a_g^3); the accumulators
+    // scattered so that lane group g ends with head g & 1, dims d0 + 4 ((g >> 1) & 1) + n (n < 4),
+    // each summed in the order a full butterfly gives (the halves' sums commute exactly)
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       l[h] += xlane_f<4>(l[h]);
       l[h] += xlane_f<5>(l[h]);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        acc[h][i] += xlane_f<4>(acc[h][i]);
-        acc[h][i] += xlane_f<5>(acc[h][i]);
-      }
-      if (lane < 16) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) s.wpart[wv][h][d0 + i] = acc[h][i];
-      }
       if (lane == 0) { s.wpart[wv][h][HDIM] = m[h]; s.wpart[wv][h][HDIM + 1] = l[h]; }
+    }
+    {
+      const bool hi1 = (g & 1) != 0, hi2 = (g & 2) != 0;
+      float k8[8];
+#pragma unroll
+      for (int n = 0; n < 8; ++n) {
+        const float send = hi1 ? acc[0][n] : acc[1][n];
+        const float keep = hi1 ? acc[1][n] : acc[0][n];
+        k8[n] = keep + xlane_f<4>(send);
+      }
+      float* dst = &s.wpart[wv][hi1 ? 1 : 0][d0 + (hi2 ? 4 : 0)];
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        const float send = hi2 ? k8[n] : k8[n + 4];
+        const float keep = hi2 ? k8[n + 4] : k8[n];
+        dst[n] = keep + xlane_f<5>(send);
+      }
     }
     step_barrier();
     if (u.us >= 0 && tid < 2 * HDIM) {
