@@ -181,15 +181,9 @@ __device__ __forceinline__ bf16x8 as_bf8(u32x4 v) { return __builtin_bit_cast(bf
 __device__ __forceinline__ float ror8(float v) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, false));
 }
-// exact three-piece bf16 split: x = hi + mid + lo up to 2^-24 |x|
-__device__ __forceinline__ void split3(float x, bf16_t& h, bf16_t& m, bf16_t& l) {
-  h = f2bf(x);
-  const float r1 = x - bf2f(h);
-  m = f2bf(r1);
-  l = f2bf(r1 - bf2f(m));
-}
-// the same split of two values as packed pairs with the conversion instruction (three per pair
-// instead of about forty); each residual is exact in f32, so the pieces equal split3's
+// exact three-piece bf16 split of two values, as packed pairs: x = hi + mid + lo up to 2^-24 |x|
+// (each residual is exact in f32); the conversion instruction rounds to nearest even, three per
+// pair instead of about forty for the bit-manipulation rounding
 __device__ __forceinline__ void split3x2(float x0, float x1, uint32_t& h, uint32_t& m, uint32_t& l) {
   h = f2bf2(x0, x1);
   const float r0 = x0 - bflo(h), r1 = x1 - bfhi(h);
@@ -389,18 +383,7 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
   // projection input of this wave's stream: element e of piece p at xb[p][wv][e]
   auto put_pair = [&](int e, float v0, float v1) {
     uint32_t h, m, l;
-    if constexpr (BB) {
-      // the backbone instantiation keeps the bit-manipulation rounding: its register allocation
-      // spills with the shorter sequence (a spill reload waits behind the in-flight weight tile)
-      bf16_t h0, m0, l0, h1, m1, l1;
-      split3(v0, h0, m0, l0);
-      split3(v1, h1, m1, l1);
-      h = (uint32_t)h0 | ((uint32_t)h1 << 16);
-      m = (uint32_t)m0 | ((uint32_t)m1 << 16);
-      l = (uint32_t)l0 | ((uint32_t)l1 << 16);
-    } else {
-      split3x2(v0, v1, h, m, l);
-    }
+    split3x2(v0, v1, h, m, l);
     *reinterpret_cast<uint32_t*>(&s.xb[0][wv][e]) = h;
     *reinterpret_cast<uint32_t*>(&s.xb[1][wv][e]) = m;
     *reinterpret_cast<uint32_t*>(&s.xb[2][wv][e]) = l;
