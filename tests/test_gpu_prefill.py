@@ -133,6 +133,47 @@ def test_prefill_full_model_and_first_token(pkg):
     assert t == int(m.argmax())
 
 
+def test_prefill_per_layer_teacher_forced(pkg):
+    """Every one of the 28 layers on its own, from the oracle's own input to that layer: the GPU
+    prefill runs a one-layer model holding layer l's weights on the hf_bf16 oracle's residual
+    stream entering layer l (40 tokens), and its K/V entries and the last token's output (through
+    the final norm) must be within the north star's rel-L2 1e-2 of the oracle's layer l. This
+    holds each layer to the bar without the depth-compounded rounding spread of the 28-layer run."""
+    from oracle.qtts_oracle import rms_norm_hf
+    sd = pkg.synthetic_state_dict(seed=1234)
+    tw = TalkerWeights.from_state_dict(sd, 28, 5)
+    S = 40
+    orc = DecoderOracle(tw.bb_layers, tw.bb_norm, 64, "backbone", "hf_bf16")
+    x = torch.randn(S, 1024, generator=torch.Generator().manual_seed(19)).to(torch.bfloat16)
+    outs = []
+    for i in range(S):
+        _, o = orc.step(x[i], pos=i)
+        outs.append(o)
+    prefix = "talker.model.layers."
+    worst = [0.0, 0.0, 0.0]
+    for l in range(28):
+        sd1 = {}
+        for k, v in sd.items():
+            if k.startswith(prefix):
+                if k.startswith(f"{prefix}{l}."):
+                    sd1[prefix + "0." + k[len(f"{prefix}{l}."):]] = v.cuda()
+            else:
+                sd1[k] = v.cuda()
+        x_in = x if l == 0 else torch.stack([outs[i][l - 1] for i in range(S)]).to(torch.bfloat16)
+        bb = pkg.TTSMegakernelGenerator(model=sd1, max_seq_len=64)
+        h = bb.prefill(x_in.cuda())
+        torch.cuda.synchronize()
+        ek = rel_l2(bb.get_k_cache()[0, :, :S].float().cpu(), orc.k[l, :, :S].float())
+        ev = rel_l2(bb.get_v_cache()[0, :, :S].float().cpu(), orc.v[l, :, :S].float())
+        href = rms_norm_hf(outs[S - 1][l].to(torch.bfloat16), tw.bb_norm.to(torch.bfloat16), 1e-6).float()
+        eh = rel_l2(h.cpu(), href)
+        worst = [max(worst[0], ek), max(worst[1], ev), max(worst[2], eh)]
+        assert ek < TOL and ev < TOL and eh < TOL, (l, ek, ev, eh)
+        del bb, sd1
+    _print(f"per-layer teacher-forced prefill, 28 layers, S={S}: worst K {worst[0]:.2e}, V {worst[1]:.2e}, "
+           f"output {worst[2]:.2e} (bar {TOL:.0e})")
+
+
 def test_prefill_rejects_bad_arguments(pkg, small):
     """Host-side validation before any launch: an empty prompt, a prompt past max_seq_len, a
     wrong embedding width, a pos3 of the wrong shape; the decoder's position is left unchanged."""
