@@ -1158,6 +1158,20 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
         if (me) prep_att(lp, layer, pos, iss);
         else iss();
       } else {
+        if (pi == 0 && last_layer && a.n_pos > 1) {
+          // position 0 feeds no head: of its last layer only the K/V entry is read later. The
+          // next step is position 1's layer-0 QKV; its input is prepared here.
+          auto iss = [&]() SH_INLINE { load_q(tq, 0); };
+          if (me) {
+            cp_prep_att(lp, layer, pos, iss);
+            cp_prep_input0(1, []() SH_INLINE {});
+          } else {
+            iss();
+          }
+          stamp(2 + wv);
+          ++nstep;
+          continue;
+        }
         auto iss = [&]() SH_INLINE { load_o(to, layer); };
         if (me) cp_prep_att(lp, layer, pos, iss);
         else iss();
