@@ -51,6 +51,7 @@ namespace pf {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float EPS = 1e-6f;                 // Qwen3RMSNorm eps (config rms_norm_eps)
 constexpr int BM = 128;                      // GEMM tile rows (columns TN: 64 or 128)
@@ -89,6 +90,17 @@ __device__ __forceinline__ bf16_t f2bh(float x) { return __builtin_bit_cast(bf16
 __device__ __forceinline__ uint32_t pack_bh(float lo, float hi) {
   const bf16x2 v = {(__bf16)lo, (__bf16)hi};
   return __builtin_bit_cast(uint32_t, v);
+}
+
+// Token-fragment layout of the row GEMM's token operand (a [rows][K] bf16 matrix of at most RM
+// rows, K a multiple of 32, rows allocated in whole 16-row blocks): element (m, k) sits where
+// lane (m & 15) + 16 ((k >> 3) & 3) of fragment (m >> 4, k >> 5) holds it in the
+// v_mfma_f32_16x16x32_bf16 B operand. A fragment is 64 x 16 contiguous bytes, so the GEMM reads it
+// with one fully coalesced load. (Rows of 16 lanes on 16 different rows cost the address unit
+// four times the cycles of the same bytes in contiguous order.) Eight consecutive k of one row stay
+// together.
+__device__ __forceinline__ size_t frag_at(int m, int k, int K) {
+  return ((((size_t)(m >> 4) * (K >> 5) + (k >> 5)) * 64 + ((k >> 3) & 3) * 16 + (m & 15)) << 3) + (k & 7);
 }
 
 __device__ __forceinline__ const bf16_t* tbl(const TTSLayerWeights* lw, int field) {
@@ -285,6 +297,142 @@ __global__ void __launch_bounds__(GT, TN == 128 ? 2 : 1) gemm_kernel(const GemmA
     }
 }
 
+// Token-row GEMM for prompts of at most RM tokens: all M rows in one workgroup, a tile of TN
+// weight rows (virtual columns). At this size the weights are the only large operand (the token
+// rows are at most 256 KB and stay in L2), so the kernel is a weight stream. Each workgroup
+// streams its own slice of the weights, and all the operands go straight into registers in the
+// v_mfma_f32_16x16x32_bf16 layout, with no LDS staging and no barrier in the K loop:
+// - weight block nb is the A operand: lane l holds 8 bf16 of weight row 16 nb + (l & 15) at
+//   k = 32 s + 8 (l >> 4);
+// - token block mb is the B operand: the same for token row 16 mb + (l & 15), read from the
+//   token-fragment layout (frag_at) as one contiguous 1 KB fragment. Blocks past the last row
+//   block read the last one, and the sums of rows past M are never stored.
+// The 4 waves split the workgroup's K range (g.kchunk = 4 x 32 x NST) into quarters. Each wave
+// keeps D steps of loads in flight. The quarter sums meet in LDS and are added in wave order,
+// then go through the GEMM's epilogue, or to the split-K partials when grid.z > 1. A SwiGLU
+// tile's first TN / 2 weight rows are gate rows of outputs TN / 2 x tile + 0 .. TN / 2 - 1, its
+// last TN / 2 the up rows of the same outputs; its output (the down projection's input) is
+// written in the token-fragment layout. This kernel never splits SwiGLU.
+constexpr int RM = 128;
+
+template <int WM, int EPI, int TN, int NST>
+__global__ void __launch_bounds__(GT, 2) gemm_rows_kernel(const GemmArgs g) {
+  static_assert(WM != W_DIRECT && TN % 32 == 0, "row GEMM: layer weights, 16-row blocks in pairs");
+  constexpr int NB = TN / 16, MB = RM / 16;
+  constexpr int D = NST < 4 ? NST : 4;
+  constexpr int RROW = TN + 4;                 // f32 LDS row of a quarter sum (16-byte aligned)
+  __shared__ __attribute__((aligned(16))) float red[4][RM * RROW];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, i = lane & 15, kg = lane >> 4;
+  const int n0 = blockIdx.x * TN;
+  const int k0 = blockIdx.z * g.kchunk + w * (32 * NST) + 8 * kg;
+  const TTSLayerWeights* lw = g.layers + g.layer;
+  const bf16_t* wp[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int n = n0 + 16 * nb + i;
+    const bf16_t* p;
+    if constexpr (WM == W_QKV) {
+      p = n < 2048 ? tbl(lw, 1) + (size_t)n * g.K
+                   : (n < 3072 ? tbl(lw, 2) + (size_t)(n - 2048) * g.K : tbl(lw, 3) + (size_t)(n - 3072) * g.K);
+    } else if constexpr (WM == W_O) {
+      p = tbl(lw, 6) + (size_t)n * g.K;
+    } else if constexpr (WM == W_GU) {
+      const int j = n0 / 2 + 16 * (nb % (NB / 2)) + i;
+      p = (nb < NB / 2 ? tbl(lw, 8) : tbl(lw, 9)) + (size_t)j * g.K;
+    } else {
+      p = tbl(lw, 10) + (size_t)n * g.K;
+    }
+    wp[nb] = p + k0;
+  }
+  const bf16_t* xp[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+    xp[mb] = g.A + (((size_t)min(mb, (g.M - 1) >> 4) * (g.K >> 5) + ((k0 - 8 * kg) >> 5)) * 64 + lane) * 8;
+
+  u32x4 wr[D][NB], xr[D][MB];
+  f32x4 acc[NB][MB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < D; ++s) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) wr[s][nb] = ldw(wp[nb] + 32 * s);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) xr[s][mb] = ldw(xp[mb] + 512 * s);
+  }
+#pragma unroll
+  for (int s = 0; s < NST; ++s) {
+    const int d = s % D;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        acc[nb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(wr[d][nb]), as_bf8(xr[d][mb]), acc[nb][mb], 0, 0, 0);
+    if (s + D < NST) {   // compile-time after unrolling
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) wr[d][nb] = ldw(wp[nb] + 32 * (s + D));
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) xr[d][mb] = ldw(xp[mb] + 512 * (s + D));
+    }
+  }
+
+  // D layout: lane l holds weight rows 4 (l >> 4) + e of token column l & 15
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+      *reinterpret_cast<f32x4*>(&red[w][(16 * mb + i) * RROW + 16 * nb + 4 * kg]) = acc[nb][mb];
+  __syncthreads();
+  auto qsum = [&](int off) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(&red[0][off]);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(&red[1][off]);
+    const f32x4 c = *reinterpret_cast<const f32x4*>(&red[2][off]);
+    const f32x4 e = *reinterpret_cast<const f32x4*>(&red[3][off]);
+    return ((a + b) + c) + e;
+  };
+  if constexpr (EPI == E_SWIGLU) {
+    constexpr int C4 = TN / 8;                 // groups of 4 outputs per token row
+#pragma unroll
+    for (int q = t; q < RM * C4; q += GT) {
+      const int m = q / C4, c = 4 * (q % C4);
+      if (m >= g.M) break;
+      const f32x4 gs = qsum(m * RROW + c), us = qsum(m * RROW + TN / 2 + c);
+      u32x2 o;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float a0 = rbh(silu_f(rbh(gs[2 * e]))) * rbh(us[2 * e]);
+        const float a1 = rbh(silu_f(rbh(gs[2 * e + 1]))) * rbh(us[2 * e + 1]);
+        o[e] = pack_bh(a0, a1);
+      }
+      *reinterpret_cast<u32x2*>(g.out + frag_at(m, n0 / 2 + c, g.ldo)) = o;
+    }
+  } else {
+    constexpr int C4 = TN / 4;
+#pragma unroll
+    for (int q = t; q < RM * C4; q += GT) {
+      const int m = q / C4, c = 4 * (q % C4);
+      if (m >= g.M) break;
+      const f32x4 v = qsum(m * RROW + c);
+      if (gridDim.z > 1) {
+        *reinterpret_cast<f32x4*>(g.part + (size_t)blockIdx.z * g.M * g.N + (size_t)m * g.N + n0 + c) = v;
+      } else if constexpr (EPI == E_RESID) {
+        const u32x2 r = *reinterpret_cast<const u32x2*>(g.res + (size_t)m * g.ldr + n0 + c);
+        u32x2 o;
+        o[0] = pack_bh(bflo(r[0]) + rbh(v[0]), bfhi(r[0]) + rbh(v[1]));
+        o[1] = pack_bh(bflo(r[1]) + rbh(v[2]), bfhi(r[1]) + rbh(v[3]));
+        *reinterpret_cast<u32x2*>(g.out + (size_t)m * g.ldo + n0 + c) = o;
+      } else {
+        u32x2 o;
+        o[0] = pack_bh(v[0], v[1]);
+        o[1] = pack_bh(v[2], v[3]);
+        *reinterpret_cast<u32x2*>(g.out + (size_t)m * g.ldo + n0 + c) = o;
+      }
+    }
+  }
+}
+
 // Sum of the split-K partials in split order, then the GEMM's epilogue; four consecutive
 // outputs per thread (16-byte partial loads; a SwiGLU group of four lies in one 32-column block).
 template <int EPI, int TN>
@@ -326,7 +474,7 @@ __global__ void __launch_bounds__(256) reduce_kernel(const GemmArgs g, int split
 // table is null. out_f32 (optional) receives the bf16 result widened to f32.
 __global__ void __launch_bounds__(256) rmsnorm_kernel(const bf16_t* x, int ldx, const TTSLayerWeights* layers,
                                                       int layer, int field, const bf16_t* gain, bf16_t* out,
-                                                      int ldo, float* out_f32, int M) {
+                                                      int ldo, float* out_f32, int M, int frag) {
   const int lane = threadIdx.x & 63;
   const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (m >= M) return;
@@ -361,7 +509,7 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const bf16_t* x, int ldx, 
         out_f32[e0 + 2 * e + 1] = b;
       }
     }
-    if (out) *reinterpret_cast<u32x4*>(out + (size_t)m * ldo + e0) = o;
+    if (out) *reinterpret_cast<u32x4*>(out + (frag ? frag_at(m, e0, ldo) : (size_t)m * ldo + e0)) = o;
   }
 }
 
@@ -462,7 +610,7 @@ __global__ void __launch_bounds__(256) reduce_rope_kernel(const GemmArgs g, int 
 // (h = bf16(h + bf16(sum))), then the RMSNorm of the new row with gain field `field` of layer
 // `nlayer` into xn (skipped when nlayer < 0): one launch instead of a reduction and a norm.
 __global__ void __launch_bounds__(256) reduce_resid_norm_kernel(const GemmArgs g, int splits, int nlayer, int field,
-                                                                bf16_t* xn) {
+                                                                bf16_t* xn, int frag) {
   __shared__ float red[4];
   const int m = blockIdx.x, t = threadIdx.x, lane = t & 63;
   const size_t stride = (size_t)g.M * g.N;
@@ -497,7 +645,7 @@ __global__ void __launch_bounds__(256) reduce_resid_norm_kernel(const GemmArgs g
   u32x2 o;
   o[0] = pack_bh(bflo(gw[0]) * rbh(hv[0] * rs), bfhi(gw[0]) * rbh(hv[1] * rs));
   o[1] = pack_bh(bflo(gw[1]) * rbh(hv[2] * rs), bfhi(gw[1]) * rbh(hv[3] * rs));
-  *reinterpret_cast<u32x2*>(xn + (size_t)m * HID + 4 * t) = o;
+  *reinterpret_cast<u32x2*>(xn + (frag ? frag_at(m, 4 * t, HID) : (size_t)m * HID + 4 * t)) = o;
 }
 
 // Causal GQA attention of S queries (positions p0 .. p0 + S - 1) over cache positions
@@ -536,7 +684,7 @@ __device__ __forceinline__ u32x2 lds_tr16(const bf16_t* p) {
 
 __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, const bf16_t* kc, const bf16_t* vc,
                                                        int layer, int max_seq, int p0, int S, bf16_t* att,
-                                                       float scale) {
+                                                       float scale, int frag) {
   __shared__ __attribute__((aligned(16))) char smem[ATT_SMEM];
   bf16_t* sq = reinterpret_cast<bf16_t*>(smem);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hf = lane >> 5, c = lane & 31;
@@ -727,7 +875,7 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
       for (int r = 0; r < 16; ++r) o[mb][r] += ob[((v - 1) * 64 + mb * 16 + r) * 64 + lane];
   const float rl = L > 0.0f ? 1.0f / L : 0.0f;
   // O^T layout: column = query c, register r of block mb = dim 32 mb + 8 (r >> 2) + 4 hf + (r & 3)
-  bf16_t* op = att + (size_t)i * (NQH * HDIM) + hq * HDIM;
+  const size_t orow = (size_t)i * (NQH * HDIM) + hq * HDIM;
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
@@ -736,7 +884,7 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
       u32x2 pk;
       pk[0] = pack_bh(o[mb][4 * rq] * rl, o[mb][4 * rq + 1] * rl);
       pk[1] = pack_bh(o[mb][4 * rq + 2] * rl, o[mb][4 * rq + 3] * rl);
-      *reinterpret_cast<u32x2*>(op + d0) = pk;
+      *reinterpret_cast<u32x2*>(att + (frag ? frag_at(i, hq * HDIM + d0, NQH * HDIM) : orow + d0)) = pk;
     }
 }
 
@@ -785,6 +933,16 @@ int splits_for(int M, int N, int K, bool swiglu = false) {
   return ks;
 }
 
+// The row GEMM (M <= RM) per projection: tile width and split count, for a grid of 192-256
+// workgroups (QKV 128 tiles x 2 splits, O and down 32 tiles x 8, gate/up 192 tiles unsplit)
+constexpr int rows_tn(int) { return 32; }
+constexpr int rows_ks(int wm) { return wm == W_QKV ? 2 : (wm == W_GU ? 1 : 8); }
+constexpr Shape shape_of(int wm) { return wm == W_QKV ? kQKV : (wm == W_O ? kO : (wm == W_GU ? kGU : kDown)); }
+int splits_of(int wm, int M) {
+  const Shape sh = shape_of(wm);
+  return M <= RM ? rows_ks(wm) : splits_for(M, sh.N, sh.K, wm == W_GU);
+}
+
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct Layout {
@@ -796,16 +954,18 @@ Layout layout(int S, int vocab) {
   size_t o = 0;
   auto take = [&](size_t bytes) { const size_t at = o; o = align256(o + bytes); return at; };
   L.h = take((size_t)S * HID * 2);
-  L.xn = take((size_t)S * HID * 2);
+  // the row GEMM's token operands hold whole 16-row blocks
+  const size_t SP = S <= RM ? (size_t)(S + 15) / 16 * 16 : (size_t)S;
+  L.xn = take(SP * HID * 2);
   L.qkv = take((size_t)S * QKVW * 2);
-  L.att = take((size_t)S * NQH * HDIM * 2);
-  L.act = take((size_t)S * INTER * 2);
+  L.att = take(SP * NQH * HDIM * 2);
+  L.act = take(SP * INTER * 2);
   L.hb = take(HID * 2);
   L.logits = take((size_t)(vocab > 0 ? vocab : MAXV) * 2);
   size_t pb = 0;
-  for (Shape sh : {kQKV, kO, kDown}) {
-    const int ks = splits_for(S, sh.N, sh.K);
-    if (ks > 1) pb = std::max(pb, (size_t)ks * S * sh.N * 4);
+  for (int wm : {W_QKV, W_O, W_DOWN}) {
+    const int ks = splits_of(wm, S);
+    if (ks > 1) pb = std::max(pb, (size_t)ks * S * shape_of(wm).N * 4);
   }
   const int ksh = splits_for(1, vocab > 0 ? vocab : MAXV, HID);
   if (ksh > 1) pb = std::max(pb, (size_t)ksh * (vocab > 0 ? vocab : MAXV) * 4);
@@ -828,6 +988,19 @@ void gemm_launch(const GemmArgs& g, int ks, bool reduce, hipStream_t st) {
 // `reduce` is false, else reduced here. Returns the split count (0 on a launch error).
 template <int WM, int EPI>
 int gemm(GemmArgs& g, hipStream_t st, bool reduce = true) {
+  if constexpr (WM != W_DIRECT) {
+    if (g.M <= RM) {
+      constexpr int TN = rows_tn(WM), KS = rows_ks(WM), K = shape_of(WM).K;
+      static_assert(K % (KS * 128) == 0 && (KS == 1 || EPI != E_SWIGLU), "row GEMM plan");
+      if (g.K != K || g.N != shape_of(WM).N) return 0;
+      g.kchunk = K / KS;
+      hipLaunchKernelGGL((gemm_rows_kernel<WM, EPI, TN, K / KS / 128>), dim3(g.N / TN, 1, KS), dim3(GT), 0, st, g);
+      if (KS > 1 && reduce)
+        hipLaunchKernelGGL((reduce_kernel<EPI, 64>), dim3((unsigned)(((long)g.M * g.N / 4 + 255) / 256)), dim3(256), 0,
+                           st, g, KS);
+      return hipGetLastError() == hipSuccess ? KS : 0;
+    }
+  }
   const int ks = splits_for(g.M, g.N, g.K, EPI == E_SWIGLU);
   g.kchunk = g.K / ks;
   if (tile_n(g.M) == 128) gemm_launch<WM, EPI, 128>(g, ks, reduce, st);
@@ -881,12 +1054,14 @@ hipError_t qtts_backbone_prefill(void* workspace, size_t workspace_bytes, const 
   const auto* sn = static_cast<const bf16_t*>(sin_table);
   const float scale = 1.0f / sqrtf((float)HDIM);
   const unsigned norm_grid = (unsigned)((S + 3) / 4);
+  // prompts the row GEMM takes: its token operands (xn, att, act) in the token-fragment layout
+  const int frag = S <= RM ? 1 : 0;
 
   hipError_t e = hipMemcpyAsync(h, input_embeddings, (size_t)S * HID * 2, hipMemcpyDeviceToDevice, stream);
   if (e != hipSuccess) return e;
   // layer 0's input norm; later input norms come with the previous layer's down projection
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(norm_grid), dim3(256), 0, stream, h, HID, layer_weights, 0, 0,
-                     (const bf16_t*)nullptr, xn, HID, (float*)nullptr, S);
+                     (const bf16_t*)nullptr, xn, HID, (float*)nullptr, S, frag);
   const unsigned rows = (unsigned)S;
   for (int l = 0; l < num_layers; ++l) {
     GemmArgs g{};
@@ -905,15 +1080,15 @@ hipError_t qtts_backbone_prefill(void* workspace, size_t workspace_bytes, const 
       hipLaunchKernelGGL(rope_kv_kernel, dim3(rows), dim3(256), 0, stream, qkv, layer_weights, l, cs, sn, pos3, position,
                          S, kc, vc, max_seq_len);
     hipLaunchKernelGGL(attn_kernel, dim3((S + 31) / 32 * NQH), dim3(64 * AW), 0, stream, qkv, kc, vc, l, max_seq_len,
-                       position, S, att, scale);
+                       position, S, att, scale, frag);
     // O + residual, then the post-attention norm (fused with the split-K reduction)
     g.A = att; g.lda = NQH * HDIM; g.N = kO.N; g.K = kO.K; g.out = h; g.ldo = HID; g.res = h; g.ldr = HID;
     if ((ks = gemm<W_O, E_RESID>(g, stream, false)) == 0) return hipGetLastError();
     if (ks > 1)
-      hipLaunchKernelGGL(reduce_resid_norm_kernel, dim3(rows), dim3(256), 0, stream, g, ks, l, 7, xn);
+      hipLaunchKernelGGL(reduce_resid_norm_kernel, dim3(rows), dim3(256), 0, stream, g, ks, l, 7, xn, frag);
     else
       hipLaunchKernelGGL(rmsnorm_kernel, dim3(norm_grid), dim3(256), 0, stream, h, HID, layer_weights, l, 7,
-                         (const bf16_t*)nullptr, xn, HID, (float*)nullptr, S);
+                         (const bf16_t*)nullptr, xn, HID, (float*)nullptr, S, frag);
     g.A = xn; g.lda = HID; g.N = kGU.N; g.K = kGU.K; g.out = act; g.ldo = INTER; g.res = nullptr;
     if (gemm<W_GU, E_SWIGLU>(g, stream) == 0) return hipGetLastError();
     // down + residual, then the next layer's input norm (fused with the split-K reduction)
@@ -921,15 +1096,15 @@ hipError_t qtts_backbone_prefill(void* workspace, size_t workspace_bytes, const 
     g.A = act; g.lda = INTER; g.N = kDown.N; g.K = kDown.K; g.out = h; g.ldo = HID; g.res = h; g.ldr = HID;
     if ((ks = gemm<W_DOWN, E_RESID>(g, stream, false)) == 0) return hipGetLastError();
     if (ks > 1)
-      hipLaunchKernelGGL(reduce_resid_norm_kernel, dim3(rows), dim3(256), 0, stream, g, ks, nl, 0, xn);
+      hipLaunchKernelGGL(reduce_resid_norm_kernel, dim3(rows), dim3(256), 0, stream, g, ks, nl, 0, xn, frag);
     else if (nl >= 0)
       hipLaunchKernelGGL(rmsnorm_kernel, dim3(norm_grid), dim3(256), 0, stream, h, HID, layer_weights, nl, 0,
-                         (const bf16_t*)nullptr, xn, HID, (float*)nullptr, S);
+                         (const bf16_t*)nullptr, xn, HID, (float*)nullptr, S, frag);
   }
   // final norm of the last token -> hidden (bf16 values; f32 copy for the caller)
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(256), 0, stream, h + (size_t)(S - 1) * HID, HID,
                      (const TTSLayerWeights*)nullptr, 0, 0, static_cast<const bf16_t*>(final_norm_weight), hb, HID,
-                     out_hidden, 1);
+                     out_hidden, 1, 0);
   if (codec_head != nullptr) {
     bf16_t* lg = reinterpret_cast<bf16_t*>(ws + L.logits);
     GemmArgs g{};
