@@ -22,13 +22,17 @@
 //
 // Kernels (the host loop over layers is in qtts_backbone_prefill below):
 //   rmsnorm_kernel   one wave per token
-//   gemm_kernel      C = A W^T, tile 128 x 64 (4 waves, each 32 rows x 2 MFMA 32x32x16 blocks)
-//                    or, from 256 rows on, 128 x 128 (2 x 2 waves of 64 x 64), K steps of 64,
-//                    LDS double buffer + 2 (3 for 128 x 128) register stages of branch-free
-//                    loads, split-K over grid.z when the tile grid alone
-//                    would leave CUs idle (partials in f32, summed in a fixed order by
-//                    reduce_kernel); epilogues: store, residual add, SwiGLU (gate and up rows
-//                    interleaved by 32 in one tile)
+//   gemm_rows_kernel C = A W^T for prompts of at most 128 tokens: all rows in one workgroup, a
+//                    32-row weight slice, operands straight into registers (the token operand
+//                    in the token-fragment layout its producers write), 4 waves splitting K
+//   gemm_dma_kernel  C = A W^T from 256 rows on: 128 x 128 tiles (2 x 2 waves of 64 x 64),
+//                    K steps of 64 copied global -> LDS by DMA through 2-3 swizzled stages
+//   gemm_kernel      C = A W^T for 129-255 rows and the codec head: 128 x 64 tiles (4 waves,
+//                    each 32 rows x 2 MFMA 32x32x16 blocks), K steps of 128, LDS double buffer
+//                    + 2 register stages of branch-free loads
+//                    All three: split-K over grid.z when the tile grid alone would leave CUs
+//                    idle (partials in f32, summed in a fixed order by the reductions);
+//                    epilogues: store, residual add, SwiGLU
 //   rope_kv_kernel   q/k RMSNorm + interleaved mRoPE, K/V cache write, one workgroup per token
 //                    (fused into the split-K reduction of QKV when split: reduce_rope_kernel)
 //   reduce_resid_norm_kernel  split-K O / down: sums, residual add and the next RMSNorm per token
@@ -58,7 +62,7 @@ constexpr int BM = 128;                      // GEMM tile rows (columns TN: 64 o
 constexpr int GT = 256;                      // GEMM threads (4 waves)
 // K step of a TN-column tile: 128 for the 64-column (small-M, latency-bound) tiles, whose short
 // K loops then take half the load round trips; 64 for the 128-column tiles
-template <int TN> constexpr int bk_of() { return TN == 64 ? 128 : 64; }
+template <int TN> constexpr int bk_of() { return TN == 64 ? 128 : 64; }  // 128-column tiles: gemm_dma_kernel
 constexpr int QKVW = 4096;                   // q | k | v row of one token
 constexpr int QROW = 136;                    // LDS row of the query block: 128 dims + 16-byte pad
 constexpr int MAX_SPLIT = 16;
@@ -141,51 +145,52 @@ __device__ __forceinline__ int swiglu_gate_col(int j) {
   return TN * tt + 64 * (r >> 5) + (r & 31);
 }
 
-// C = A W^T on a BM x TN tile. TN = 64: wave w owns rows 32 w .. 32 w + 31 and both 32-column
-// blocks. TN = 128: waves form 2 x 2, wave w owns rows 64 (w & 1) .. + 63 (two 32-row blocks)
-// and columns 64 (w >> 1) .. + 63 (two 32-column blocks): one LDS operand read per MFMA.
+// Weight row of virtual column n of a layer projection (SwiGLU: the tile interleave of swiglu_row)
+template <int WM, int TN>
+__device__ __forceinline__ const bf16_t* weight_row(const GemmArgs& g, const TTSLayerWeights* lw, int n) {
+  if constexpr (WM == W_DIRECT) {
+    return g.B + (size_t)n * g.K;
+  } else if constexpr (WM == W_QKV) {
+    return n < 2048 ? tbl(lw, 1) + (size_t)n * g.K
+                    : (n < 3072 ? tbl(lw, 2) + (size_t)(n - 2048) * g.K : tbl(lw, 3) + (size_t)(n - 3072) * g.K);
+  } else if constexpr (WM == W_O) {
+    return tbl(lw, 6) + (size_t)n * g.K;
+  } else if constexpr (WM == W_GU) {
+    bool up;
+    const int row = swiglu_row<TN>(n, up);
+    return (up ? tbl(lw, 9) : tbl(lw, 8)) + (size_t)row * g.K;
+  } else {
+    return tbl(lw, 10) + (size_t)n * g.K;
+  }
+}
+
+// C = A W^T on a BM x 64 tile (prompts of 129-255 tokens, and the codec head): wave w owns rows
+// 32 w .. 32 w + 31 and both 32-column blocks; K steps of 128 through an LDS double buffer fed
+// from register stages.
 template <int WM, int EPI, int TN>
-__global__ void __launch_bounds__(GT, TN == 128 ? 2 : 1) gemm_kernel(const GemmArgs g) {
+__global__ void __launch_bounds__(GT, 1) gemm_kernel(const GemmArgs g) {
+  static_assert(TN == 64, "the 128-column tiles run in gemm_dma_kernel");
   constexpr int BK = bk_of<TN>();
   constexpr int LROW = BK + 8;                     // LDS row (bf16): 16-byte aligned, skewed banks
   constexpr int CPR = BK / 8;                      // 16-byte chunks per tile row
   constexpr int RPP = GT / CPR;                    // tile rows one pass of the workgroup loads
   constexpr int NAR = BM / RPP;                    // A chunks per thread
   constexpr int NBR = TN / RPP;                    // B chunks per thread
-  constexpr int MBW = TN == 128 ? 2 : 1;          // 32-row blocks per wave
+  constexpr int MBW = 1;                           // 32-row blocks per wave
   __shared__ __attribute__((aligned(16))) bf16_t sa[2][BM * LROW];
   __shared__ __attribute__((aligned(16))) bf16_t sb[2][TN * LROW];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * TN;
   const int kbeg = blockIdx.z * g.kchunk, nk = g.kchunk / BK;
   const int lr = t / CPR, lc = (t % CPR) * 8;   // this thread's load row (within RPP) and column
-  const int wr0 = TN == 128 ? 64 * (w & 1) : 32 * w;   // wave's first tile row
-  const int wc0 = TN == 128 ? 64 * (w >> 1) : 0;       // wave's first tile column
+  const int wr0 = 32 * w, wc0 = 0;                // wave's first tile row and column
 
   // weight rows this thread stages (virtual columns n0 + lr + 32 i)
   const bf16_t* brow[NBR];
   {
     const TTSLayerWeights* lw = g.layers + g.layer;
 #pragma unroll
-    for (int i = 0; i < NBR; ++i) {
-      const int n = n0 + lr + RPP * i;
-      const bf16_t* p;
-      if constexpr (WM == W_DIRECT) {
-        p = g.B + (size_t)n * g.K;
-      } else if constexpr (WM == W_QKV) {
-        p = n < 2048 ? tbl(lw, 1) + (size_t)n * g.K
-                     : (n < 3072 ? tbl(lw, 2) + (size_t)(n - 2048) * g.K : tbl(lw, 3) + (size_t)(n - 3072) * g.K);
-      } else if constexpr (WM == W_O) {
-        p = tbl(lw, 6) + (size_t)n * g.K;
-      } else if constexpr (WM == W_GU) {
-        bool up;
-        const int row = swiglu_row<TN>(n, up);
-        p = (up ? tbl(lw, 9) : tbl(lw, 8)) + (size_t)row * g.K;
-      } else {
-        p = tbl(lw, 10) + (size_t)n * g.K;
-      }
-      brow[i] = p + kbeg + lc;
-    }
+    for (int i = 0; i < NBR; ++i) brow[i] = weight_row<WM, TN>(g, lw, n0 + lr + RPP * i) + kbeg + lc;
   }
   const bf16_t* arow[NAR];
   bool aok[NAR];
@@ -200,7 +205,7 @@ __global__ void __launch_bounds__(GT, TN == 128 ? 2 : 1) gemm_kernel(const GemmA
   // kt + 1 moves to LDS). Every load is issued unconditionally (rows past M read row 0 and are
   // zeroed afterwards; K steps past the end reload the last one): a load under a branch makes the
   // compiler wait for all outstanding loads instead of just the old ones.
-  constexpr int NST = TN == 128 ? 3 : 2;   // a third stage on 64-column tiles measured 5-10% slower
+  constexpr int NST = 2;   // a third stage measured 5-10% slower
   u32x4 ra[NST][NAR], rb[NST][NBR];
   auto gload = [&](int k0, u32x4 (&a)[NAR], u32x4 (&b)[NBR]) {
 #pragma unroll
@@ -260,10 +265,7 @@ __global__ void __launch_bounds__(GT, TN == 128 ? 2 : 1) gemm_kernel(const GemmA
   __syncthreads();
   for (int kt = 0; kt < nk; kt += NST) {
     step(kt, ra[0], rb[0], ra[1], rb[1]);
-    if (kt + 1 < nk) step(kt + 1, ra[1], rb[1], ra[2 % NST], rb[2 % NST]);
-    if constexpr (NST == 3) {
-      if (kt + 2 < nk) step(kt + 2, ra[2], rb[2], ra[0], rb[0]);
-    }
+    if (kt + 1 < nk) step(kt + 1, ra[1], rb[1], ra[0], rb[0]);
   }
 
   // D layout of a 32x32 block: lane column lane & 31; register r holds row
@@ -431,6 +433,134 @@ __global__ void __launch_bounds__(GT, 2) gemm_rows_kernel(const GemmArgs g) {
       }
     }
   }
+}
+
+#define QTTS_PF_INLINE __attribute__((always_inline))
+typedef __attribute__((address_space(1))) void gvoid_t;
+typedef __attribute__((address_space(3))) void lvoid_t;
+
+// C = A W^T on a 128 x 128 tile (prompts from 256 tokens on), K steps of 64, with the operands
+// copied from global memory straight into LDS (global_load_lds_dwordx4: each wave instruction
+// writes 64 x 16 bytes at a wave-uniform LDS address) through NS stages. No register staging and
+// no LDS store instructions; one barrier per K step.
+// - LDS tile layout: row r of a stage holds its 8 16-byte k-chunks with chunk c at position
+//   c ^ (r & 7). A DMA instruction covers 8 rows; lane l writes position l & 7 of row l >> 3 and
+//   so loads chunk (l & 7) ^ (r & 7) of that row: 8 lanes read one 128-byte row segment.
+// - The XOR swizzle makes the MFMA operand reads (32 rows at one chunk) conflict-free.
+// - Waves form 2 x 2; wave w owns rows 64 (w & 1) .. + 63 and columns 64 (w >> 1) .. + 63 (two
+//   32 x 32 MFMA blocks each way), as in gemm_kernel's 128-column tile, and the epilogues match.
+// - Rows past M read row M - 1; their sums are never stored.
+// - The wait before each barrier counts this wave's DMA instructions still in flight: the
+//   compiler does not track LDS writes made by DMA.
+template <int WM, int EPI, int NS>
+__global__ void __launch_bounds__(GT, NS <= 2 ? 2 : 1) gemm_dma_kernel(const GemmArgs g) {
+  constexpr int TN = 128, TM = 128, BK = 64;
+  constexpr int STAGE = (TM + TN) * BK * 2;        // bytes of one stage (A then B)
+  constexpr int NIA = TM * BK * 2 / 1024 / 4;      // DMA instructions per wave for A (4)
+  constexpr int NIB = TN * BK * 2 / 1024 / 4;      // ... and for B (4)
+  constexpr int NIW = NIA + NIB;
+  static_assert(NS >= 2 && NS <= 4 && NIW <= 15, "stages / vmcnt field");
+  __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int m0 = blockIdx.y * TM, n0 = blockIdx.x * TN;
+  const int kbeg = blockIdx.z * g.kchunk, nk = g.kchunk / BK;
+  const TTSLayerWeights* lw = g.layers + g.layer;
+
+  // this lane's source rows: instruction i of the wave covers tile rows 8 (NIA w + i) .. + 7
+  const bf16_t* asrc[NIA];
+  const bf16_t* bsrc[NIB];
+#pragma unroll
+  for (int i = 0; i < NIA; ++i) {
+    const int r = 8 * (NIA * w + i) + (lane >> 3);
+    const int c = (lane & 7) ^ (r & 7);
+    asrc[i] = g.A + (size_t)min(m0 + r, g.M - 1) * g.lda + kbeg + 8 * c;
+  }
+#pragma unroll
+  for (int i = 0; i < NIB; ++i) {
+    const int r = 8 * (NIB * w + i) + (lane >> 3);
+    const int c = (lane & 7) ^ (r & 7);
+    bsrc[i] = weight_row<WM, TN>(g, lw, n0 + r) + kbeg + 8 * c;
+  }
+  // stage s <- K step kt (clamped: steps past the end reload the last one)
+  auto issue = [&](int s, int kt) QTTS_PF_INLINE {
+    const int k = BK * min(kt, nk - 1);
+    char* base = lds + s * STAGE;
+#pragma unroll
+    for (int i = 0; i < NIA; ++i)
+      __builtin_amdgcn_global_load_lds((gvoid_t*)(asrc[i] + k), (lvoid_t*)(base + 1024 * (NIA * w + i)), 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < NIB; ++i)
+      __builtin_amdgcn_global_load_lds((gvoid_t*)(bsrc[i] + k), (lvoid_t*)(base + TM * BK * 2 + 1024 * (NIB * w + i)),
+                                       16, 0, 0);
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mb][nb][r] = 0.0f;
+  const int wr0 = 64 * (w & 1), wc0 = 64 * (w >> 1), hk = lane >> 5;
+  // byte offset of (row r, chunk c) in a stage's A or B part
+  auto at = [](int r, int c) { return (r * 8 + (c ^ (r & 7))) * 16; };
+  auto compute = [&](int s) QTTS_PF_INLINE {
+    const char* a = lds + s * STAGE;
+    const char* b = a + TM * BK * 2;
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      const int c = 2 * kk + hk;
+      bf16x8 av[2], bv[2];
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) av[mb] = as_bf8(*reinterpret_cast<const u32x4*>(a + at(wr0 + 32 * mb + (lane & 31), c)));
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) bv[nb] = as_bf8(*reinterpret_cast<const u32x4*>(b + at(wc0 + 32 * nb + (lane & 31), c)));
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+          acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[mb], bv[nb], acc[mb][nb], 0, 0, 0);
+    }
+  };
+
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s) issue(s, s);
+  for (int kt = 0; kt < nk; ++kt) {
+    // this wave's DMA for step kt has landed when at most (NS - 2) stages' instructions remain
+    __builtin_amdgcn_s_waitcnt(0x0F70 | ((NS - 2) * NIW));
+    __builtin_amdgcn_s_barrier();   // every wave's step kt is in LDS; step kt - 1's buffer is free
+    issue((kt + NS - 1) % NS, kt + NS - 1);
+    compute(kt % NS);
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);   // no DMA may still target LDS when the workgroup ends
+
+  const int col = lane & 31, hrow = 4 * (lane >> 5);
+  if (gridDim.z > 1) {
+    float* P = g.part + (size_t)blockIdx.z * g.M * g.N;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + wr0 + 32 * mb + 8 * (r >> 2) + hrow + (r & 3);
+          if (m < g.M) P[(size_t)m * g.N + n0 + wc0 + 32 * nb + col] = acc[mb][nb][r];
+        }
+    return;
+  }
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = m0 + wr0 + 32 * mb + 8 * (r >> 2) + hrow + (r & 3);
+      if (m >= g.M) continue;
+      if constexpr (EPI == E_SWIGLU) {
+        epilogue_swiglu(g, m, n0 / 2 + wc0 / 2 + col, acc[mb][0][r], acc[mb][1][r]);
+      } else {
+        epilogue<EPI>(g, m, n0 + wc0 + col, acc[mb][0][r]);
+        epilogue<EPI>(g, m, n0 + wc0 + 32 + col, acc[mb][1][r]);
+      }
+    }
 }
 
 // Sum of the split-K partials in split order, then the GEMM's epilogue; four consecutive
@@ -1003,8 +1133,21 @@ int gemm(GemmArgs& g, hipStream_t st, bool reduce = true) {
   }
   const int ks = splits_for(g.M, g.N, g.K, EPI == E_SWIGLU);
   g.kchunk = g.K / ks;
-  if (tile_n(g.M) == 128) gemm_launch<WM, EPI, 128>(g, ks, reduce, st);
-  else gemm_launch<WM, EPI, 64>(g, ks, reduce, st);
+  if (tile_n(g.M) == 128) {
+    // two stages and two workgroups per CU when the grid covers the CUs twice or more; a grid of
+    // at most one workgroup per CU (the split O and down projections) takes three stages instead
+    const dim3 grid(g.N / 128, (g.M + 127) / 128, ks);
+    if (grid.x * grid.y * grid.z > 256)
+      hipLaunchKernelGGL((gemm_dma_kernel<WM, EPI, 2>), grid, dim3(GT), 0, st, g);
+    else
+      hipLaunchKernelGGL((gemm_dma_kernel<WM, EPI, 3>), grid, dim3(GT), 0, st, g);
+    if (ks > 1 && reduce) {
+      const long nout = (long)g.M * (EPI == E_SWIGLU ? g.N / 2 : g.N) / 4;
+      hipLaunchKernelGGL((reduce_kernel<EPI, 128>), dim3((unsigned)((nout + 255) / 256)), dim3(256), 0, st, g, ks);
+    }
+  } else {
+    gemm_launch<WM, EPI, 64>(g, ks, reduce, st);
+  }
   return hipGetLastError() == hipSuccess ? ks : 0;
 }
 
