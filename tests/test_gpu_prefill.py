@@ -43,11 +43,14 @@ def _compare(bb, orc, p0, S, hidden, hidden_ref, label, bars=(TOL, TOL, TOL)):
     return eh
 
 
-@pytest.mark.parametrize("S", [1, 7, 64, 130, 333, 1100])
+@pytest.mark.parametrize("S", [1, 7, 64, 128, 130, 256, 333, 1100])
 def test_prefill_two_layers(pkg, small, S):
-    """Prompt lengths across the tile edges: one token, a partial 32-query block, exactly two
-    blocks, a partial 128-row GEMM tile, several tiles with a ragged last one, and a long prompt
-    (the widest split-K target, 35 query blocks, a ragged last block)."""
+    """Prompt lengths across the tile edges and GEMM forms: one token and 7 (a partial 32-query
+    block; the row GEMM's partial 16-row block), 64 (two query blocks; 4 whole row blocks), 128
+    (the row GEMM's largest prompt, all 8 row blocks), 130 (the 64-column tile, a partial 128-row
+    tile), 256 (the smallest prompt of the DMA-fed 128 x 128 GEMM), several tiles with a ragged
+    last one, and a long prompt (the widest split-K target, 35 query blocks, a ragged last
+    block)."""
     dsd, tw = small
     ms = 512 if S <= 512 else 2048
     bb = pkg.TTSMegakernelGenerator(model=dsd, max_seq_len=ms)
