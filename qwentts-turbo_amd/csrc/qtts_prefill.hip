@@ -85,6 +85,18 @@ struct GemmArgs {
   float* part;                     // split-K partials [splits][M][N]
 };
 
+// What the QKV GEMM needs to finish a head itself (q/k RMSNorm, RoPE, the K/V cache write);
+// kc == nullptr: plain store
+struct RopeArgs {
+  const bf16_t* cos_t;
+  const bf16_t* sin_t;
+  const int* pos3;                 // [3][M] (t, h, w) table rows, or nullptr: row = p0 + token
+  int p0;
+  bf16_t* kc;
+  bf16_t* vc;
+  int max_seq;
+};
+
 __device__ __forceinline__ bf16x8 as_bf8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 // bf16 rounding (round to nearest even) with gfx950's conversion instruction
@@ -452,8 +464,12 @@ typedef __attribute__((address_space(3))) void lvoid_t;
 // - Rows past M read row M - 1; their sums are never stored.
 // - The wait before each barrier counts this wave's DMA instructions still in flight: the
 //   compiler does not track LDS writes made by DMA.
+// - Unsplit QKV with rope arguments: a tile is one head of 128 tokens, and the epilogue finishes
+//   it as rope_kv_row does: bf16 tile through LDS, then two threads per token (32 channel pairs
+//   (d, d + 64) each) for the q/k RMSNorm and the interleaved mRoPE. q goes back to the QKV rows;
+//   k and v go to the cache.
 template <int WM, int EPI, int NS>
-__global__ void __launch_bounds__(GT, NS <= 2 ? 2 : 1) gemm_dma_kernel(const GemmArgs g) {
+__global__ void __launch_bounds__(GT, NS <= 2 ? 2 : 1) gemm_dma_kernel(const GemmArgs g, const RopeArgs ra) {
   constexpr int TN = 128, TM = 128, BK = 64;
   constexpr int STAGE = (TM + TN) * BK * 2;        // bytes of one stage (A then B)
   constexpr int NIA = TM * BK * 2 / 1024 / 4;      // DMA instructions per wave for A (4)
@@ -535,6 +551,131 @@ __global__ void __launch_bounds__(GT, NS <= 2 ? 2 : 1) gemm_dma_kernel(const Gem
   __builtin_amdgcn_s_waitcnt(0x0F70);   // no DMA may still target LDS when the workgroup ends
 
   const int col = lane & 31, hrow = 4 * (lane >> 5);
+  if constexpr (WM == W_QKV && EPI == E_STORE) {
+    if (ra.kc != nullptr) {
+      constexpr int TR = HDIM + 8;   // bf16 row of the staged head tile (16-byte aligned, skewed)
+      bf16_t* T = reinterpret_cast<bf16_t*>(lds);
+      __syncthreads();   // every wave's DMA has landed and its last MFMA reads are done
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            T[(wr0 + 32 * mb + 8 * (r >> 2) + hrow + (r & 3)) * TR + wc0 + 32 * nb + col] = f2bh(acc[mb][nb][r]);
+      __syncthreads();
+      const int head = n0 / HDIM;   // q heads 0..15, k heads 16..23, v heads 24..31
+      if (head >= NQH + NKVH) {
+        bf16_t* vbase = ra.vc + ((size_t)g.layer * NKVH + (head - NQH - NKVH)) * ra.max_seq * HDIM;
+        for (int q = t; q < TM * 16; q += GT) {
+          const int row = q >> 4, ch = 8 * (q & 15), m = m0 + row;
+          if (m < g.M)
+            *reinterpret_cast<u32x4*>(vbase + (size_t)(ra.p0 + m) * HDIM + ch) =
+                *reinterpret_cast<const u32x4*>(&T[row * TR + ch]);
+        }
+        return;
+      }
+      const int row = t >> 1, hf = t & 1, m = min(m0 + row, g.M - 1);
+      const bf16_t* tr = &T[row * TR + 32 * hf];
+      float ss = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(tr + 8 * c);
+        const u32x4 b = *reinterpret_cast<const u32x4*>(tr + 64 + 8 * c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          ss += bflo(a[e]) * bflo(a[e]) + bflo(b[e]) * bflo(b[e]);
+          ss += bfhi(a[e]) * bfhi(a[e]) + bfhi(b[e]) * bfhi(b[e]);
+        }
+      }
+      ss += __shfl_xor(ss, 1, 64);
+      const float rs = 1.0f / sqrtf(ss / (float)HDIM + EPS);
+      const bool isq = head < NQH;
+      const bf16_t* gn = tbl(lw, isq ? 4 : 5);
+      // table rows of the three sections (t, h, w); channel d < 60 takes h when d % 3 == 1 and w
+      // when d % 3 == 2, every other channel t (the same row for d and d + 64)
+      const int pos = ra.p0 + m;
+      int rsec[3];
+#pragma unroll
+      for (int j = 0; j < 3; ++j) rsec[j] = ra.pos3 ? min(max(ra.pos3[j * g.M + m], 0), ra.max_seq - 1) : pos;
+      bf16_t* dst = isq ? g.out + (size_t)m * g.ldo + n0
+                        : ra.kc + (((size_t)g.layer * NKVH + (head - NQH)) * ra.max_seq + pos) * HDIM;
+      // 8 channel pairs (d0 + e, d0 + 64 + e); cs/sn: this chunk's cos and sin for d and d + 64,
+      // already picked per section
+      auto finish = [&](int c, const float (&c0)[8], const float (&c1)[8], const float (&s0)[8],
+                        const float (&s1)[8], const u32x4& g0, const u32x4& g1) QTTS_PF_INLINE {
+        const int d0 = 32 * hf + 8 * c;
+        const u32x4 a = *reinterpret_cast<const u32x4*>(tr + 8 * c);
+        const u32x4 b = *reinterpret_cast<const u32x4*>(tr + 64 + 8 * c);
+        u32x4 o0, o1;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float r0[2], r1[2];
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2) {
+            const int k = 2 * e + h2;
+            const float x0 = h2 ? bfhi(a[e]) : bflo(a[e]), x1 = h2 ? bfhi(b[e]) : bflo(b[e]);
+            const float ga = h2 ? bfhi(g0[e]) : bflo(g0[e]), gb = h2 ? bfhi(g1[e]) : bflo(g1[e]);
+            const float y0 = rbh(ga * rbh(x0 * rs)), y1 = rbh(gb * rbh(x1 * rs));
+            r0[h2] = rbh(y0 * c0[k]) + rbh(-y1 * s0[k]);
+            r1[h2] = rbh(y1 * c1[k]) + rbh(y0 * s1[k]);
+          }
+          o0[e] = pack_bh(r0[0], r0[1]);
+          o1[e] = pack_bh(r1[0], r1[1]);
+        }
+        if (m0 + row < g.M) {
+          *reinterpret_cast<u32x4*>(dst + d0) = o0;
+          *reinterpret_cast<u32x4*>(dst + d0 + 64) = o1;
+        }
+      };
+      auto unpack8 = [](const u32x4& v, float (&f)[8]) QTTS_PF_INLINE {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { f[2 * e] = bflo(v[e]); f[2 * e + 1] = bfhi(v[e]); }
+      };
+      if (ra.pos3 == nullptr) {
+        // one table row per token: every load of the 4 chunks issued before the first use
+        const bf16_t* cr = ra.cos_t + (size_t)pos * HDIM + 32 * hf;
+        const bf16_t* sr = ra.sin_t + (size_t)pos * HDIM + 32 * hf;
+        u32x4 vc0[4], vc1[4], vs0[4], vs1[4], vg0[4], vg1[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          vc0[c] = ldw(cr + 8 * c); vc1[c] = ldw(cr + 64 + 8 * c);
+          vs0[c] = ldw(sr + 8 * c); vs1[c] = ldw(sr + 64 + 8 * c);
+          vg0[c] = ldw(gn + 32 * hf + 8 * c); vg1[c] = ldw(gn + 64 + 32 * hf + 8 * c);
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          float c0[8], c1[8], s0[8], s1[8];
+          unpack8(vc0[c], c0); unpack8(vc1[c], c1); unpack8(vs0[c], s0); unpack8(vs1[c], s1);
+          finish(c, c0, c1, s0, s1, vg0[c], vg1[c]);
+        }
+      } else {
+#pragma unroll 1
+        for (int c = 0; c < 4; ++c) {
+          const int d0 = 32 * hf + 8 * c;
+          u32x4 cs0[3], cs1[3], sn0[3], sn1[3];
+#pragma unroll
+          for (int j = 0; j < 3; ++j) {
+            const size_t ro = (size_t)rsec[j] * HDIM + d0;
+            cs0[j] = ldw(ra.cos_t + ro); cs1[j] = ldw(ra.cos_t + ro + 64);
+            sn0[j] = ldw(ra.sin_t + ro); sn1[j] = ldw(ra.sin_t + ro + 64);
+          }
+          float c0[8], c1[8], s0[8], s1[8];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const int d = d0 + k, sec = (d < 60 && d % 3 == 1) ? 1 : ((d < 60 && d % 3 == 2) ? 2 : 0);
+            auto pick = [&](const u32x4 (&v)[3]) {
+              const uint32_t wv = sec == 0 ? v[0][k >> 1] : (sec == 1 ? v[1][k >> 1] : v[2][k >> 1]);
+              return (k & 1) ? bfhi(wv) : bflo(wv);
+            };
+            c0[k] = pick(cs0); c1[k] = pick(cs1); s0[k] = pick(sn0); s1[k] = pick(sn1);
+          }
+          finish(c, c0, c1, s0, s1, ldw(gn + d0), ldw(gn + d0 + 64));
+        }
+      }
+      return;
+    }
+  }
   if (gridDim.z > 1) {
     float* P = g.part + (size_t)blockIdx.z * g.M * g.N;
 #pragma unroll
@@ -1115,9 +1256,10 @@ void gemm_launch(const GemmArgs& g, int ks, bool reduce, hipStream_t st) {
 }
 
 // Launches the GEMM; with split-K the partial sums are left in g.part for a fused consumer when
-// `reduce` is false, else reduced here. Returns the split count (0 on a launch error).
+// `reduce` is false, else reduced here. `rope` (QKV only): an unsplit 128-column QKV GEMM finishes
+// the heads itself (q/k-norm, RoPE, K/V write). Returns the split count (0 on a launch error).
 template <int WM, int EPI>
-int gemm(GemmArgs& g, hipStream_t st, bool reduce = true) {
+int gemm(GemmArgs& g, hipStream_t st, bool reduce = true, const RopeArgs* rope = nullptr) {
   if constexpr (WM != W_DIRECT) {
     if (g.M <= RM) {
       constexpr int TN = rows_tn(WM), KS = rows_ks(WM), K = shape_of(WM).K;
@@ -1137,10 +1279,11 @@ int gemm(GemmArgs& g, hipStream_t st, bool reduce = true) {
     // two stages and two workgroups per CU when the grid covers the CUs twice or more; a grid of
     // at most one workgroup per CU (the split O and down projections) takes three stages instead
     const dim3 grid(g.N / 128, (g.M + 127) / 128, ks);
+    const RopeArgs rr = (rope != nullptr && ks == 1) ? *rope : RopeArgs{};
     if (grid.x * grid.y * grid.z > 256)
-      hipLaunchKernelGGL((gemm_dma_kernel<WM, EPI, 2>), grid, dim3(GT), 0, st, g);
+      hipLaunchKernelGGL((gemm_dma_kernel<WM, EPI, 2>), grid, dim3(GT), 0, st, g, rr);
     else
-      hipLaunchKernelGGL((gemm_dma_kernel<WM, EPI, 3>), grid, dim3(GT), 0, st, g);
+      hipLaunchKernelGGL((gemm_dma_kernel<WM, EPI, 3>), grid, dim3(GT), 0, st, g, rr);
     if (ks > 1 && reduce) {
       const long nout = (long)g.M * (EPI == E_SWIGLU ? g.N / 2 : g.N) / 4;
       hipLaunchKernelGGL((reduce_kernel<EPI, 128>), dim3((unsigned)((nout + 255) / 256)), dim3(256), 0, st, g, ks);
@@ -1206,6 +1349,7 @@ hipError_t qtts_backbone_prefill(void* workspace, size_t workspace_bytes, const 
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(norm_grid), dim3(256), 0, stream, h, HID, layer_weights, 0, 0,
                      (const bf16_t*)nullptr, xn, HID, (float*)nullptr, S, frag);
   const unsigned rows = (unsigned)S;
+  const RopeArgs rope{cs, sn, pos3, position, kc, vc, max_seq_len};
   for (int l = 0; l < num_layers; ++l) {
     GemmArgs g{};
     g.layers = layer_weights;
@@ -1213,10 +1357,13 @@ hipError_t qtts_backbone_prefill(void* workspace, size_t workspace_bytes, const 
     g.M = S;
     g.part = part;
     int ks;
-    // QKV, then q/k-norm + RoPE + K/V write (fused with the split-K reduction)
+    // QKV, then q/k-norm + RoPE + K/V write: in the GEMM's epilogue (unsplit 128-column tiles), in
+    // the split-K reduction, or (64-column tiles, unsplit) in rope_kv_kernel
     g.A = xn; g.lda = HID; g.N = kQKV.N; g.K = kQKV.K; g.out = qkv; g.ldo = QKVW;
-    if ((ks = gemm<W_QKV, E_STORE>(g, stream, false)) == 0) return hipGetLastError();
-    if (ks > 1)
+    if ((ks = gemm<W_QKV, E_STORE>(g, stream, false, &rope)) == 0) return hipGetLastError();
+    if (ks == 1 && tile_n(S) == 128) {
+      // q/k-norm, RoPE and the K/V write ran in the QKV GEMM's epilogue
+    } else if (ks > 1)
       hipLaunchKernelGGL(reduce_rope_kernel, dim3(rows), dim3(256), 0, stream, g, ks, cs, sn, pos3, position, kc, vc,
                          max_seq_len);
     else

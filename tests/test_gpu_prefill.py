@@ -66,13 +66,16 @@ def test_prefill_two_layers(pkg, small, S):
     assert bb.position == S
 
 
-def test_prefill_after_prefix_and_distinct_mrope(pkg, small):
-    """A prompt continuing a cached prefix (positions 50..149 attend 0..149) with distinct
-    (t, h, w) rotary rows per token."""
+@pytest.mark.parametrize("S", [100, 1100])
+def test_prefill_after_prefix_and_distinct_mrope(pkg, small, S):
+    """A prompt continuing a cached prefix (positions 50..50 + S - 1 attend 0..50 + S - 1) with
+    distinct (t, h, w) rotary rows per token. At 1100 tokens the QKV GEMM is unsplit on 128-column
+    tiles and finishes each head (q/k-norm, RoPE, K/V write) in its own epilogue."""
     dsd, tw = small
-    p0, S = 50, 100
-    bb = pkg.TTSMegakernelGenerator(model=dsd, max_seq_len=512)
-    orc = DecoderOracle(tw.bb_layers, tw.bb_norm, 512, "backbone", "hf_bf16")
+    p0 = 50
+    ms = 512 if p0 + S <= 512 else 2048
+    bb = pkg.TTSMegakernelGenerator(model=dsd, max_seq_len=ms)
+    orc = DecoderOracle(tw.bb_layers, tw.bb_norm, ms, "backbone", "hf_bf16")
     g = torch.Generator().manual_seed(77)
     k = torch.randn(2, 8, p0, 128, generator=g).to(torch.bfloat16)
     v = torch.randn(2, 8, p0, 128, generator=g).to(torch.bfloat16)
@@ -88,7 +91,7 @@ def test_prefill_after_prefix_and_distinct_mrope(pkg, small):
     hr = None
     for i in range(S):
         hr, _ = orc.step(x[i], pos=p0 + i, pos3=[int(pos3[j, i]) for j in range(3)])
-    _compare(bb, orc, p0, S, h, hr, "prefill after prefix, mRoPE")
+    _compare(bb, orc, p0, S, h, hr, f"prefill after prefix, mRoPE, S={S}")
     assert bb.position == p0 + S
 
 
