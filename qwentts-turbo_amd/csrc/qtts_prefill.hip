@@ -11,10 +11,10 @@
 //   xn  = bf16(w * bf16(x * (1 / sqrt(mean(x^2) + eps))))              RMSNorm (:59-64)
 //   q,k,v = bf16(W xn); q,k per head through RMSNorm, then
 //   rope = bf16(bf16(q * cos) + bf16(rotate_half(q) * sin))            bf16 cos/sin tables
-//   s   = bf16(bf16(q . k) * scale); att = bf16((sum_j bf16(e^(s_j - m)) v_j) / sum_j e^(s_j - m))
-//         with the running max m: the softmax as flash-style attention kernels (torch's sdpa on
-//         bf16) round it, normalised after the P V product (eager torch rounds p = bf16(e / l)
-//         before it; :185-208)
+//   s   = scale * (q . k) in f32; att = bf16((sum_j bf16(e^(s_j - m)) v_j) / sum_j e^(s_j - m))
+//         with the running max m: the scores and softmax as flash-style attention kernels
+//         (torch's sdpa on bf16) keep and round them, normalised after the P V product (eager
+//         torch rounds s = bf16(bf16(q . k) * scale) and p = bf16(e / l) before it; :185-208)
 //   h1  = bf16(h + bf16(W_o att)); a = bf16(bf16(silu(bf16(W_g xn))) * bf16(W_u xn))
 //   h   = bf16(h1 + bf16(W_d a)); hidden = RMSNorm_final(h[S-1]); logits = bf16(W_head hidden)
 // The f32 sums run in MFMA order rather than the CPU's, so an f32 result can land on the other
@@ -925,7 +925,8 @@ __global__ void __launch_bounds__(256) reduce_resid_norm_kernel(const GemmArgs g
 //   * S^T = K Q^T on MFMA 32x32x16 (A = the K block staged in the wave's LDS rows, B = Q^T from
 //     the block's queries in LDS): lane (half hf, column c) holds query 32 qb + c's scores for
 //     keys 8 (r >> 2) + 4 hf + (r & 3), r < 16, so a query's row max and sum stay in the lane and
-//     its partner half-wave; s = bf16(bf16(q . k) * scale) as the reference rounds them.
+//     its partner half-wave. The scores stay in f32 and the scale goes into the exponent:
+//     e^(s - m) = 2^((q . k - m') scale log2 e) for the unscaled running max m'.
 //   * The running max m moves to m' = max(m, block max); O^T and the sum l scale by e^(m - m')
 //     (skipped when no query of the wave moved); p = e^(s - m') rounded to bf16 is the B operand
 //     of O^T += V^T P^T, reusing the score registers in place (k-index 8 hf + j of step kk2 is key
@@ -1033,19 +1034,19 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
     // blocks that every query of the block sees whole (the wave-uniform common case) skip the mask
     if (32 * kb + 31 <= p0 + 32 * qb && 32 * qb + 31 < S) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sc[r] = rbh(rbh(acc[r]) * scale);
+      for (int r = 0; r < 16; ++r) sc[r] = acc[r];
     } else {
+      const int lim = qok ? qpos : -1;   // last key this lane's query sees (none past the prompt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int kr = 32 * kb + 8 * (r >> 2) + 4 * hf + (r & 3);
-        const float v = rbh(rbh(acc[r]) * scale);
-        sc[r] = (qok && kr <= qpos) ? v : -INFINITY;
+        sc[r] = kr <= lim ? acc[r] : -INFINITY;
       }
     }
   };
-  // e^(s - m) as 2^(s log2 e - m log2 e): one fma into the hardware exp2
-  constexpr float L2E = 1.4426950408889634f;
-  auto ex = [](float s, float nm) { return __builtin_amdgcn_exp2f(fmaf(s, L2E, nm)); };
+  // e^(scale (s - m)) as 2^(s scale log2 e - m scale log2 e): one fma into the hardware exp2
+  const float SL = scale * 1.4426950408889634f;
+  auto ex = [SL](float s, float nm) { return __builtin_amdgcn_exp2f(fmaf(s, SL, nm)); };
 
   float m = -INFINITY, l = 0.0f;
   f32x16 o[4];
@@ -1073,9 +1074,9 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
     for (int r = 1; r < 16; ++r) bm = fmaxf(bm, sc[r]);
     bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
     const float mn = fmaxf(m, bm);
-    const float nm = mn == -INFINITY ? 0.0f : -mn * L2E;
+    const float nm = mn == -INFINITY ? 0.0f : -mn * SL;
     if (__builtin_amdgcn_ballot_w64(mn != m) != 0ull) {
-      const float al = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m - mn) * L2E);
+      const float al = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m - mn) * SL);
       l *= al;
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb)
@@ -1119,7 +1120,7 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
   float M = -INFINITY;
 #pragma unroll
   for (int v = 0; v < AW; ++v) M = fmaxf(M, sml[(v * 2) * 32 + c]);
-  const float sw = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m - M) * L2E);
+  const float sw = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m - M) * SL);
   if (w > 0) {
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
@@ -1132,7 +1133,7 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
 #pragma unroll
   for (int v = 0; v < AW; ++v) {
     const float mv = sml[(v * 2) * 32 + c];
-    L += mv == -INFINITY ? 0.0f : sml[(v * 2 + 1) * 32 + c] * __builtin_amdgcn_exp2f((mv - M) * L2E);
+    L += mv == -INFINITY ? 0.0f : sml[(v * 2 + 1) * 32 + c] * __builtin_amdgcn_exp2f((mv - M) * SL);
   }
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb)
