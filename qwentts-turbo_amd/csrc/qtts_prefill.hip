@@ -987,8 +987,10 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
 
   // K and V blocks (32 keys x 128 dims each) in 8 coalesced 1 KB rounds, issued a block ahead:
   // round r, lane j loads key 32 kb + 4 r + (j >> 4), dims 8 (j & 15) .. + 7. Loads are
-  // unconditional from a clamped row and zeroed when staged: a load under a branch would make the
-  // compiler wait for every outstanding load, the prefetch included.
+  // unconditional from a clamped row (row 0 past `last`) and staged as loaded: a load or a store
+  // under a branch makes the compiler wait for every outstanding load, the prefetch included. Keys
+  // past `last` are past every query of the block, so their scores are masked to -inf and their
+  // weights are exactly 0 against the finite K and V of row 0.
   auto load = [&](const bf16_t* base, int kb, u32x4 (&rr)[8]) {
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
@@ -996,17 +998,9 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
       rr[r] = ldw(base + (size_t)(key <= last ? key : 0) * HDIM + 8 * (lane & 15));
     }
   };
-  auto stage = [&](int kb, const u32x4 (&rr)[8], int pitch) {
-    if (32 * kb + 31 <= last) {   // wave-uniform: a whole block needs no zeroing
+  auto stage = [&](const u32x4 (&rr)[8], int pitch) {
 #pragma unroll
-      for (int r = 0; r < 8; ++r) *reinterpret_cast<u32x4*>(&st[(4 * r + (lane >> 4)) * pitch + 8 * (lane & 15)]) = rr[r];
-    } else {
-#pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        const int row = 4 * r + (lane >> 4);
-        *reinterpret_cast<u32x4*>(&st[row * pitch + 8 * (lane & 15)]) = 32 * kb + row <= last ? rr[r] : u32x4{0u, 0u, 0u, 0u};
-      }
-    }
+    for (int r = 0; r < 8; ++r) *reinterpret_cast<u32x4*>(&st[(4 * r + (lane >> 4)) * pitch + 8 * (lane & 15)]) = rr[r];
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   };
   auto scores = [&](int kb, float (&sc)[16]) {
@@ -1058,15 +1052,19 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
   const int gi = lane & 15, g = lane >> 4;
   const int tr_off = (4 * (g >> 1) + (gi >> 2)) * VROW + 16 * (g & 1) + 4 * (gi & 3);
   u32x4 kr[8], vr[8];
+  // K before V here as in the loop: with the same load order on both edges into the loop, the
+  // wait before each staging counts only the block it stages (the other block's prefetch stays in
+  // flight); with V scheduled first here, the compiler waited for every load at the loop top
   load(kb_, w, kr);
+  __builtin_amdgcn_sched_barrier(0);
   load(vb_, w, vr);
   for (int kb = w; kb < nkb; kb += AW) {
-    stage(kb, kr, QROW);
+    stage(kr, QROW);
     load(kb_, kb + AW, kr);
     float sc[16];
     scores(kb, sc);
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");   // K reads before the V staging
-    stage(kb, vr, VROW);
+    stage(vr, VROW);
     load(vb_, kb + AW, vr);
     // running max; a fully masked row so far keeps m = -inf and adds nothing
     float bm = sc[0];
