@@ -704,6 +704,40 @@ __global__ void __launch_bounds__(GT, NS <= 2 ? 2 : 1) gemm_dma_kernel(const Gem
     }
 }
 
+// Sums in split order of the partials at p + z stride, z < splits: 4 NQ consecutive floats
+// (NQ 16-byte loads per split). The loads go out in groups of G splits before any of them is
+// added (each clamped to the last split, so an unconditional load from a valid address): the
+// group's round trips overlap, where a rolled loop waits for each load before it issues the next.
+// The additions run in split order, so the sums are the ones of a plain loop, bit for bit.
+template <int G, int NQ>
+__device__ __forceinline__ void sum_splits(const float* p, size_t stride, int splits, float (&s)[4 * NQ]) {
+#pragma unroll
+  for (int i = 0; i < 4 * NQ; ++i) s[i] = 0.0f;
+  for (int z0 = 0; z0 < splits; z0 += G) {
+    u32x4 v[G][NQ];
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+#pragma unroll
+      for (int q = 0; q < NQ; ++q)
+        v[j][q] = *reinterpret_cast<const u32x4*>(p + (size_t)min(z0 + j, splits - 1) * stride + 4 * q);
+    // every load of the group is issued here: the compiler may not sink one into a later branch
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) asm volatile("" : "+v"(v[j][q]));
+    // a clamped duplicate adds -0.0, the exact identity of IEEE addition, so the sum is the one of
+    // the valid splits alone
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      const bool ok = z0 + j < splits;
+#pragma unroll
+      for (int q = 0; q < NQ; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s[4 * q + e] += ok ? __uint_as_float(v[j][q][e]) : -0.0f;
+    }
+  }
+}
+
 // Sum of the split-K partials in split order, then the GEMM's epilogue; four consecutive
 // outputs per thread (16-byte partial loads; a SwiGLU group of four lies in one 32-column block).
 template <int EPI, int TN>
@@ -716,27 +750,16 @@ __global__ void __launch_bounds__(256) reduce_kernel(const GemmArgs g, int split
   const float* P = g.part + (size_t)m * g.N;
   if constexpr (EPI == E_SWIGLU) {
     const int nv = swiglu_gate_col<TN>(j);
-    float4 gs = {0.0f, 0.0f, 0.0f, 0.0f}, us = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int z = 0; z < splits; ++z) {
-      const float4 a = *reinterpret_cast<const float4*>(P + z * stride + nv);
-      const float4 b = *reinterpret_cast<const float4*>(P + z * stride + nv + 32);
-      gs.x += a.x; gs.y += a.y; gs.z += a.z; gs.w += a.w;
-      us.x += b.x; us.y += b.y; us.z += b.z; us.w += b.w;
-    }
-    epilogue_swiglu(g, m, j, gs.x, us.x);
-    epilogue_swiglu(g, m, j + 1, gs.y, us.y);
-    epilogue_swiglu(g, m, j + 2, gs.z, us.z);
-    epilogue_swiglu(g, m, j + 3, gs.w, us.w);
+    float gs[4], us[4];
+    sum_splits<4, 1>(P + nv, stride, splits, gs);
+    sum_splits<4, 1>(P + nv + 32, stride, splits, us);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) epilogue_swiglu(g, m, j + e, gs[e], us[e]);
   } else {
-    float4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int z = 0; z < splits; ++z) {
-      const float4 a = *reinterpret_cast<const float4*>(P + z * stride + j);
-      v.x += a.x; v.y += a.y; v.z += a.z; v.w += a.w;
-    }
-    epilogue<EPI>(g, m, j, v.x);
-    epilogue<EPI>(g, m, j + 1, v.y);
-    epilogue<EPI>(g, m, j + 2, v.z);
-    epilogue<EPI>(g, m, j + 3, v.w);
+    float v[4];
+    sum_splits<4, 1>(P + j, stride, splits, v);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) epilogue<EPI>(g, m, j + e, v[e]);
   }
 }
 
@@ -857,15 +880,7 @@ __global__ void __launch_bounds__(256) reduce_rope_kernel(const GemmArgs g, int 
   // thread t: elements 16 t .. 16 t + 15, in 16-byte loads
   const int n0 = 16 * threadIdx.x;
   float v[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) v[i] = 0.0f;
-  for (int z = 0; z < splits; ++z) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float4 p = *reinterpret_cast<const float4*>(P + z * stride + n0 + 4 * q);
-      v[4 * q] += p.x; v[4 * q + 1] += p.y; v[4 * q + 2] += p.z; v[4 * q + 3] += p.w;
-    }
-  }
+  sum_splits<2, 4>(P + n0, stride, splits, v);
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     u32x4 o;
@@ -890,11 +905,8 @@ __global__ void __launch_bounds__(256) reduce_resid_norm_kernel(const GemmArgs g
   const u32x2 rv = *reinterpret_cast<const u32x2*>(g.res + (size_t)m * g.ldr + 4 * t);
   float hv[4];
   {
-    float sv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int z = 0; z < splits; ++z) {
-      const float4 p = *reinterpret_cast<const float4*>(P + z * stride);
-      sv[0] += p.x; sv[1] += p.y; sv[2] += p.z; sv[3] += p.w;
-    }
+    float sv[4];
+    sum_splits<8, 1>(P, stride, splits, sv);
     hv[0] = rbh(bflo(rv[0]) + rbh(sv[0]));
     hv[1] = rbh(bfhi(rv[0]) + rbh(sv[1]));
     hv[2] = rbh(bflo(rv[1]) + rbh(sv[2]));
