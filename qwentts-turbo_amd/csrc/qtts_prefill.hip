@@ -465,7 +465,7 @@ typedef __attribute__((address_space(3))) void lvoid_t;
 // - The wait before each barrier counts this wave's DMA instructions still in flight: the
 //   compiler does not track LDS writes made by DMA.
 // - Unsplit QKV with rope arguments: a tile is one head of 128 tokens, and the epilogue finishes
-//   it as rope_kv_row does: bf16 tile through LDS, then two threads per token (32 channel pairs
+//   it as rope_kv_apply does: bf16 tile through LDS, then two threads per token (32 channel pairs
 //   (d, d + 64) each) for the q/k RMSNorm and the interleaved mRoPE. q goes back to the QKV rows;
 //   k and v go to the cache.
 template <int WM, int EPI, int NS>
@@ -807,27 +807,41 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const bf16_t* x, int ldx, 
   }
 }
 
-// Per token: q/k head RMSNorm (field 4 / 5 gains), interleaved mRoPE from the bf16 tables, q
-// written back in place, the rotated k and the v of every KV head written to the cache at
+// Per token: q/k head RMSNorm (field 4 / 5 gains), interleaved mRoPE from the bf16 tables, the
+// rotated q written to qdst, the rotated k and the v of every KV head written to the cache at
 // position p0 + s. Lane j of a wave handles channels j and j + 64 (the rotate_half pair). Run by
-// a whole 256-thread workgroup on token s's q | k | v row `src`.
-__device__ __forceinline__ void rope_kv_row(bf16_t* src, int s, const TTSLayerWeights* layers, int layer,
-                                            const bf16_t* cos_t, const bf16_t* sin_t, const int* pos3, int p0, int S,
-                                            bf16_t* kc, bf16_t* vc, int max_seq) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int pos = p0 + s;
+// a whole 256-thread workgroup on token s's q | k | v row `src` (global memory or LDS). The table
+// and gain values come first (rope_inputs), so a caller can issue those loads before it builds
+// the row.
+struct RopeIn { float c0, c1, s0, s1, gq0, gq1, gk0, gk1; };
+
+__device__ __forceinline__ RopeIn rope_inputs(int s, const TTSLayerWeights* layers, int layer, const bf16_t* cos_t,
+                                              const bf16_t* sin_t, const int* pos3, int p0, int S, int max_seq) {
+  const int lane = threadIdx.x & 63;
   const int sec = (lane < 60 && lane % 3 == 1) ? 1 : ((lane < 60 && lane % 3 == 2) ? 2 : 0);
   // table row of this channel's section (clamped into the table: a caller's out-of-range
   // position must not read outside it)
-  const int row = pos3 ? min(max(pos3[sec * S + s], 0), max_seq - 1) : pos;
-  const float c0 = ldbf(cos_t + (size_t)row * HDIM + lane), c1 = ldbf(cos_t + (size_t)row * HDIM + lane + 64);
-  const float s0 = ldbf(sin_t + (size_t)row * HDIM + lane), s1 = ldbf(sin_t + (size_t)row * HDIM + lane + 64);
-  // wave w takes heads w + 4 k (k < 6): q heads for k < 4, k heads 16 + w, 20 + w for k = 4, 5;
-  // every load is issued before the first reduction, the six reductions interleave
-  constexpr int HPW = (NQH + NKVH) / 4;
+  const int row = pos3 ? min(max(pos3[sec * S + s], 0), max_seq - 1) : p0 + s;
   const TTSLayerWeights* lw = layers + layer;
   const bf16_t* qn = tbl(lw, 4);
   const bf16_t* kn = tbl(lw, 5);
+  RopeIn r;
+  r.c0 = ldbf(cos_t + (size_t)row * HDIM + lane);
+  r.c1 = ldbf(cos_t + (size_t)row * HDIM + lane + 64);
+  r.s0 = ldbf(sin_t + (size_t)row * HDIM + lane);
+  r.s1 = ldbf(sin_t + (size_t)row * HDIM + lane + 64);
+  r.gq0 = ldbf(qn + lane); r.gq1 = ldbf(qn + lane + 64);
+  r.gk0 = ldbf(kn + lane); r.gk1 = ldbf(kn + lane + 64);
+  return r;
+}
+
+__device__ __forceinline__ void rope_kv_apply(const RopeIn& r, const bf16_t* src, bf16_t* qdst, int s, int layer,
+                                              int p0, bf16_t* kc, bf16_t* vc, int max_seq) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int pos = p0 + s;
+  // wave w takes heads w + 4 k (k < 6): q heads for k < 4, k heads 16 + w, 20 + w for k = 4, 5;
+  // every load is issued before the first reduction, the six reductions interleave
+  constexpr int HPW = (NQH + NKVH) / 4;
   float x0[HPW], x1[HPW], ss[HPW];
 #pragma unroll
   for (int k = 0; k < HPW; ++k) {
@@ -835,8 +849,6 @@ __device__ __forceinline__ void rope_kv_row(bf16_t* src, int s, const TTSLayerWe
     x0[k] = bf2f(hp[lane]);
     x1[k] = bf2f(hp[lane + 64]);
   }
-  const float gq0 = ldbf(qn + lane), gq1 = ldbf(qn + lane + 64);
-  const float gk0 = ldbf(kn + lane), gk1 = ldbf(kn + lane + 64);
 #pragma unroll
   for (int k = 0; k < HPW; ++k) ss[k] = x0[k] * x0[k] + x1[k] * x1[k];
 #pragma unroll
@@ -846,11 +858,11 @@ __device__ __forceinline__ void rope_kv_row(bf16_t* src, int s, const TTSLayerWe
 #pragma unroll
   for (int k = 0; k < HPW; ++k) {
     const float rs = 1.0f / sqrtf(ss[k] / (float)HDIM + EPS);
-    const float y0 = rbh((k < 4 ? gq0 : gk0) * rbh(x0[k] * rs));
-    const float y1 = rbh((k < 4 ? gq1 : gk1) * rbh(x1[k] * rs));
-    const bf16_t o0 = f2bh(rbh(y0 * c0) + rbh(-y1 * s0));
-    const bf16_t o1 = f2bh(rbh(y1 * c1) + rbh(y0 * s1));
-    bf16_t* dst = k < 4 ? src + (w + 4 * k) * HDIM
+    const float y0 = rbh((k < 4 ? r.gq0 : r.gk0) * rbh(x0[k] * rs));
+    const float y1 = rbh((k < 4 ? r.gq1 : r.gk1) * rbh(x1[k] * rs));
+    const bf16_t o0 = f2bh(rbh(y0 * r.c0) + rbh(-y1 * r.s0));
+    const bf16_t o1 = f2bh(rbh(y1 * r.c1) + rbh(y0 * r.s1));
+    bf16_t* dst = k < 4 ? qdst + (w + 4 * k) * HDIM
                         : kc + (((size_t)layer * NKVH + (w + 4 * (k - 4))) * max_seq + pos) * HDIM;
     dst[lane] = o0;
     dst[lane + 64] = o1;
@@ -865,18 +877,22 @@ __device__ __forceinline__ void rope_kv_row(bf16_t* src, int s, const TTSLayerWe
 __global__ void __launch_bounds__(256) rope_kv_kernel(bf16_t* qkv, const TTSLayerWeights* layers, int layer,
                                                       const bf16_t* cos_t, const bf16_t* sin_t, const int* pos3,
                                                       int p0, int S, bf16_t* kc, bf16_t* vc, int max_seq) {
-  rope_kv_row(qkv + (size_t)blockIdx.x * QKVW, blockIdx.x, layers, layer, cos_t, sin_t, pos3, p0, S, kc, vc, max_seq);
+  const RopeIn r = rope_inputs(blockIdx.x, layers, layer, cos_t, sin_t, pos3, p0, S, max_seq);
+  bf16_t* row = qkv + (size_t)blockIdx.x * QKVW;
+  rope_kv_apply(r, row, row, blockIdx.x, layer, p0, kc, vc, max_seq);   // q rotated in place
 }
 
-// Split-K QKV: token m's 4096 sums in split order -> bf16 q | k | v row, then rope_kv_row on it
-// (one launch instead of a reduction and a rope pass).
+// Split-K QKV: token m's 4096 sums in split order -> bf16 q | k | v row in LDS, then the q/k-norm,
+// RoPE and cache write on it, the rotated q to the token's QKV row (one launch instead of a
+// reduction and a rope pass). The table and gain loads go out before the partial sums.
 __global__ void __launch_bounds__(256) reduce_rope_kernel(const GemmArgs g, int splits, const bf16_t* cos_t,
                                                           const bf16_t* sin_t, const int* pos3, int p0, bf16_t* kc,
                                                           bf16_t* vc, int max_seq) {
+  __shared__ __attribute__((aligned(16))) bf16_t srow[QKVW];
   const int m = blockIdx.x;
   const size_t stride = (size_t)g.M * g.N;
   const float* P = g.part + (size_t)m * g.N;
-  bf16_t* row = g.out + (size_t)m * g.ldo;
+  const RopeIn r = rope_inputs(m, g.layers, g.layer, cos_t, sin_t, pos3, p0, g.M, max_seq);
   // thread t: elements 16 t .. 16 t + 15, in 16-byte loads
   const int n0 = 16 * threadIdx.x;
   float v[16];
@@ -886,10 +902,10 @@ __global__ void __launch_bounds__(256) reduce_rope_kernel(const GemmArgs g, int 
     u32x4 o;
 #pragma unroll
     for (int e = 0; e < 4; ++e) o[e] = pack_bh(v[8 * q + 2 * e], v[8 * q + 2 * e + 1]);
-    *reinterpret_cast<u32x4*>(row + n0 + 8 * q) = o;
+    *reinterpret_cast<u32x4*>(srow + n0 + 8 * q) = o;
   }
   __syncthreads();   // the row is read back by other threads of the workgroup
-  rope_kv_row(row, m, g.layers, g.layer, cos_t, sin_t, pos3, p0, g.M, kc, vc, max_seq);
+  rope_kv_apply(r, srow, g.out + (size_t)m * g.ldo, m, g.layer, p0, kc, vc, max_seq);
 }
 
 // Split-K O or down projection of token m: sums in split order, residual add in place
