@@ -1195,8 +1195,17 @@ __global__ void __launch_bounds__(64) select_kernel(const bf16_t* logits, int n,
   __shared__ float stage[MAXV];
   __shared__ SelScratch sc;
   const int lane = threadIdx.x;
-  for (int i = lane; i < n; i += 64) {
-    float v = bf2f(logits[i]);
+  // every logit load is issued before the first is used (a rolled loop waited for each in turn);
+  // loads past n are clamped to n - 1 and dropped
+  constexpr int NJ = (MAXV + 63) / 64;
+  float lv[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) lv[j] = bf2f(logits[min(lane + 64 * j, n - 1)]);
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int i = lane + 64 * j;
+    if (i >= n) break;
+    float v = lv[j];
     if (out_logits) out_logits[i] = v;
     if (mask_tail && i >= n - 1024 && i != eos_id) v = -INFINITY;
     if (suppress_eos && i == eos_id) v = -INFINITY;
