@@ -123,7 +123,11 @@ __device__ __forceinline__ const bf16_t* tbl(const TTSLayerWeights* lw, int fiel
   return reinterpret_cast<const bf16_t*>(ld_const(reinterpret_cast<const void* const*>(lw) + field));
 }
 
-__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+// x sigmoid(x) in f32 from the hardware exp2 and reciprocal (about 2 ulp of f32 from x / (1 + e^-x),
+// far below the bf16 rounding that follows; large |x| gives x or -0 as the exact form does)
+__device__ __forceinline__ float silu_f(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
+}
 
 template <int EPI>
 __device__ __forceinline__ void epilogue(const GemmArgs& g, int m, int n, float v) {
