@@ -1004,9 +1004,9 @@ __global__ void __launch_bounds__(64 * AW, 2) attn_kernel(const bf16_t* qkv, con
   const int nkb = last / 32 + 1;
   bf16_t* st = sq + ATT_Q + w * WST;   // the wave's K block, then its V block
 
-  // the block's 32 query rows go to LDS once (two 16-byte chunks per thread)
+  // the block's 32 query rows (512 16-byte chunks) go to LDS once
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < 512 / (64 * AW); ++j) {
     const int ch = threadIdx.x + 64 * AW * j, qrow = ch >> 4, qcol = 8 * (ch & 15);
     const int qi = 32 * qb + qrow;
     const u32x4 v = ldw(qkv + (size_t)(qi < S ? qi : 0) * QKVW + hq * HDIM + qcol);   // clamped row
