@@ -10,10 +10,11 @@ Prints one JSON line (see the repository's bench contract) with:
   value         frames/s over the timed K frames (inputs resident in HBM, no host sync inside)
   roofline      algorithmic bytes / kernel time for the dominant kernel, timed with HIP events
                 on the launch stream, against MI355X's 8 TB/s
-  cpu_baseline  the same frame through the CPU oracle's HF-bf16 path (eager PyTorch, bf16
-                weights) on this host, timed on a bounded sample of frames; also split into
-                backbone steps/s (config 0's unit) and code-predictor steps/s (config 1's), plus
-                the prefill's tokens/s (the oracle's bf16 policy, the reference's prefill arithmetic)
+  backbone_by_context  backbone steps/s and roofline at config 0's L = 129 and config 3's L = 2048
+  cpu_baseline  the CPU oracle's HF-bf16 path (eager PyTorch, bf16 weights) on this host:
+                3 warm-ups, then the median of >= 10 runs; value = config 2's greedy frame loop
+                (frames/s), plus backbone steps/s at L = 129 (config 0), code-predictor steps/s
+                (config 1), the 512-context frame and the prefill's tokens/s
 """
 from __future__ import annotations
 
@@ -54,57 +55,89 @@ def frame_bytes(L: int = 512) -> int:
     return backbone_bytes(L) + cp_frame_bytes()
 
 
-def cpu_baseline(sample_seconds: float = 15.0) -> dict:
-    """The frame through the oracle's HF-bf16 path on the host CPU, over a bounded sample."""
+def _median(xs):
+    xs = sorted(xs)
+    n = len(xs)
+    return xs[n // 2] if n % 2 else 0.5 * (xs[n // 2 - 1] + xs[n // 2])
+
+
+def cpu_baseline(runs: int = 10, warmup: int = 3, c2_frames: int = 64) -> dict:
+    """The decode path through the oracle's HF-bf16 policy (eager PyTorch, bf16 weights,
+    transformers' Qwen3 op order) on the host CPU, with every host thread. Each figure takes
+    `warmup` untimed runs, then the median of at least `runs` timed runs (time.perf_counter):
+      backbone_steps_per_s  config 0: one backbone step at L = 129 (128 cached tokens) + codec head
+      cp_steps_per_s        config 1: the 15-group code-predictor loop of one frame (2-token
+                            prefill, 14 steps, 15 lm-heads, greedy); 15 / the median frame time
+      value (frames/s)      config 2's greedy frame loop: frames from a 128-token prompt (the
+                            prompt's K/V seeded directly; the prefill is timed separately), each
+                            frame = code-predictor loop + backbone step + codec head + greedy g0 +
+                            the embedding combine fed back; c2_frames frames, 1 / the median
+      frame512_frames_per_s the GPU figure's frame (backbone at L = 512)
+      prefill_tokens_per_s  the prompt stepped token by token (a bounded sample)."""
     import torch
     import __graft_entry__ as ge
-    from oracle.qtts_oracle import DecoderOracle, TalkerWeights, head_logits, sample_token, rb
+    from oracle.qtts_oracle import DecoderOracle, TalkerWeights, rb
     pkg = ge.import_package()
     threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
     sd = pkg.synthetic_state_dict(seed=1234)
     tw = TalkerWeights.from_state_dict(sd, 28, 5)
-    bb = DecoderOracle(tw.bb_layers, tw.bb_norm, 520, "backbone", "hf_bf16")
+    bb = DecoderOracle(tw.bb_layers, tw.bb_norm, 600, "backbone", "hf_bf16")
     cp = DecoderOracle(tw.cp_layers, tw.cp_norm, 17, "cp", "hf_bf16")
     heads = [h.to(torch.bfloat16) for h in tw.cp_heads]
     embs = [e.to(torch.bfloat16) for e in tw.cp_embeddings]
+    bb_emb = tw.codec_embedding.to(torch.bfloat16)
     codec_head = tw.codec_head.to(torch.bfloat16)
     g = torch.Generator().manual_seed(9)
     bb.k[:, :, :511] = torch.randn(28, 8, 511, 128, generator=g).to(torch.bfloat16)
     bb.v[:, :, :511] = torch.randn(28, 8, 511, 128, generator=g).to(torch.bfloat16)
-    hidden = torch.randn(1024, generator=g)
-    x = torch.randn(1024, generator=g).to(torch.bfloat16)
+    text = torch.randn(1024, generator=g).to(torch.bfloat16)
 
-    t_parts = [0.0, 0.0]   # code predictor, backbone
+    def timed(fn, n):
+        ts = []
+        for i in range(warmup + n):
+            t = time.perf_counter()
+            fn(i)
+            if i >= warmup:
+                ts.append(time.perf_counter() - t)
+        return _median(ts)
 
-    def frame(hidden, x):
-        t = time.perf_counter()
+    def cp_loop(hidden, g0):
         cp.reset()
-        cp.step(rb(hidden).to(torch.bfloat16), pos=0)
-        h, _ = cp.step(tw.codec_embedding[5].to(torch.bfloat16), pos=1)
+        cp.step(rb(hidden.float()).to(torch.bfloat16), pos=0)
+        h, _ = cp.step(bb_emb[g0], pos=1)
         toks = []
         for gi in range(15):
             if gi:
                 h, _ = cp.step(embs[gi - 1][toks[-1]], pos=gi + 1)
             toks.append(int(torch.argmax(torch.mv(heads[gi], h.to(torch.bfloat16)).float())))
-        t1 = time.perf_counter()
-        hb, _ = bb.step(x, pos=511)
-        lg = torch.mv(codec_head, hb.to(torch.bfloat16)).float()
-        t_parts[0] += t1 - t
-        t_parts[1] += time.perf_counter() - t1
-        return hb, int(torch.argmax(lg))
+        return toks
 
-    frame(hidden, x)  # warm-up
-    t_parts[0] = t_parts[1] = 0.0
-    n, t0 = 0, time.perf_counter()
-    while True:
-        frame(hidden, x)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= sample_seconds or n >= 500:
-            break
-    # the prefill (scope row f3): the oracle's bf16 policy over a prompt from position 0, on a
-    # bounded sample of tokens (about 3 s)
+    def bb_step(x, pos):
+        hb, _ = bb.step(x, pos=pos)
+        return hb, int(torch.argmax(torch.mv(codec_head, hb.to(torch.bfloat16)).float()))
+
+    x0 = torch.randn(1024, generator=g).to(torch.bfloat16)
+    h0 = torch.randn(1024, generator=g)
+    t_bb = timed(lambda i: bb_step(x0, 128), runs)            # config 0: L = 129
+    t_cp = timed(lambda i: cp_loop(h0, 5 + i), runs)          # config 1
+    t_512 = timed(lambda i: (cp_loop(h0, 5), bb_step(x0, 511)), runs)
+
+    # config 2, greedy: the frame loop from position 128 on, the combine fed back
+    state = {"h": h0, "g0": 5, "pos": 128}
+
+    def c2_frame(i):
+        toks = [state["g0"]] + cp_loop(state["h"], state["g0"])
+        acc = bb_emb[toks[0]].clone()
+        for gi in range(15):
+            acc = acc + embs[gi][toks[gi + 1]]
+        x = acc + text
+        state["h"], state["g0"] = bb_step(x, state["pos"])
+        state["pos"] += 1
+
+    t_c2 = timed(c2_frame, c2_frames)
+
+    # the prefill: the oracle's bf16 policy over a prompt from position 0, a bounded sample
     pf = DecoderOracle(tw.bb_layers, tw.bb_norm, 520, "backbone", "hf_bf16")
     xs = torch.randn(64, 1024, generator=g).to(torch.bfloat16)
     pf.step(xs[0], pos=0)
@@ -115,23 +148,18 @@ def cpu_baseline(sample_seconds: float = 15.0) -> dict:
         if time.perf_counter() - tp0 >= 3.0:
             break
     pf_rate = npf / (time.perf_counter() - tp0)
-    return {"value": n / el, "unit": "frames/s", "cores": threads, "kind": "port", "cpu_model": _cpu_model(),
-            "backbone_steps_per_s": round(n / t_parts[1], 2), "cp_steps_per_s": round(15 * n / t_parts[0], 2),
-            "prefill_tokens_per_s": round(pf_rate, 2),
-            "sample": f"{n} frames (1 backbone step at 512 context + 16 code-predictor steps, HF-bf16 eager "
-                      f"PyTorch oracle) in {el:.1f} s"}
+    return {"value": round(1.0 / t_c2, 3), "unit": "frames/s", "cores": threads, "kind": "port",
+            "cpu_model": _cpu_model(),
+            "backbone_steps_per_s": round(1.0 / t_bb, 2), "cp_steps_per_s": round(15.0 / t_cp, 2),
+            "frame512_frames_per_s": round(1.0 / t_512, 3), "prefill_tokens_per_s": round(pf_rate, 2),
+            "protocol": f"{warmup} warm-ups, then the median of {runs} runs ({c2_frames} frames for config 2)",
+            "sample": f"HF-bf16 eager PyTorch oracle on {threads} host threads: backbone step at L=129 + codec head "
+                      f"(config 0); 15-group code-predictor loop (config 1); config 2's greedy frame loop from a "
+                      f"128-token prompt, {c2_frames} frames; the frame at 512 context"}
 
 
 def _cpu_model() -> str:
-    """The host CPU's model name (lscpu "Model name", else /proc/cpuinfo "model name")."""
-    import subprocess
-    try:
-        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
-        for line in out.splitlines():
-            if line.strip().startswith("Model name:"):
-                return line.split(":", 1)[1].strip()
-    except (OSError, subprocess.SubprocessError):
-        pass
+    """The host CPU's model name (/proc/cpuinfo "model name"; read from the file, no subprocess)."""
     try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name"):
@@ -180,6 +208,40 @@ def prefill_figures(bbg, reps: int = 5) -> dict:
                         "tflops": round(fl / t / 1e12, 1), "mfma_frac": round(fl / t / 1e12 / 2500.0, 4)}
     bbg.decoder.check_error()
     return out
+
+
+def backbone_figure(bbg, L: int, steps: int = 30, warmup: int = 5) -> dict:
+    """The backbone step (28 layers + codec head + greedy selection) at KV length L: L - 1 cached
+    random bf16 entries, each launch writing slot L - 1. Timed with HIP events on the launch
+    stream over `steps` launches after `warmup`; roofline = backbone_bytes(L) / time / 8 TB/s."""
+    import torch
+    bb = bbg.decoder
+    g = torch.Generator(device="cuda").manual_seed(100 + L)
+    k = torch.randn(28, 8, L - 1, 128, generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn(28, 8, L - 1, 128, generator=g, device="cuda").to(torch.bfloat16)
+    bb.set_kv_cache(k, v)
+    del k, v
+    i32 = dict(dtype=torch.int32, device="cuda")
+    tok, hist = torch.zeros(1, **i32), torch.zeros(1, **i32)
+    x = torch.randn(1024, generator=g, device="cuda").to(torch.bfloat16)
+
+    def step(i):
+        bb.set_position(L - 1)
+        bb.decode_step_select(x, tok, hist, 0, 1.0, -1, False, False, 1.0, 0, 1.0, 0, i)
+
+    for i in range(warmup):
+        step(i)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        step(warmup + i)
+    e1.record()
+    torch.cuda.synchronize()
+    bb.check_error()
+    t = e0.elapsed_time(e1) / steps * 1e-3
+    gbs = backbone_bytes(L) / t / 1e9
+    return {"L": L, "us": round(t * 1e6, 2), "steps_per_s": round(1.0 / t, 1), "algorithmic_bytes": backbone_bytes(L),
+            "achieved_gbs": round(gbs, 1), "roofline_frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 def batched_frame_bytes(lengths) -> int:
@@ -248,7 +310,9 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-runs", type=int, default=10, help="timed runs per CPU-baseline figure (median)")
+    ap.add_argument("--backbone-context", type=int, default=0, metavar="L",
+                    help="only time the backbone step at KV length L (one JSON line; for per-context profiles)")
     ap.add_argument("--no-batched", action="store_true", help="skip the batch-8 ragged-context figure")
     ap.add_argument("--no-prefill", action="store_true", help="skip the MFMA prefill figures")
     ap.add_argument("--prefill-only", action="store_true", help="only the MFMA prefill figures (one JSON line)")
@@ -279,6 +343,10 @@ def main():
 
     sd = pkg.synthetic_state_dict(seed=1234, device="cuda")
     bbg = pkg.TTSMegakernelGenerator(model=sd, max_seq_len=4096)
+    if args.backbone_context:
+        print(json.dumps({"backbone": backbone_figure(bbg, args.backbone_context, steps=args.steps,
+                                                      warmup=args.warmup)}), flush=True)
+        return
     if args.prefill_only:
         print(json.dumps({"prefill": prefill_figures(bbg)}), flush=True)
         return
@@ -363,6 +431,8 @@ def main():
                      "unit": "GB/s", "frac": round(dominant[1] / HBM_PEAK_GBS, 4),
                      "algorithmic_bytes": dominant[2], "traffic": dominant[3]},
     }
+    # backbone steps/s and roofline at config 0's context (L = 129) and config 3's (L = 2048)
+    out["backbone_by_context"] = {f"L{L}": backbone_figure(bbg, L) for L in (129, 2048)}
     # the prefill is timed before the batched phase, whose 8 stream decoders stay allocated until
     # it returns (with them alive, the 229 host launches of a 128-token prefill fell behind the GPU)
     if not args.no_prefill:
@@ -376,7 +446,7 @@ def main():
     pkg._ext.load().shutdown()
     torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        out["cpu_baseline"] = cpu_baseline(max(10, args.cpu_runs))
     print(json.dumps(out), flush=True)
 
 

@@ -149,6 +149,23 @@ hipError_t qtts_debug_set_sequence(void* workspace, unsigned int sequence);
  * *error_code = 0 when every wait completed; bit 0 = a wait timed out. */
 hipError_t qtts_workspace_check(void* workspace, unsigned int* error_code, hipStream_t stream);
 
+/* Launch residency. The launches are plain (not cooperative): all 256 workgroups are resident
+ * at once only when no other kernel holds CUs. The waits of a launch's first layer pass can
+ * complete only once every workgroup has started, so they run under a short cap (about 30 ms of
+ * polling, against about 4 s for later waits): a launch that does not find the whole GPU sets
+ * the error word within milliseconds, every later wait gives up at its next check, and every
+ * workgroup runs to its end; qtts_workspace_check (the extension's check_error) reports it.
+ * No counterpart in the reference, whose cooperative launch would fail at launch instead. */
+
+/* Test hook: pre-sets the error word of a workspace that has been launched on at least once
+ * (its first launch zero-fills it) to `code` (nonzero), so that every wait of the next launch
+ * gives up at its first check, as after a timed-out wait. Synchronises the stream. */
+hipError_t qtts_debug_set_error(void* workspace, unsigned int code, hipStream_t stream);
+
+/* Test hook: the poll cap of the first layer pass of every later persistent launch (0 restores
+ * the default of 2^15 poll rounds). */
+hipError_t qtts_debug_entry_spin_cap(unsigned int cap);
+
 /* Diagnostics: when device_buffer is non-NULL (>= 256 * 1024 * 2 * 8 bytes), every later launch
  * records, per workgroup and step, the s_memrealtime stamp (100 MHz) at which its poller wave
  * (slot 1) and math waves (slot 0) finished the step: buffer[(wg * 1024 + step) * 2 + slot].

@@ -64,9 +64,14 @@ class BatchedTTSDecoder:
         """One backbone step per stream at its own position, codec head, suppress mask (ids
         [V-1024, V) except EOS), optional repetition penalty over ``history[s][:n_history[s]]``
         and selection of each stream's group-0 token into ``tokens_out[s]`` (device int32), with
-        sampling key ``seed + s``. Up to 8 streams share one launch (``decode_steps_streams``). A stream whose ``skip[s]`` (device int32 [n]) is nonzero computes
-        nothing and leaves its outputs as they were. Returns the final-norm hiddens (f32
-        [n_streams, 1024], device)."""
+        sampling key ``seed + s``. Up to 8 streams share one launch (``decode_steps_streams``).
+
+        ``skip`` (device int32 [n]) marks finished streams, and skipping is terminal: a stream
+        whose ``skip[s]`` is nonzero computes nothing, writes no KV entry and leaves its token,
+        logits and residual as they were, but its position still advances (the host does not
+        read the flag, so no launch waits on the device), so its cache holds an unwritten slot
+        and the stream must not be resumed. Its row of the returned hiddens is zero. Returns the
+        final-norm hiddens (f32 [n_streams, 1024], device)."""
         if skip is not None and (skip.dtype != torch.int32 or skip.numel() != self.n_streams or not skip.is_contiguous()):
             raise ValueError("skip must be a contiguous device int32 tensor with one entry per stream")
         if embeds.shape != (self.n_streams, 1024):
@@ -76,7 +81,8 @@ class BatchedTTSDecoder:
         emb = embeds.to(self.device, torch.bfloat16).contiguous()
         hist = history.to(self.device, torch.int32).contiguous() if history is not None else None
         nh = [int(x) for x in n_history] if n_history else [0] * self.n_streams
-        hidden = torch.empty(self.n_streams, 1024, dtype=torch.float32, device=self.device)
+        # zeros: a skipped stream's row is not written by the kernel
+        hidden = torch.zeros(self.n_streams, 1024, dtype=torch.float32, device=self.device)
         lead = self.streams[0].decoder
         for b in range(0, self.n_streams, self.MAX_PER_LAUNCH):
             e = min(self.n_streams, b + self.MAX_PER_LAUNCH)

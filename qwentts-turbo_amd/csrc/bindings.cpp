@@ -365,6 +365,11 @@ class MegakernelTTSDecoder {
   torch::Tensor residual_buffer() const { return hidden_buffer_; }
   torch::Tensor logits_buffer() const { return logits_; }
   void check_error() const { check_device_error(ws_); }
+  // test hook: pre-sets the workspace's error word (after at least one launch), so that every
+  // wait of the next launch gives up at its first check
+  void debug_set_error(int64_t code) {
+    hip_check(qtts_debug_set_error(ws_.data_ptr(), (unsigned int)code, cur_stream()), "qtts_debug_set_error");
+  }
 
   void set_kv_cache(torch::Tensor k_cache, torch::Tensor v_cache) {
     TORCH_CHECK(k_cache.dim() == 4 && k_cache.sizes() == v_cache.sizes(), "k/v must be [layers, 8, seq, 128]");
@@ -601,6 +606,11 @@ class MegakernelCodePredictorDecoder {
   torch::Tensor get_k_cache() const { return k_cache_; }
   torch::Tensor get_v_cache() const { return v_cache_; }
   void check_error() const { check_device_error(ws_); }
+  // test hook: pre-sets the workspace's error word (after at least one launch), so that every
+  // wait of the next launch gives up at its first check
+  void debug_set_error(int64_t code) {
+    hip_check(qtts_debug_set_error(ws_.data_ptr(), (unsigned int)code, cur_stream()), "qtts_debug_set_error");
+  }
 
   void set_kv_cache(torch::Tensor k_cache, torch::Tensor v_cache) {
     TORCH_CHECK(k_cache.dim() == 4 && k_cache.sizes() == v_cache.sizes(), "k/v must be [layers, 8, seq, 128]");
@@ -673,6 +683,7 @@ PYBIND11_MODULE(_qwentts_amd_C, m) {
            py::arg("temperature"), py::arg("top_k"), py::arg("top_p"), py::arg("seed"), py::arg("frame_step"),
            py::arg("skip") = py::none(), py::arg("shared") = false)
       .def("check_error_streams", &MegakernelTTSDecoder::check_error_streams)
+      .def("debug_set_error", &MegakernelTTSDecoder::debug_set_error)
       .def("check_error", &MegakernelTTSDecoder::check_error);
   py::class_<MegakernelCodePredictorDecoder>(m, "MegakernelCodePredictorDecoder")
       .def(py::init<std::vector<torch::Tensor>, torch::Tensor, torch::Tensor, torch::Tensor, int64_t, int64_t>())
@@ -694,5 +705,6 @@ PYBIND11_MODULE(_qwentts_amd_C, m) {
       .def("get_k_cache", &MegakernelCodePredictorDecoder::get_k_cache)
       .def("get_v_cache", &MegakernelCodePredictorDecoder::get_v_cache)
       .def("set_kv_cache", &MegakernelCodePredictorDecoder::set_kv_cache)
+      .def("debug_set_error", &MegakernelCodePredictorDecoder::debug_set_error)
       .def("check_error", &MegakernelCodePredictorDecoder::check_error);
 }

@@ -24,6 +24,7 @@
 //     cross-XCD sums + residuals, token selection) and leaves ready operands in LDS. Keeping
 //     the polls on their own wave keeps them out of the math waves' in-order load queue.
 #include <hip/hip_runtime.h>
+#include <atomic>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -107,6 +108,7 @@ struct KArgs {
   float scale;
   uint32_t tag_base;
   uint32_t spin_cap;
+  uint32_t entry_spin_cap;   // cap of the first layer pass's waits (the arrival check)
   int n_pos;       // positions processed by this launch
   const bf16_t* embed_w;   // token-id gather table
   // backbone codec head + selection
@@ -424,7 +426,9 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   P.rs = __builtin_amdgcn_make_buffer_rsrc(ws, (short)0, (int)sizeof(Workspace), 0x00020000);
   P.base = ws;
   P.ec.err = &ws->err;
-  P.ec.spin_cap = a.spin_cap;
+  // the first layer pass waits under the short entry cap (an arrival check: its exchanges need
+  // every workgroup of the launch); the poller restores the long cap from the second pass on
+  P.ec.spin_cap = a.entry_spin_cap;
   // Slot publishes go through the workspace buffer descriptor (SGPRs) with a 32-bit offset:
   // XCD-local slots as plain stores (they land in the XCD's L2), cross-XCD slots with sc1
   // (written through to memory). One 8-byte store carries value and tag together.
@@ -1331,8 +1335,13 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   // step loop (that would keep all tiles resident at once and spill).
 
   if (poller) {
+    int npass = 0;   // layer passes begun
     walk([&](int st, int pi, int layer) {
       lane = opaque(lane);
+      if (st == S_QKV || st == S_QKV2) {
+        if (npass > 0) P.ec.spin_cap = a.spin_cap;
+        ++npass;
+      }
       const PosInfo q = pinfo(pi);
       const int lp = pi * NL + layer;
       const int nl = layer + 1 < NL ? layer + 1 : 0;   // next layer pass (wraps to the next position)
@@ -1748,6 +1757,8 @@ std::unordered_map<const void*, uint32_t> g_seq;
 // launches on one stream are ordered, so they never overlap on a workspace.
 std::map<std::pair<int, hipStream_t>, void*> g_lib_ws;
 uint64_t* g_trace = nullptr;   // optional step timeline buffer
+// cap of the first layer pass's waits in every persistent launch (qtts_debug_entry_spin_cap)
+std::atomic<uint32_t> g_entry_cap{qtts_host::kEntrySpinCap};
 
 // XCC id of every workgroup of the probe launch (a static device array: the set-up allocates nothing)
 __device__ int g_xcc_probe[qtts::NWG];
@@ -1870,6 +1881,7 @@ hipError_t launch(bool bb, KArgs& a, hipStream_t stream, bool xl = false, int n_
   if (a.num_layers < 1 || a.n_pos < 1 || a.num_layers * a.n_pos > qtts::MAX_LAYER_PASSES) return hipErrorInvalidValue;
   if (a.io[0].pos0 < 0 || a.io[0].pos0 + a.n_pos > a.max_seq) return hipErrorInvalidValue;
   a.spin_cap = kSpinCap;
+  a.entry_spin_cap = g_entry_cap.load(std::memory_order_relaxed);
   a.trace = g_trace;
   const void* fn = bb ? (xl ? (const void*)qtts::qtts_decode_kernel<true, true> : (const void*)qtts::qtts_decode_kernel<true, false>)
                       : (xl ? (const void*)qtts::qtts_decode_kernel<false, true> : (const void*)qtts::qtts_decode_kernel<false, false>);
@@ -1972,6 +1984,8 @@ hipError_t launch_persistent(const void* fn, int threads, void* kargs, uint32_t*
   return ordered_launch(dev, fn, threads, kargs, tag_base, ws, n_ws, ws_bytes, stream);
 }
 
+uint32_t entry_spin_cap() { return g_entry_cap.load(std::memory_order_relaxed); }
+
 }  // namespace qtts_host
 
 extern "C" {
@@ -2054,6 +2068,19 @@ hipError_t qtts_debug_set_sequence(void* workspace, unsigned int sequence) {
   if (workspace == nullptr || sequence < 1 || sequence > kSeqLimit) return hipErrorInvalidValue;
   std::lock_guard<std::mutex> lk(g_mu);
   g_seq[workspace] = sequence;
+  return hipSuccess;
+}
+
+hipError_t qtts_debug_set_error(void* workspace, unsigned int code, hipStream_t stream) {
+  if (workspace == nullptr || code == 0u) return hipErrorInvalidValue;
+  Workspace* ws = reinterpret_cast<Workspace*>(workspace);
+  hipError_t e = hipMemcpyAsync(&ws->err, &code, sizeof(code), hipMemcpyHostToDevice, stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);
+  return e;
+}
+
+hipError_t qtts_debug_entry_spin_cap(unsigned int cap) {
+  g_entry_cap.store(cap == 0u ? qtts_host::kEntrySpinCap : cap, std::memory_order_relaxed);
   return hipSuccess;
 }
 

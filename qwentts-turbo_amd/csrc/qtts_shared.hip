@@ -30,6 +30,7 @@
 // XCD takes unit li, its 8 waves split the unit's positions, and every workgroup merges the
 // units of each stream when it forms that stream's O-projection input.
 #include <hip/hip_runtime.h>
+#include <atomic>
 #include <cstddef>
 #include <cstring>
 #include <mutex>
@@ -120,6 +121,7 @@ struct SArgs {
   float scale;
   uint32_t tag_base;
   uint32_t spin_cap;
+  uint32_t entry_spin_cap;   // cap of the first layer pass's waits (the arrival check)
   int n_pos;
   int n_streams;
   const bf16_t* head;
@@ -315,7 +317,9 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
   P.rs = __builtin_amdgcn_make_buffer_rsrc(ws, (short)0, (int)sizeof(SWorkspace), 0x00020000);
   P.base = ws;
   P.ec.err = &ws->err;
-  P.ec.spin_cap = a.spin_cap;
+  // the first layer pass waits under the short entry cap (an arrival check: its exchanges need
+  // every workgroup of the launch); the long cap from the second pass on
+  P.ec.spin_cap = a.entry_spin_cap;
   // slot publishes: XCD-local as plain stores (they land in the XCD's L2), cross-XCD with sc1
   // (written through to memory); one store carries value and tag together
   auto pub_local = [&](const uint64_t* p, float v, uint32_t tag) {
@@ -1136,6 +1140,7 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
       const int lp = pi * NL + layer;
       const int par = lp & 1;
       const bool last_layer = layer == NL - 1;
+      if (lp == 1) P.ec.spin_cap = a.spin_cap;
       // ---- QKV
       step_barrier();
       stamp(0);
@@ -1409,7 +1414,9 @@ template __global__ void qtts_shared_kernel<false>(const SArgs a);
 // =========================================================================================
 namespace {
 
-uint64_t* g_strace = nullptr;   // optional step timeline buffer of the weight-shared kernels
+// optional step timeline buffer of the weight-shared kernels; set from any host thread, read
+// once per launch
+std::atomic<uint64_t*> g_strace{nullptr};
 
 using qtts::sh::SArgs;
 using qtts::sh::SStream;
@@ -1432,7 +1439,8 @@ void base_sargs(SArgs& a, void* ws, int n_streams, const TTSLayerWeights* layers
   a.sel.temperature = 1.0f;
   a.sel.top_p = 1.0f;
   a.spin_cap = qtts_host::kSpinCap;
-  a.trace = g_strace;
+  a.entry_spin_cap = qtts_host::entry_spin_cap();
+  a.trace = g_strace.load(std::memory_order_acquire);
   for (int u = 0; u < qtts::sh::NUNIT; ++u) a.unit_stream[u] = -1;
 }
 
@@ -1485,7 +1493,7 @@ hipError_t qtts_debug_trace_shared(void* device_buffer, size_t bytes) {
   if (device_buffer != nullptr &&
       bytes < (size_t)qtts::NWG * qtts::sh::TRACE_STEPS * qtts::sh::TRACE_SLOTS * sizeof(uint64_t))
     return hipErrorInvalidValue;
-  g_strace = reinterpret_cast<uint64_t*>(device_buffer);
+  g_strace.store(reinterpret_cast<uint64_t*>(device_buffer), std::memory_order_release);
   return hipSuccess;
 }
 

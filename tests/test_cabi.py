@@ -87,4 +87,10 @@ def test_workspace_hooks_validate_arguments_without_a_gpu():
     assert lib.qtts_debug_set_sequence(P(4096), 0) != 0 and lib.qtts_debug_set_sequence(P(4096), 1 << 20) != 0
     assert lib.qtts_debug_set_sequence(P(4096), 5) == 0
     assert lib.qtts_workspace_release(P(4096), 1) == 0
+    # the error-word hook rejects a null workspace and a zero code before any HIP call; the
+    # entry-cap hook is host-only (0 restores the default)
+    lib.qtts_debug_set_error.argtypes = [P, ctypes.c_uint, P]
+    assert lib.qtts_debug_set_error(None, 1, None) != 0 and lib.qtts_debug_set_error(P(4096), 0, None) != 0
+    lib.qtts_debug_entry_spin_cap.argtypes = [ctypes.c_uint]
+    assert lib.qtts_debug_entry_spin_cap(64) == 0 and lib.qtts_debug_entry_spin_cap(0) == 0
     assert lib.qtts_shutdown() == 0

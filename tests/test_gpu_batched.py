@@ -82,21 +82,19 @@ def test_c4_batch8_ragged(pkg, mode):
     gaps = [_gap(d.decoder.logits_buffer()) for d in dec.streams]
     print(f"  g0 {toks[:, 0].tolist()}, top-2 gaps {[f'{g:.3f}' for g in gaps]}", flush=True)
     assert np.array_equal(toks[:, 0].cpu().numpy(), fx["tokens"][:, 0])
-    # the code-predictor frame against batch 1's from the same (GPU) backbone hidden; where that
-    # hidden equals the oracle's, against the fixture as well
-    cp = dec.cp.decoder
-    tx = torch.stack(texts).cuda()
+    # the weight-shared code-predictor frame against the oracle (kernel policy, 5 layers) run from
+    # each stream's own GPU backbone hidden, as read back after step_select; ids and combine
+    # identical, or at the first differing group a decision that a last-bit difference tips
+    orc = _cp_oracle(sd, 5)
+    toks_h, comb_h = toks.cpu(), comb.cpu()
     for s in range(n):
-        t1 = torch.full((16,), -1, **i32)
-        c1 = torch.empty(1024, dtype=torch.bfloat16, device="cuda")
-        cp.frame(hidden[s].contiguous(), g0[s:s + 1], tx[s].contiguous(), t1, c1, -1, torch.zeros(1, **i32), False,
-                 1.0, 0, 1.0, 0, 0)
-        torch.cuda.synchronize()
-        assert torch.equal(toks[s], t1), f"stream {s}: {toks[s].tolist()} vs batch 1 {t1.tolist()}"
-        assert torch.equal(comb[s], c1), f"stream {s}: combined input differs from batch 1"
-        if errs[s] == 0.0:
-            assert np.array_equal(toks[s].cpu().numpy(), fx["tokens"][s])
-            assert np.array_equal(comb[s].float().cpu().numpy(), fx["combined"][s])
+        got = toks_h[s].tolist()
+        ids = [got[0]] + orc.cp_frame(hidden[s].cpu(), got[0])
+        if got != ids:
+            _explain_cp_difference(orc, hidden[s], got[0], ids, got, False, {}, 0, f"stream {s}")
+            continue
+        assert torch.equal(comb_h[s], orc.combine(ids, texts[s])), f"stream {s}: combined input differs from the oracle"
+        print(f"  stream {s}: 15 code-predictor ids and the combine equal to the oracle's", flush=True)
 
 
 def test_shared_28_layers_literal_gains(pkg):
@@ -245,14 +243,19 @@ def _bf16_step(v: float, up: bool) -> float:
     return float(torch.tensor([b if b < 0x8000 else b - 0x10000], dtype=torch.int16).view(torch.bfloat16)[0])
 
 
-def _cp_last_bit_choice(sd, hid, g0, ids_ref, ids_got, j, sample, kw, seed):
-    """Group j (1..15) of a code-predictor frame, where two kernels chose ids_ref[j] and ids_got[j]
-    after agreeing on groups 1..j-1. The oracle (kernel policy, f64 sums), teacher-forced with the
-    agreed ids, must choose ids_ref[j] from its bf16 logits, and ids_got[j] once one logit moves by
-    one bf16 ulp (ids_got[j] up or ids_ref[j] down): a decision that a last-bit difference of one
-    sum tips, through the top-2 order, the top-k boundary or a greedy tie. Returns the move."""
-    tw = TalkerWeights.from_state_dict(sd, 1, 2)
-    orc = TalkerOracle(tw, max_seq=64, policy="kernel")
+def _cp_oracle(sd, n_cp):
+    """The oracle (kernel policy) over the n_cp code-predictor layers of sd (one backbone layer,
+    unused)."""
+    return TalkerOracle(TalkerWeights.from_state_dict(sd, 1, n_cp), max_seq=64, policy="kernel")
+
+
+def _cp_last_bit_choice(orc, hid, g0, ids_ref, ids_got, j, sample, kw, seed):
+    """Group j (1..15) of a code-predictor frame, where two computations chose ids_ref[j] and
+    ids_got[j] after agreeing on groups 1..j-1. The oracle (kernel policy, f64 sums), teacher-forced
+    with the agreed ids, must choose ids_ref[j] from its bf16 logits, and ids_got[j] once one logit
+    moves by one bf16 ulp (ids_got[j] up or ids_ref[j] down): a decision that a last-bit difference
+    of one sum tips, through the top-2 order, the top-k boundary or a greedy tie. Returns the move."""
+    tw = orc.w
     orc.cp.reset()
     orc.cp.step(rb(hid.float().cpu()).to(torch.bfloat16), pos=0)
     h, _ = orc.cp.step(orc.bb_emb[g0], pos=1)
@@ -261,16 +264,27 @@ def _cp_last_bit_choice(sd, hid, g0, ids_ref, ids_got, j, sample, kw, seed):
     lg = head_logits(tw.cp_heads[j - 1], h).float()
 
     def pick(x):
-        return sample_token(x, sample, kw["temperature"], kw["top_k"], 1.0, None, seed=seed,
-                            frame_step=kw["frame_step"], group=j)
+        return sample_token(x, sample, kw.get("temperature", 1.0), kw.get("top_k", 0), 1.0, None, seed=seed,
+                            frame_step=kw.get("frame_step", 0), group=j)
 
-    assert pick(lg) == ids_ref[j], f"group {j}: the oracle picks {pick(lg)}, batch 1 {ids_ref[j]}"
-    for idx, up, label in ((ids_got[j], True, "kernel's id one ulp up"), (ids_ref[j], False, "batch 1's id one ulp down")):
+    assert pick(lg) == ids_ref[j], f"group {j}: the oracle picks {pick(lg)}, the reference side {ids_ref[j]}"
+    for idx, up, label in ((ids_got[j], True, "kernel's id one ulp up"), (ids_ref[j], False, "reference side's id one ulp down")):
         moved = lg.clone()
         moved[idx] = _bf16_step(float(lg[idx]), up)
         if pick(moved) == ids_got[j]:
             return label
     raise AssertionError(f"group {j}: {ids_got[j]} is not the oracle's choice under a one-ulp move of either logit")
+
+
+def _explain_cp_difference(orc, hid, g0, ids_ref, ids_got, sample, kw, seed, label):
+    """ids_got differs from ids_ref (group 0 equal): the first differing group must be a decision
+    that a last-bit difference tips (_cp_last_bit_choice); later groups start from different inputs
+    and are not compared."""
+    j = next(k for k in range(16) if ids_ref[k] != ids_got[k])
+    assert j >= 1, f"{label}: group 0 id is the input and must be equal"
+    how = _cp_last_bit_choice(orc, hid, g0, ids_ref, ids_got, j, sample, kw, seed)
+    print(f"{label}: first difference at group {j} ({ids_ref[j]} vs {ids_got[j]}): the oracle's choice with the "
+          f"{how}", flush=True)
 
 
 @pytest.mark.parametrize("mode", MODES)
@@ -300,20 +314,27 @@ def test_cp_frames_streams_match_batch1(pkg, n, sample, mode):
     print(f"cp frames {n} streams sample={sample} ({mode}): launching", flush=True)
     dec.cp_frames(hid, g0, text, toks, comb, **kw)
     cp = dec.cp.decoder
+    orc = _cp_oracle(sd, 2)
     for s in range(n):
         t1 = torch.full((16,), -1, **i32)
         c1 = torch.empty(1024, dtype=torch.bfloat16, device="cuda")
         cp.frame(hid[s].contiguous(), g0[s:s + 1], text[s].contiguous(), t1, c1, -1, torch.zeros(1, **i32), sample,
                  kw["temperature"], kw["top_k"], 1.0, kw["seed"] + s, kw["frame_step"])
         torch.cuda.synchronize()
-        if mode == "shared" and not torch.equal(toks[s], t1):
-            ref, got = t1.tolist(), toks[s].tolist()
-            j = next(k for k in range(16) if ref[k] != got[k])
-            assert j >= 1, f"stream {s}: group 0 id is the input and must be equal"
-            how = _cp_last_bit_choice(sd, hid[s], int(g0[s]), ref, got, j, sample, kw, kw["seed"] + s)
-            print(f"stream {s}: first difference at group {j} ({ref[j]} vs {got[j]}): the oracle's choice "
-                  f"with the {how}", flush=True)
-            continue
+        if mode == "shared":
+            # against the oracle from the same hidden, then against batch 1
+            got = toks[s].tolist()
+            ids = [got[0]] + orc.cp_frame(hid[s].cpu(), got[0], sample, kw["temperature"], kw["top_k"],
+                                          seed=kw["seed"] + s, frame_step=kw["frame_step"])
+            if got != ids:
+                _explain_cp_difference(orc, hid[s], got[0], ids, got, sample, kw, kw["seed"] + s,
+                                       f"stream {s} (oracle)")
+            else:
+                assert torch.equal(comb[s].cpu(), orc.combine(ids, text[s].cpu())), f"stream {s}: combine vs oracle"
+            if not torch.equal(toks[s], t1):
+                _explain_cp_difference(orc, hid[s], got[0], t1.tolist(), got, sample, kw, kw["seed"] + s,
+                                       f"stream {s} (batch 1)")
+                continue
         assert torch.equal(toks[s], t1), f"stream {s}: {toks[s].tolist()} vs {t1.tolist()}"
         assert torch.equal(comb[s], c1), f"stream {s}: combined input differs"
     dec.check_error()
