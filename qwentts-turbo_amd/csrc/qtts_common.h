@@ -186,6 +186,15 @@ __device__ __forceinline__ double xlane_d(double v) {
   const uint64_t r = (uint64_t)xlane<STEP>((uint32_t)u) | ((uint64_t)xlane<STEP>((uint32_t)(u >> 32)) << 32);
   return __builtin_bit_cast(double, r);
 }
+// lane K of each group of 4 lanes, to all 4 (DPP quad_perm [K, K, K, K])
+template <int K>
+__device__ __forceinline__ double quad_bcast_d(double v) {
+  constexpr int ctrl = K | (K << 2) | (K << 4) | (K << 6);
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)u, ctrl, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(u >> 32), ctrl, 0xF, 0xF, false);
+  return __builtin_bit_cast(double, (uint64_t)lo | ((uint64_t)hi << 32));
+}
 // a pair of values reduced together (e.g. a gate and an up projection of one row)
 template <class T> struct pair2 { T a, b; };
 template <class T>

@@ -160,8 +160,7 @@ struct Lds {
   alignas(16) float q[2][HDIM];
   alignas(16) float knew[HDIM];
   alignas(16) float vnew[HDIM];
-  alignas(16) float attp[MAXC * APS];  // raw attention partials of the XCD's chunks (poller -> math)
-  float attn[2 * HDIM];    // merged attention output of the XCD's two heads
+  alignas(16) float attn[2 * HDIM];    // attention output of the XCD's two heads
   float hbv[NMATH];        // greedy head: best logit of each math wave ...
   int hbi[NMATH];          // ... and its vocabulary id
   alignas(16) float xn[HID];
@@ -419,7 +418,6 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       return;
     }
   }
-  for (int i = threadIdx.x; i < MAXC * APS; i += NTHR) s.attp[i] = 0.0f;   // weights of unused chunks are 0
   __syncthreads();
 
   Poll P;
@@ -471,17 +469,28 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   //   qn / kn: q/k-norm gains of head channels lane, lane + 64; rc / rsn: their cos / sin
   uint32_t g_in[8], g_post[8], g_fin[8];
   float qn[2], kn[2], rc[2], rsn[2];
+  // The next layer's gains are issued at the start of a step, before its poll, into these, and
+  // take over at the step's end: the pointer-table read and the loads then overlap the wait
+  // instead of sitting between the step's last vector work and the barrier.
+  uint32_t g_in_n[8], g_post_n[8];
+  float qn_n[2], kn_n[2], rc_n[2], rsn_n[2];
   float rc1[2], rsn1[2];   // two-column pass: rotary of position 1
   auto load_gain_pairs = [&](uint32_t (&g)[8], const bf16_t* src) {
     const auto* p = gmem(reinterpret_cast<const uint32_t*>(src));
 #pragma unroll
     for (int k = 0; k < 8; ++k) g[k] = p[lane + 64 * k];
   };
-  auto load_qk_gains = [&](int layer) {
+  auto load_qk_gains_to = [&](int layer, float (&qd)[2], float (&kd)[2]) QTTS_INLINE {
     const bf16_t* q = lw(LW, layer, W_QN);
     const bf16_t* k = lw(LW, layer, W_KN);
-    qn[0] = ldbf(q + lane); qn[1] = ldbf(q + lane + 64);
-    kn[0] = ldbf(k + lane); kn[1] = ldbf(k + lane + 64);
+    qd[0] = ldbf(q + lane); qd[1] = ldbf(q + lane + 64);
+    kd[0] = ldbf(k + lane); kd[1] = ldbf(k + lane + 64);
+  };
+  auto load_qk_gains = [&](int layer) { load_qk_gains_to(layer, qn, kn); };
+  auto take2 = [&](float (&d)[2], const float (&s2)[2]) QTTS_INLINE { d[0] = s2[0]; d[1] = s2[1]; };
+  auto take8 = [&](uint32_t (&d)[8], const uint32_t (&s8)[8]) QTTS_INLINE {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) d[k] = s8[k];
   };
   auto load_rope_to = [&](int pos, float (&c)[2], float (&sn)[2]) QTTS_INLINE {
     const size_t row = (size_t)rot_row(lane, pos) * HDIM;   // channel lane + 64 shares the row
@@ -708,30 +717,61 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       kv_pending = true;
     }
   };
-  // ---- poller: collect the C attention partials; per head the chunk weights
-  // w_c = exp(m_c - M) (M = max_c m_c, one chunk per lane) and 1 / Z, Z = sum_c l_c w_c.
-  // The weighted sum itself runs in the math waves (math_o), one output column per lane.
+  // ---- poller: merge the 2C attention partials (chunk c, head h) of the XCD's KV head into
+  // s.attn (the split-K combine of fused_decode_tts.cu:282-385). First every unit's (m, l) pair,
+  // one 16-byte slot pair per unit (lane (h, c); lanes past C re-read chunk C - 1): per head the
+  // chunk weights w_c = exp(m_c - M), M = max_c m_c, and Z = sum_c l_c w_c, over the 8 chunk
+  // lanes with three exchanges. Polling only these 2C pairs keeps the wait light; the 128-value
+  // accumulators are then read once (re-reading only slots not yet landed), lane (h, j) taking
+  // dims 4j .. 4j + 3 of every chunk of head h, and merged in f64:
+  // f32((sum_c acc_c w_c) * (1 / Z)).
   auto prep_o = [&](int lp, int C) {
     const int par = lp & 1;
-    poll_vec<17>(P, ws->attp[xcd][par], C * APS, tag_of(lp, T_ATT), s.attp);
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    // lane (h, c): head h = lane >> 5, chunk c = lane & 31 (c < MAXC); the max and the sum run
-    // over the 8 chunk lanes with three exchanges
+    const uint32_t o = ws_off(P, ws->attp[xcd][par]);
+    const uint32_t tg = tag_of(lp, T_ATT);
     const int h = lane >> 5, c = lane & 31;
-    const bool ok = c < C;
-    const float mc = ok ? s.attp[(2 * c + h) * APH + 128] : -INFINITY;
-    const float lc = ok ? s.attp[(2 * c + h) * APH + 129] : 0.0f;
-    float M = mc;
-    M = fmaxf(M, xlane_f<0>(M));
-    M = fmaxf(M, xlane_f<1>(M));
-    M = fmaxf(M, xlane_f<2>(M));
-    const double w = ok ? exp((double)mc - (double)M) : 0.0;
-    double Z = (double)lc * w;
-    Z += xlane_d<0>(Z);
-    Z += xlane_d<1>(Z);
-    Z += xlane_d<2>(Z);
-    if (c < MAXC) s.wts[h][c] = w;
-    if (c == 0) s.wts[h][MAXC] = 1.0 / Z;
+    // one poll of every pair this lane needs: k = 0 the (m, l) pair of unit (chunk c, head h)
+    // (lanes past C re-read chunk C - 1), k = 1 + 2 cc + e the acc dims 4 (lane & 31) + 2 e, +1
+    // of chunk cc, head h
+    float v[2 + 4 * MAXC];
+    poll_regs<1 + 2 * MAXC>(P, 64 * (1 + 2 * C), tg, v, [o, C](int i) {
+      const uint32_t k = (uint32_t)i >> 6, l = (uint32_t)i & 63u;
+      if (k == 0u) {
+        const int cc = min((int)(l & 31u), C - 1);
+        return o + 8u * (uint32_t)((2 * cc + (int)(l >> 5)) * APH + 128);
+      }
+      const uint32_t kk = k - 1u;
+      return o + 8u * ((2u * (kk >> 1) + (l >> 5)) * (uint32_t)APH + 4u * (l & 31u) + 2u * (kk & 1u));
+    });
+    {
+      const bool ok = c < C;
+      const float mc = ok ? v[0] : -INFINITY;
+      const float lc = ok ? v[1] : 0.0f;
+      float M = mc;
+      M = fmaxf(M, xlane_f<0>(M));
+      M = fmaxf(M, xlane_f<1>(M));
+      M = fmaxf(M, xlane_f<2>(M));
+      const double w = ok ? exp((double)mc - (double)M) : 0.0;
+      double Z = (double)lc * w;
+      Z += xlane_d<0>(Z);
+      Z += xlane_d<1>(Z);
+      Z += xlane_d<2>(Z);
+      if (c < MAXC) s.wts[h][c] = w;
+      if (c == 0) s.wts[h][MAXC] = 1.0 / Z;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");   // the weights written above
+    double a4[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int cc = 0; cc < MAXC; ++cc) {
+      if (cc < C) {   // chunks past C were not polled (their registers hold no value)
+        const double w = s.wts[h][cc];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a4[j] = fma((double)v[2 + 4 * cc + j], w, a4[j]);
+      }
+    }
+    const double rz = s.wts[h][MAXC];
+    *reinterpret_cast<float4*>(&s.attn[128 * h + 4 * c]) =
+        make_float4((float)(a4[0] * rz), (float)(a4[1] * rz), (float)(a4[2] * rz), (float)(a4[3] * rz));
   };
   // ---- poller: AR1 (O partials + residual) -> h1 slots; then h1 -> h1res, hn
   auto ar1 = [&](int lp, auto col) QTTS_INLINE {
@@ -879,8 +919,29 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
         }
       }
       double pr[NH * JJ];
+      if constexpr (NH * JJ % 4 == 0) {
+        // every lane of a 16-lane group holds all NH * JJ scores: lane l exponentiates those with
+        // k = l (mod 4) and its quad shares them (one f64 exp per lane instead of NH * JJ)
+        const int q4 = opaque((int)threadIdx.x) & 3;
 #pragma unroll
-      for (int k = 0; k < NH * JJ; ++k) pr[k] = exp(sc[k] == -INFINITY ? NEG : sc[k] - mn[k / JJ]);
+        for (int k4 = 0; k4 < NH * JJ / 4; ++k4) {
+          double arg = NEG;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int k = 4 * k4 + j;
+            const double v = sc[k] == -INFINITY ? NEG : sc[k] - mn[k / JJ];
+            arg = q4 == j ? v : arg;
+          }
+          const double e = exp(arg);
+          pr[4 * k4 + 0] = quad_bcast_d<0>(e);
+          pr[4 * k4 + 1] = quad_bcast_d<1>(e);
+          pr[4 * k4 + 2] = quad_bcast_d<2>(e);
+          pr[4 * k4 + 3] = quad_bcast_d<3>(e);
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < NH * JJ; ++k) pr[k] = exp(sc[k] == -INFINITY ? NEG : sc[k] - mn[k / JJ]);
+      }
 #pragma unroll
       for (int jj = 0; jj < JJ; ++jj) {
         const int pos = b0 + 4 * JJ * mw + 4 * jj + g;
@@ -1047,21 +1108,6 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     // 128 h + 2 (c' mod 64) + c' / 64, so one 16-byte pair holds channels c and c + 64
     const int lr = 16 * lg + 4 * mw + (lane >> 4), cc = lr & 127;
     if ((lane & 15) == 0) pub_local(&ws->qkv[xcd][cpar(lp, col)][(lr & ~127) + 2 * (cc & 63) + (cc >> 6)], (float)t, tg);
-  };
-  // chunked attention: merge, one column per thread: f32((sum_c acc_c w_c) * (1 / Z)); chunks
-  // c >= C carry weight 0 (their partials are finite: zero-initialised or older)
-  auto merge_attn = [&]() {
-    {
-      const int t = threadIdx.x, hh = t >> 7;
-      float pv[MAXC];
-#pragma unroll
-      for (int c = 0; c < MAXC; ++c) pv[c] = s.attp[(2 * c + hh) * APH + (t & 127)];
-      double acc = 0.0;
-#pragma unroll
-      for (int c = 0; c < MAXC; ++c) acc = fma((double)pv[c], s.wts[hh][c], acc);
-      s.attn[t] = (float)(acc * s.wts[hh][MAXC]);
-      step_barrier();
-    }
   };
   auto math_o = [&](int lp, int lg, const TileO& to, auto colc) QTTS_INLINE {
     const int col = 8 * (lane & 31);
@@ -1366,10 +1412,14 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           }
           load_gain_pairs(g_in, lw(LW, NL > 1 ? 1 : 0, W_LNIN));
           break;
-        case S_QKV:
+        case S_QKV: {
+          const bool rope_next = layer == NL - 1 && !q.last_pos;
+          load_qk_gains_to(nl, qn_n, kn_n);
+          if (rope_next) load_rope_to(q.pos + 1, rc_n, rsn_n);
           prep_att(lp, layer, q.pos, q.C, Col0{});
-          load_qk_gains(nl);
-          if (layer == NL - 1 && !q.last_pos) load_rope(q.pos + 1);
+          take2(qn, qn_n);
+          take2(kn, kn_n);
+          if (rope_next) { take2(rc, rc_n); take2(rsn, rsn_n); }
           if (kv_only(pi, layer)) {
             // position 1's input, in place of this position's DOWN step; the math waves read
             // xn before publishing the QKV rows prep_att has waited for, so xn is free
@@ -1379,6 +1429,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
             load_gain_pairs(g_post, lw(LW, 0, W_LNPOST));
           }
           break;
+        }
         case S_ATT:
           // the math waves' attention synchronises the whole workgroup (passes + 2 times);
           // this wave's inputs for the step are produced after those points anyway
@@ -1394,38 +1445,46 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
             for (int b = 0; b < nb; ++b) step_barrier();
           }
           if (q.local) {
+            load_gain_pairs(g_post_n, lw(LW, nl, W_LNPOST));
             prep_gu(lp, layer, Col0{});
-            load_gain_pairs(g_post, lw(LW, nl, W_LNPOST));
+            take8(g_post, g_post_n);
           } else {
             prep_o(lp, q.C);
           }
           break;
         case S_O:
-          step_barrier();   // joins the barrier after the math waves' attention merge
+          load_gain_pairs(g_post_n, lw(LW, nl, W_LNPOST));
           prep_gu(lp, layer, Col0{});
-          load_gain_pairs(g_post, lw(LW, nl, W_LNPOST));
+          take8(g_post, g_post_n);
           break;
         case S_GU: prep_down(lp, Col0{}); break;
-        case S_DOWN:
+        case S_DOWN: {
+          // g_in then serves the layer after next
+          const bool gin_next = layer < NL - 1 || !(q.head || q.last_pos);
+          if (gin_next) load_gain_pairs(g_in_n, lw(LW, (nl + 1) % NL, W_LNIN));
           if (layer < NL - 1) { ar2(lp, Col0{}); prep_input_next(lp, Col0{}); }
           else if (q.head || q.last_pos) { ar2(lp, Col0{}); prep_final(lp, Col0{}); }
           else {
             prep_input0(pi + 1, Col0{});
             if (a.cp_frame && lead) comb_add(pi == 0, Col0{});
           }
-          // g_in now serves the layer after next
-          if (layer < NL - 1 || !(q.head || q.last_pos)) load_gain_pairs(g_in, lw(LW, (nl + 1) % NL, W_LNIN));
+          if (gin_next) take8(g_in, g_in_n);
           break;
+        }
         case S_QKV2:
           if constexpr (DUO_OK) {
+            load_qk_gains_to(nl, qn_n, kn_n);
+            if (layer == NL - 1) load_rope_to(q.pos + 1, rc_n, rsn_n);
             prep_att(lp - NL, layer, q.pos - 1, q.C, Col0{});
             prep_att(lp, layer, q.pos, q.C, Col1{});
-            load_qk_gains(nl);
-            if (layer == NL - 1) load_rope(q.pos + 1);
+            take2(qn, qn_n);
+            take2(kn, kn_n);
+            if (layer == NL - 1) { take2(rc, rc_n); take2(rsn, rsn_n); }
           }
           break;
         case S_ATT2:
           if constexpr (DUO_OK) {
+            load_gain_pairs(g_post_n, lw(LW, nl, W_LNPOST));
             for (int b = 0; b < 3; ++b) step_barrier();   // the local attention's three barriers
             // position 0's last layer feeds nothing beyond its K/V entry; both columns' sums are
             // published before either gather, so neither gather waits behind the other's
@@ -1433,7 +1492,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
             ar1(lp, Col1{});
             if (layer < NL - 1) gather_h1(lp - NL, Col0{});
             gather_h1(lp, Col1{});
-            load_gain_pairs(g_post, lw(LW, nl, W_LNPOST));
+            take8(g_post, g_post_n);
           }
           break;
         case S_GU2:
@@ -1445,11 +1504,12 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
         case S_DOWN2:
           if constexpr (DUO_OK) {
             if (layer < NL - 1) {
+              load_gain_pairs(g_in_n, lw(LW, (nl + 1) % NL, W_LNIN));
               ar2(lp - NL, Col0{});
               ar2(lp, Col1{});
               prep_input_next(lp - NL, Col0{});
               prep_input_next(lp, Col1{});
-              load_gain_pairs(g_in, lw(LW, (nl + 1) % NL, W_LNIN));
+              take8(g_in, g_in_n);
             } else {
               ar2(lp, Col1{});
               prep_final(lp, Col1{});
@@ -1457,6 +1517,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           }
           break;
         case S_HEAD:
+          if (a.cp_frame && !q.last_pos) load_gain_pairs(g_in_n, lw(LW, NL > 1 ? 1 : 0, W_LNIN));
           if (cp_greedy) step_barrier();   // joins the math waves' head barrier
           if (a.cp_frame || lead) {
             const int tok = select(pi);
@@ -1466,7 +1527,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
               if (!q.last_pos) {
                 prep_input0(pi + 1, Col0{});
                 if (lead) comb_add(false, Col0{});
-                load_gain_pairs(g_in, lw(LW, NL > 1 ? 1 : 0, W_LNIN));
+                take8(g_in, g_in_n);
               }
             } else if (lane == 0 && SIO(out_token)) {
               *SIO(out_token) = tok;
@@ -1621,7 +1682,6 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           }
           break;
         case S_O:
-          merge_attn();
           o_stage(layer);
           load_gu<BB>(tgu, LW, layer, xcd, li, mw, lane);
           break;

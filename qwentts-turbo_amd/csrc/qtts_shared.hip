@@ -193,38 +193,6 @@ __device__ __forceinline__ void split3x2(float x0, float x1, uint32_t& h, uint32
   l = f2bf2(r0 - bflo(m), r1 - bfhi(m));
 }
 
-// Read npair 16-byte pairs into registers (pair k of this lane: i = lane + 64 k < npair) until
-// every tag matches, one round of loads in flight, re-issuing only the pairs still pending: for
-// data that has (nearly all) arrived, which a batched poll would fetch several times over.
-template <int MAXP, typename OffF>
-__device__ __forceinline__ bool read_pairs(const Poll& P, int npair, uint32_t tag, float (&out)[2 * MAXP], OffF off) {
-  const int lane = opaque((int)threadIdx.x & 63);
-  uint32_t pending = 0;
-#pragma unroll
-  for (int k = 0; k < MAXP; ++k)
-    if (lane + 64 * k < npair) pending |= 1u << k;
-  uint32_t spins = 0;
-  for (;;) {
-    u32x4 v[MAXP];
-#pragma unroll
-    for (int k = 0; k < MAXP; ++k)
-      if (pending & (1u << k)) v[k] = __builtin_amdgcn_raw_buffer_load_b128(P.rs, off(lane + 64 * k), 0, 16);
-#pragma unroll
-    for (int k = 0; k < MAXP; ++k) {
-      if ((pending & (1u << k)) && v[k].y == tag && v[k].w == tag) {
-        out[2 * k] = __uint_as_float(v[k].x);
-        out[2 * k + 1] = __uint_as_float(v[k].z);
-        pending &= ~(1u << k);
-      }
-    }
-    if (__ballot(pending != 0u) == 0ull) return true;
-    ++spins;
-    if ((spins & 63u) == 0u && (spins > P.ec.spin_cap || err_set(P.ec))) {
-      if (lane == 0) atomicOr(P.ec.err, 1u);
-      return false;
-    }
-  }
-}
 // Sum of the 8 XCD partials of rows r0 + 2 (lane & 15) + {0, 1} of one stream: lane group
 // g = lane >> 4 polls XCDs 2 g and 2 g + 1; two exchanges complete the sum as
 // ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7)), the same in every lane and workgroup.
@@ -245,17 +213,6 @@ __device__ __forceinline__ bool poll_sum8s(const Poll& P, const uint64_t* p0, ui
   return ok;
 }
 
-// A 1024-vector published by the 32 workgroups of an XCD, workgroup j writing rows
-// [32 j, 32 j + 32) as 16 pairs from one store instruction: lanes 0..31 poll the last pair of
-// producer `lane` until all 32 have landed, then every pair is read once (lane gets elements
-// 2 (lane + 64 k) + {0, 1}). Polling one pair per producer instead of all 512 keeps the eight
-// waves' polls from filling the CU's memory pipeline.
-__device__ __forceinline__ bool gather1024(const Poll& P, const uint64_t* p, uint32_t tag, float (&out)[16]) {
-  const uint32_t o = ws_off(P, p);
-  float pr[2];
-  if (!poll_regs<1>(P, WPX, tag, pr, [o](int i) { return o + 16u * (16u * (uint32_t)i + 15u); })) return false;
-  return read_pairs<8>(P, HID / 2, tag, out, [o](int i) { return o + 16u * (uint32_t)i; });
-}
 
 // Token selection over an LDS logit vector, kept out of line: inlined, the loop-invariant parts of
 // its sampler would be hoisted out of the step loops and hold registers (or spill) for the whole

@@ -220,6 +220,90 @@ def test_qtts_backbone_step_streams(lib, model):
               None, 0, _stream()) != 0
 
 
+def test_qtts_backbone_step_shared_skip(lib, model):
+    """The weight-shared launch (qtts_backbone_step_shared, the default batched mode) over three
+    streams at positions 0, 9 and 40: each within the shared kernel's bar (f32 MFMA sums against
+    the f64 oracle, 2 layers: rel-L2 < 2e-3). Then its skip flags: with flags [0, 1, 0] stream 1
+    keeps a marker in its hidden and its KV slot stays zero while the others step; a launch with
+    every stream skipped (its early return) writes nothing; the launch after it on the same
+    workspace is again equal to the oracle."""
+    sd, tw = model
+    tol = 2e-3
+    layers = [[t.cuda().contiguous() for t in lw] for lw in tw.bb_layers]
+    table = _layer_table(layers)
+    norm = tw.bb_norm.cuda()
+    max_seq = 64
+    cos, sin = (t.cuda() for t in rope_tables(max_seq, 128, 1e6))
+    lib.qtts_shared_workspace_bytes.restype = ctypes.c_size_t
+    ws = torch.zeros(lib.qtts_shared_workspace_bytes(), dtype=torch.uint8, device="cuda")
+    lib.qtts_shared_workspace_check.argtypes = [P, ctypes.POINTER(ctypes.c_uint), P]
+    lib.qtts_shared_workspace_check.restype = I
+    fn = lib.qtts_backbone_step_shared
+    fn.argtypes = [I, P, P, I, P, P, P, I, ctypes.POINTER(QttsBackboneStream), P, I, I, F, I, I, P, I, P]
+    fn.restype = I
+    g = torch.Generator().manual_seed(9)
+    positions = [0, 9, 40]
+    bufs, orcs, xs = [], [], []
+    arr = (QttsBackboneStream * 3)()
+    for s, pos in enumerate(positions):
+        kc = torch.zeros(2, 8, max_seq, 128, dtype=torch.bfloat16)
+        vc = torch.zeros_like(kc)
+        kc[:, :, :pos] = torch.randn(2, 8, pos, 128, generator=g).to(torch.bfloat16)
+        vc[:, :, :pos] = torch.randn(2, 8, pos, 128, generator=g).to(torch.bfloat16)
+        orc = DecoderOracle(tw.bb_layers, tw.bb_norm, max_seq, "backbone", "kernel")
+        orc.set_kv(kc[:, :, :pos], vc[:, :, :pos])
+        x = torch.randn(1024, generator=g).to(torch.bfloat16)
+        b = dict(kc=kc.cuda(), vc=vc.cuda(), x=x.cuda(), hid=torch.empty(1024, device="cuda"),
+                 res=torch.empty(1024, dtype=torch.bfloat16, device="cuda"))
+        bufs.append(b); orcs.append(orc); xs.append(x)
+        st = arr[s]
+        st.k_cache, st.v_cache = b["kc"].data_ptr(), b["vc"].data_ptr()
+        st.input_embedding, st.out_hidden, st.out_residual = b["x"].data_ptr(), b["hid"].data_ptr(), b["res"].data_ptr()
+
+    def launch(step, flags):
+        for s in range(3):
+            arr[s].position = positions[s] + step
+            arr[s].pos3[0] = arr[s].pos3[1] = arr[s].pos3[2] = positions[s] + step
+            arr[s].skip_if = flags.data_ptr() + 4 * s if flags is not None else None
+        assert fn(3, _ptr(ws), _ptr(table), 2, _ptr(norm), _ptr(cos), _ptr(sin), max_seq, arr, None, 0, 0, 1.0, -1,
+                  0, None, 0, _stream()) == 0
+        torch.cuda.synchronize()
+        code = ctypes.c_uint(0)
+        assert lib.qtts_shared_workspace_check(_ptr(ws), ctypes.byref(code), _stream()) == 0 and code.value == 0
+
+    def check(s, step):
+        hr, _ = orcs[s].step(xs[s], pos=positions[s] + step)
+        e = rel_l2(bufs[s]["hid"].cpu(), hr)
+        ek = rel_l2(bufs[s]["kc"][:, :, positions[s] + step].float().cpu(), orcs[s].k[:, :, positions[s] + step].float())
+        assert e < tol and ek < tol, (s, step, e, ek)
+        return e
+
+    print("qtts_backbone_step_shared, 3 streams: launching", flush=True)
+    launch(0, None)
+    worst = max(check(s, 0) for s in range(3))
+    print(f"qtts_backbone_step_shared, 3 streams: worst rel_l2 {worst:.2e}", flush=True)
+    marker = torch.full((1024,), 7.0, device="cuda")
+    bufs[1]["hid"].copy_(marker)
+    launch(1, torch.tensor([0, 1, 0], dtype=torch.int32, device="cuda"))
+    assert torch.equal(bufs[1]["hid"], marker)
+    assert int(bufs[1]["kc"][:, :, positions[1] + 1].float().abs().sum()) == 0
+    assert int(bufs[1]["vc"][:, :, positions[1] + 1].float().abs().sum()) == 0
+    for s in (0, 2):
+        check(s, 1)
+    # every stream skipped: the launch returns early and writes nothing
+    hid_before = [b["hid"].clone() for b in bufs]
+    launch(2, torch.ones(3, dtype=torch.int32, device="cuda"))
+    for s in range(3):
+        assert torch.equal(bufs[s]["hid"], hid_before[s])
+        assert int(bufs[s]["kc"][:, :, positions[s] + 2].float().abs().sum()) == 0
+    # the next launch on the same workspace; stream 1's slot of step 1 was never written and stays
+    # zero, in its cache and in the oracle's (a skipped stream's position still advances)
+    launch(2, None)
+    for s in range(3):
+        check(s, 2)
+    print("qtts_backbone_step_shared: skip [0, 1, 0], all skipped, then a normal launch: all as expected", flush=True)
+
+
 def test_qtts_backbone_prefill(lib, model):
     """A 20-token prompt in one call, K/V straight into the cache, against the oracle's
     transformers-bf16 policy stepped token by token (2 layers: rel-L2 <= 1e-2)."""
