@@ -315,6 +315,7 @@ def main():
                     help="only time the backbone step at KV length L (one JSON line; for per-context profiles)")
     ap.add_argument("--no-batched", action="store_true", help="skip the batch-8 ragged-context figure")
     ap.add_argument("--no-prefill", action="store_true", help="skip the MFMA prefill figures")
+    ap.add_argument("--no-contexts", action="store_true", help="skip the backbone figures at L=129 and L=2048")
     ap.add_argument("--prefill-only", action="store_true", help="only the MFMA prefill figures (one JSON line)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device-to-device copies of MIB MiB (the reference kernel for "
@@ -432,7 +433,8 @@ def main():
                      "algorithmic_bytes": dominant[2], "traffic": dominant[3]},
     }
     # backbone steps/s and roofline at config 0's context (L = 129) and config 3's (L = 2048)
-    out["backbone_by_context"] = {f"L{L}": backbone_figure(bbg, L) for L in (129, 2048)}
+    if not args.no_contexts:
+        out["backbone_by_context"] = {f"L{L}": backbone_figure(bbg, L) for L in (129, 2048)}
     # the prefill is timed before the batched phase, whose 8 stream decoders stay allocated until
     # it returns (with them alive, the 229 host launches of a 128-token prefill fell behind the GPU)
     if not args.no_prefill:

@@ -69,11 +69,13 @@ __device__ bool poll_regs(const Poll& P, int npair, uint32_t tag, float (&out)[2
       if (timed_out()) return false;
     }
   } else {
+    // one round in flight; every load issued unconditionally (a load under a branch makes the
+    // compiler wait for it before issuing the next)
     for (;;) {
       u32x4 v[MAXP];
 #pragma unroll
       for (int k = 0; k < MAXP; ++k)
-        if (pending & (1u << k)) v[k] = __builtin_amdgcn_raw_buffer_load_b128(P.rs, off(lane + 64 * k), 0, 16);
+        v[k] = __builtin_amdgcn_raw_buffer_load_b128(P.rs, off((valid >> k) & 1u ? lane + 64 * k : 0), 0, 16);
       if (check(v)) return true;
       if (timed_out()) return false;
     }
