@@ -448,7 +448,11 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   TileKV<BB> tk;
 
   auto tag_of = [&](int lp, int slot) -> uint32_t { return a.tag_base + (uint32_t)(lp * T_NSLOT + slot); };
-  const bool cp_greedy = a.cp_frame && !a.sel.do_sample;
+  // greedy heads (code-predictor groups, the backbone's codec head) select through a two-level
+  // exchange of workgroup candidates instead of gathering every logit in one workgroup
+  const bool greedy_sel = !a.sel.do_sample && (BB || a.cp_frame);
+  // backbone greedy head with a repetition penalty: the history as a bitmap in LDS (built at launch)
+  const bool pen_rows = BB && !a.cp_frame && greedy_sel && a.head != nullptr && a.rep_penalty != 1.0f && SIO(n_history) > 0;
   auto has_head = [&](int pi) -> bool { return a.cp_frame ? pi >= 1 : (a.head != nullptr && pi == a.n_pos - 1); };
 
   // rotary row of channel c (c < 64) at position pos
@@ -1185,9 +1189,21 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     const int r = lane >> 4;
     // logits are bf16 values, as the reference's torch.mv over bf16 operands returns them
     // (generator.py:158, :351); ties then go to the lowest id, as torch.argmax
-    if (cp_greedy) {
-      float cv = ((lane & 15) == 0 && r < nrows) ? rbf((float)t) : -INFINITY;
-      int ci = row0 + r;
+    if (greedy_sel) {
+      const int ci0 = row0 + r;
+      float cv = -INFINITY;
+      if ((lane & 15) == 0 && r < nrows) {
+        cv = rbf((float)t);
+        if (BB && !a.cp_frame) {
+          // the backbone's codec head: raw logit out, then the selection's mask, repetition
+          // penalty and EOS suppression on this row (generator.py:71-75, 161-167)
+          if (SIO(out_logits)) SIO(out_logits[ci0]) = cv;
+          if (a.mask_tail && ci0 >= a.vocab - 1024 && ci0 != a.eos_id) cv = -INFINITY;
+          if (pen_rows && ((s.pen_bits[ci0 >> 5] >> (ci0 & 31)) & 1u)) cv = rbf(cv > 0.f ? cv / a.rep_penalty : cv * a.rep_penalty);
+          if (a.suppress_eos && ci0 == a.eos_id) cv = -INFINITY;
+        }
+      }
+      int ci = ci0;
       best_merge(cv, ci, xlane_f<4>(cv), (int)xlane<4>((uint32_t)ci));
       best_merge(cv, ci, xlane_f<5>(cv), (int)xlane<5>((uint32_t)ci));
       best_merge(bv, bi, cv, ci);
@@ -1200,7 +1216,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   // greedy code-predictor head: only the workgroup's best (value, lowest id on ties) is published;
   // the selecting waves reduce the workgroup candidates instead of the whole vocabulary
   auto head_publish = [&](int pi, float bv, int bi) {
-    if (!cp_greedy) return;
+    if (!greedy_sel) return;
     const uint32_t tg = a.tag_base + TAG_HEAD + (uint32_t)pi;
     if (lane == 0) { s.hbv[mw] = bv; s.hbi[mw] = bi; }
     step_barrier();
@@ -1218,7 +1234,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   };
   // ---- poller: collect a head's logits and select a token
   auto select = [&](int pi) -> int {
-    if (cp_greedy) {
+    if (greedy_sel) {
       // Candidates {value, index} are merged by larger value, lower index on ties (an
       // order-independent choice). Level 1: the 32 workgroup bests of this XCD (L2-local).
       const uint32_t tg = a.tag_base + TAG_HEAD + (uint32_t)pi;
@@ -1246,7 +1262,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       if constexpr (XL) {
         // one stream per XCD: the XCD's best is the stream's
         bi = __builtin_amdgcn_readfirstlane(bi);
-        return (bi >= 0 && bi < a.cp_vocab) ? bi : 0;
+        return (bi >= 0 && bi < (a.cp_frame ? a.cp_vocab : a.vocab)) ? bi : 0;
       }
       // Level 2: this workgroup's copy of the XCD best goes to hx[li][xcd]; the 8 XCD bests are
       // read from the copies of workgroup index li (each cache line has 8 readers).
@@ -1273,10 +1289,10 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       }
       bi = __builtin_amdgcn_readfirstlane(bi);
       // a timed-out poll leaves the error word set and may leave garbage: keep the id in range
-      return (bi >= 0 && bi < a.cp_vocab) ? bi : 0;
+      return (bi >= 0 && bi < (a.cp_frame ? a.cp_vocab : a.vocab)) ? bi : 0;
     }
     const int n = a.cp_frame ? a.cp_vocab : a.vocab;
-    poll_vec<24>(P, ws->logits[pi & 1], n, a.tag_base + TAG_HEAD + (uint32_t)pi, s.stage);
+    poll_vec_long(P, ws->logits[pi & 1], n, a.tag_base + TAG_HEAD + (uint32_t)pi, s.stage);
     SelParams sp = a.sel;
     sp.seed = SIO(seed);
     if (a.cp_frame) {
@@ -1396,6 +1412,15 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           if (a.cp_frame) {
             if (lane < a.n_groups) s.embp[lane] = a.cp_embs[lane];
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          }
+          if (pen_rows) {
+            // ids in the history, once per distinct id (generator.py:161-167); read by the head rows
+            for (int i = lane; i < MAXV / 32; i += 64) s.pen_bits[i] = 0u;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            for (int i = lane; i < SIO(n_history); i += 64) {
+              const int id = SIO(history[i]);
+              if (id >= 0 && id < a.vocab) atomicOr(&s.pen_bits[id >> 5], 1u << (id & 31));
+            }
           }
           load_gain_pairs(g_in, lw(LW, 0, W_LNIN));
           load_gain_pairs(g_post, lw(LW, 0, W_LNPOST));
@@ -1518,8 +1543,9 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           break;
         case S_HEAD:
           if (a.cp_frame && !q.last_pos) load_gain_pairs(g_in_n, lw(LW, NL > 1 ? 1 : 0, W_LNIN));
-          if (cp_greedy) step_barrier();   // joins the math waves' head barrier
-          if (a.cp_frame || lead) {
+          if (greedy_sel) step_barrier();   // joins the math waves' head barrier
+          // greedy backbone head: workgroup 0 of every XCD takes part in the candidate exchange
+          if (a.cp_frame || lead || (greedy_sel && !XL && li == 0)) {
             const int tok = select(pi);
             if (a.cp_frame) {
               if (lane == 0) s.tok[pi - 1] = tok;
@@ -1529,7 +1555,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
                 if (lead) comb_add(false, Col0{});
                 take8(g_in, g_in_n);
               }
-            } else if (lane == 0 && SIO(out_token)) {
+            } else if (lead && lane == 0 && SIO(out_token)) {
               *SIO(out_token) = tok;
             }
           }

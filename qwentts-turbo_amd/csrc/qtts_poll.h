@@ -133,6 +133,16 @@ __device__ __forceinline__ bool poll_vec(const Poll& P, const uint64_t* p, int n
   const uint32_t o = ws_off(P, p);
   return poll_pairs<MAXP>(P, n >> 1, tag, dst, [o](int i) { return o + 16u * (uint32_t)i; });
 }
+// contiguous n slots (n even, up to MAXV) into LDS, in pieces of 1024 slots (8 pairs per lane):
+// each piece keeps two batches of 8 loads in flight, and no more registers than that are held
+__device__ __forceinline__ bool poll_vec_long(const Poll& P, const uint64_t* p, int n, uint32_t tag, float* dst) {
+  bool ok = true;
+  for (int s0 = 0; s0 < n; s0 += 1024) {
+    const int m = n - s0 < 1024 ? n - s0 : 1024;
+    ok = poll_vec<8>(P, p + s0, m, tag, dst + s0) && ok;
+  }
+  return ok;
+}
 // contiguous 1024 slots into registers: this lane gets elements 2 (lane + 64 k) + {0, 1}
 __device__ __forceinline__ bool poll_vec_regs(const Poll& P, const uint64_t* p, uint32_t tag, float (&out)[16]) {
   const uint32_t o = ws_off(P, p);

@@ -1042,7 +1042,7 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
   // workgroup only: the selection scratch overlays the projection inputs)
   auto select_full = [&](int pi) -> int {
     const int n = cp ? a.cp_vocab : a.vocab;
-    poll_vec<24>(P, &ws->logits[pi & 1][wv][0], n, a.tag_base + TAG_HEAD + (uint32_t)pi, s.z.stage);
+    poll_vec_long(P, &ws->logits[pi & 1][wv][0], n, a.tag_base + TAG_HEAD + (uint32_t)pi, s.z.stage);
     SelParams sp = a.sel;
     sp.seed = IO->seed;
     if (cp) {
