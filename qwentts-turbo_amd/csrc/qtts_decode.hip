@@ -55,10 +55,10 @@ struct Workspace {
   uint64_t opart[2][NXCD][HID];
   uint64_t dpart[2][NXCD][HID];
   uint64_t logits[2][MAXV];
-  // greedy code-predictor heads, two-level candidate exchange ({value, tag, index, tag} each):
-  //   hloc: each workgroup's best, read by the 32 workgroups of its XCD
+  // greedy heads, two-level candidate exchange ({value, tag, index, tag} each):
+  //   hloc: each math wave's best (4 per workgroup), read by the 32 workgroups of its XCD
   //   hx:   every workgroup's copy of its XCD's best, [li][xcd], read by the 8 workgroups li
-  uint64_t hloc[NXCD][2][2 * WPX];
+  uint64_t hloc[NXCD][2][2 * NMATH * WPX];
   uint64_t hx[2][WPX][2 * NXCD];
   uint32_t err;
   uint32_t pad[63];
@@ -161,8 +161,6 @@ struct Lds {
   alignas(16) float knew[HDIM];
   alignas(16) float vnew[HDIM];
   alignas(16) float attn[2 * HDIM];    // attention output of the XCD's two heads
-  float hbv[NMATH];        // greedy head: best logit of each math wave ...
-  int hbi[NMATH];          // ... and its vocabulary id
   alignas(16) float xn[HID];
   alignas(16) float hn[HID];
   float inter[XI];
@@ -1215,18 +1213,14 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   };
   // greedy code-predictor head: only the workgroup's best (value, lowest id on ties) is published;
   // the selecting waves reduce the workgroup candidates instead of the whole vocabulary
+  // (each math wave publishes its own best: no workgroup barrier on the way to the exchange)
   auto head_publish = [&](int pi, float bv, int bi) {
     if (!greedy_sel) return;
     const uint32_t tg = a.tag_base + TAG_HEAD + (uint32_t)pi;
-    if (lane == 0) { s.hbv[mw] = bv; s.hbi[mw] = bi; }
-    step_barrier();
-    if (mw == 0 && lane == 0) {
-      float wv = s.hbv[0];
-      int wi = s.hbi[0];
-#pragma unroll
-      for (int w = 1; w < NMATH; ++w) best_merge(wv, wi, s.hbv[w], s.hbi[w]);
-      const u32x4 d = {__float_as_uint(wv), tg, (uint32_t)wi, tg};
-      __builtin_amdgcn_raw_buffer_store_b128(d, P.rs, (int)ws_off(P, &ws->hloc[XL ? 0 : xcd][pi & 1][2 * (XL ? li_hw : li)]), 0, 0);
+    if (lane == 0) {
+      const u32x4 d = {__float_as_uint(bv), tg, (uint32_t)bi, tg};
+      const int slot = NMATH * (XL ? li_hw : li) + mw;
+      __builtin_amdgcn_raw_buffer_store_b128(d, P.rs, (int)ws_off(P, &ws->hloc[XL ? 0 : xcd][pi & 1][2 * slot]), 0, 0);
     }
   };
   auto head_weights = [&](int pi) -> const bf16_t* {
@@ -1236,18 +1230,19 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   auto select = [&](int pi) -> int {
     if (greedy_sel) {
       // Candidates {value, index} are merged by larger value, lower index on ties (an
-      // order-independent choice). Level 1: the 32 workgroup bests of this XCD (L2-local).
+      // order-independent choice). Level 1: the 128 wave bests of this XCD (L2-local), two per lane.
       const uint32_t tg = a.tag_base + TAG_HEAD + (uint32_t)pi;
       const int par = pi & 1;
-      float cv[2];
+      float cv[4];
       {
         const uint32_t o = ws_off(P, &ws->hloc[XL ? 0 : xcd][par][0]);
-        poll_regs<1>(P, WPX, tg, cv, [o](int i) { return o + 16u * (uint32_t)i; });
+        poll_regs<2>(P, NMATH * WPX, tg, cv, [o](int i) { return o + 16u * (uint32_t)i; });
       }
-      float bv = lane < WPX ? cv[0] : -INFINITY;
-      int bi = lane < WPX ? (int)__float_as_uint(cv[1]) : 0x7fffffff;
+      float bv = cv[0];
+      int bi = (int)__float_as_uint(cv[1]);
+      best_merge(bv, bi, cv[2], (int)__float_as_uint(cv[3]));
 #pragma unroll
-      for (int st = 0; st < 5; ++st) {
+      for (int st = 0; st < 6; ++st) {
         float ov;
         int oi;
         switch (st) {
@@ -1255,7 +1250,8 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           case 1: ov = xlane_f<1>(bv); oi = (int)xlane<1>((uint32_t)bi); break;
           case 2: ov = xlane_f<2>(bv); oi = (int)xlane<2>((uint32_t)bi); break;
           case 3: ov = xlane_f<3>(bv); oi = (int)xlane<3>((uint32_t)bi); break;
-          default: ov = xlane_f<4>(bv); oi = (int)xlane<4>((uint32_t)bi); break;
+          case 4: ov = xlane_f<4>(bv); oi = (int)xlane<4>((uint32_t)bi); break;
+          default: ov = xlane_f<5>(bv); oi = (int)xlane<5>((uint32_t)bi); break;
         }
         best_merge(bv, bi, ov, oi);
       }
@@ -1270,12 +1266,13 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
         const u32x4 d = {__float_as_uint(bv), tg, (uint32_t)bi, tg};
         __builtin_amdgcn_raw_buffer_store_b128(d, P.rs, (int)ws_off(P, &ws->hx[par][li][2 * xcd]), 0, 16);
       }
+      float cx[2];
       {
         const uint32_t o = ws_off(P, &ws->hx[par][li][0]);
-        poll_regs<1>(P, NXCD, tg, cv, [o](int i) { return o + 16u * (uint32_t)i; });
+        poll_regs<1>(P, NXCD, tg, cx, [o](int i) { return o + 16u * (uint32_t)i; });
       }
-      bv = lane < NXCD ? cv[0] : -INFINITY;
-      bi = lane < NXCD ? (int)__float_as_uint(cv[1]) : 0x7fffffff;
+      bv = lane < NXCD ? cx[0] : -INFINITY;
+      bi = lane < NXCD ? (int)__float_as_uint(cx[1]) : 0x7fffffff;
 #pragma unroll
       for (int st = 0; st < 3; ++st) {
         float ov;
@@ -1543,7 +1540,6 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           break;
         case S_HEAD:
           if (a.cp_frame && !q.last_pos) load_gain_pairs(g_in_n, lw(LW, NL > 1 ? 1 : 0, W_LNIN));
-          if (greedy_sel) step_barrier();   // joins the math waves' head barrier
           // greedy backbone head: workgroup 0 of every XCD takes part in the candidate exchange
           if (a.cp_frame || lead || (greedy_sel && !XL && li == 0)) {
             const int tok = select(pi);
