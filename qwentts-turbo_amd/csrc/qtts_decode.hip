@@ -15,10 +15,11 @@
 //     XCDs hold bit-identical activations).
 //   * Inside an XCD the 32 workgroups split rows evenly: 16 QKV rows, 32 O rows, 12 gate +
 //     12 up rows, 32 down rows each, so every weight byte is read exactly once per step.
-//   * Attention of the XCD's KV head is split over C sequence chunks (one per workgroup);
-//     the chunk partials (m, l, acc) are merged by every O-projection workgroup.
+//   * Attention of the XCD's KV head is split over C sequence chunks, one workgroup per
+//     (chunk, query head); the poller of every O-projection workgroup merges the chunk partials
+//     (m, l, acc). Contexts that fit one pass are attended locally by every workgroup.
 //   * Each workgroup = 4 math waves + 1 poller wave. Math waves hold their weight slices in
-//     VGPRs, prefetched two stages ahead, and run the GEMVs and attention. The poller wave
+//     VGPRs, the next step's tile issued one step ahead, and run the GEMVs and attention. The poller wave
 //     waits for the inputs of the next stage (tagged exchange slots, see qtts_common.h),
 //     applies the vector work (RMSNorm, q/k-norm + RoPE, KV write, split-K merge, the
 //     cross-XCD sums + residuals, token selection) and leaves ready operands in LDS. Keeping
