@@ -54,8 +54,11 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int NS = 8;                 // stream slots of a launch (one per wave)
 constexpr int SWAV = 8;               // waves per workgroup
 constexpr int STHR = 64 * SWAV;
-constexpr int KP = HID + 8;           // bf16 row of one input piece; the pad puts the 16 rows one
+constexpr int KP = HID + 8;           // bf16 row of one input column; the pad puts the 16 rows one
                                       // fragment read touches on distinct LDS banks
+constexpr int XPS = 2 * NS * KP + 64; // bf16 elements from one input piece to the next (32 dwords past a
+                                      // multiple of 64 banks: hi of stream s and mid of stream s, read
+                                      // by one fragment, sit on distinct banks)
 constexpr int NUNIT = WPX;            // attention units per KV head (one per workgroup)
 constexpr int UMAX = 8;               // attention units of one stream
 constexpr int UPH = 132;              // slots of one (unit, head) partial: acc[128], m, l, pad
@@ -148,19 +151,24 @@ constexpr int TRACE_STEPS = 1024;
 
 struct SLds {
   union {
-    alignas(16) bf16_t xb[3][NS][KP];   // projection input pieces (hi, mid, lo) of every stream
+    // projection input pieces (hi, mid, lo): piece p of column n at xb[p * XPS + n * KP]. Columns
+    // 0..7 are the streams; the code-predictor frame's two-column pass puts position 1 of
+    // stream s in column 8 + s
+    alignas(16) bf16_t xb[3 * XPS];
     struct {
       alignas(16) float stage[MAXV];    // token selection of one stream (its own workgroup)
       SelScratch sel;
     } z;
   };
-  alignas(16) float red[SWAV][16][NS];  // per wave: its K-slice's partial of 16 rows x 8 streams
+  alignas(16) float red[SWAV][16][2 * NS];   // per wave: its K-slice's partial of 16 rows x 16 columns
   alignas(16) float q[NS][2][HDIM];
   alignas(16) float knew[NS][HDIM];
   alignas(16) float vnew[NS][HDIM];
   float wpart[SWAV][2][HDIM + 2];       // backbone attention: per wave (acc, m, l) of each head
   float xres[NS][32];                   // the workgroup's 32 rows of each stream's residual x ...
   float h1res[NS][32];                  // ... and of h1
+  float xres1[NS][32];                  // the same of position 1 in the two-column pass
+  float h1res1[NS][32];
   alignas(16) float comb[HID];          // CP frame: running combine of this workgroup's stream
   const bf16_t* embp[16];
   int tok[NS][16];
@@ -266,7 +274,7 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
 
   // projection inputs start at zero: a stream that computes nothing keeps finite columns
   for (int i = threadIdx.x; i < (int)(sizeof(s.xb) / 16); i += STHR)
-    reinterpret_cast<u32x4*>(&s.xb[0][0][0])[i] = u32x4{0u, 0u, 0u, 0u};
+    reinterpret_cast<u32x4*>(&s.xb[0])[i] = u32x4{0u, 0u, 0u, 0u};
   if (cp && (int)threadIdx.x < a.n_groups) s.embp[threadIdx.x] = a.cp_embs[threadIdx.x];
   __syncthreads();
 
@@ -341,18 +349,29 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
       y[2 * k + 1] = (float)(((A)xv[2 * k + 1] * r) * (A)bfhi(gp[k]));
     }
   };
-  // projection input of this wave's stream: element e of piece p at xb[p][wv][e]
-  auto put_pair = [&](int e, float v0, float v1) {
+  // projection input column n: elements e, e + 1 of its three pieces
+  auto put_pair_n = [&](int n, int e, float v0, float v1) {
     uint32_t h, m, l;
     split3x2(v0, v1, h, m, l);
-    *reinterpret_cast<uint32_t*>(&s.xb[0][wv][e]) = h;
-    *reinterpret_cast<uint32_t*>(&s.xb[1][wv][e]) = m;
-    *reinterpret_cast<uint32_t*>(&s.xb[2][wv][e]) = l;
+    *reinterpret_cast<uint32_t*>(&s.xb[n * KP + e]) = h;
+    *reinterpret_cast<uint32_t*>(&s.xb[XPS + n * KP + e]) = m;
+    *reinterpret_cast<uint32_t*>(&s.xb[2 * XPS + n * KP + e]) = l;
   };
-  auto put_vec = [&](const float (&y)[16]) {
+  // element e alone
+  auto put_one_n = [&](int n, int e, float v) {
+    uint32_t h, m, l;
+    split3x2(v, 0.0f, h, m, l);
+    s.xb[n * KP + e] = (bf16_t)h;
+    s.xb[XPS + n * KP + e] = (bf16_t)m;
+    s.xb[2 * XPS + n * KP + e] = (bf16_t)l;
+  };
+  // this wave's stream (column wv)
+  auto put_pair = [&](int e, float v0, float v1) { put_pair_n(wv, e, v0, v1); };
+  auto put_vec_n = [&](int n, const float (&y)[16]) {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) put_pair(2 * (lane + 64 * k), y[2 * k], y[2 * k + 1]);
+    for (int k = 0; k < 8; ++k) put_pair_n(n, 2 * (lane + 64 * k), y[2 * k], y[2 * k + 1]);
   };
+  auto put_vec = [&](const float (&y)[16]) { put_vec_n(wv, y); };
   // the workgroup's 32 rows 32 li + m of a lane-distributed vector: lanes 16 (li & 3) .. + 15
   // hold them at k = li >> 2
   auto keep_rows = [&](float* dst, const float (&xv)[16]) {
@@ -371,7 +390,7 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
   // input of layer 0 at position pi; the code-predictor frame's combine accumulates the inputs
   // of positions 1.. in the stream's own workgroup (bf16 rounding after each add, in the order
   // emb_bb[g0] + emb_0[t_0] + ...; generator.py:356-362)
-  auto prep_input0 = [&](int pi) {
+  auto prep_input0 = [&](int pi, int n, float* keep) {
     load_gains(lw(LW, 0, W_LNIN));
     float xv[16];
     if (cp && pi == 0) {
@@ -389,7 +408,7 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) { const uint32_t w = p[lane + 64 * k]; xv[2 * k] = bflo(w); xv[2 * k + 1] = bfhi(w); }
     }
-    keep_rows(s.xres[wv], xv);
+    keep_rows(keep, xv);
     if (cp && pi >= 1 && wg == wv) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
@@ -401,7 +420,7 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
     }
     float y[16];
     normed(xv, y);
-    put_vec(y);
+    put_vec_n(n, y);
   };
   // q/k norm, RoPE and the KV write of layer `layer` at cache slot pos. The lane holds channels
   // c = lane and c + 64 (the rotate_half partners) of q head 0, q head 1, k and v.
@@ -496,9 +515,10 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
     put_pair(128 * h + dq + 2, o4[2] * rz, o4[3] * rz);
   };
   // AR1: h1 = x + the sum of the 8 XCD O partials, rows 32 li .. + 31 of this stream
-  auto ar1 = [&](int lp) {
-    const int par = lp & 1, r2 = 2 * (lane & 15);
-    const float r0 = s.xres[wv][r2], r1 = s.xres[wv][r2 + 1];
+  // (lp: the layer pass whose tags are used, par: the buffer, xr: the residual rows)
+  auto ar1 = [&](int lp, int par, const float* xr) {
+    const int r2 = 2 * (lane & 15);
+    const float r0 = xr[r2], r1 = xr[r2 + 1];
     double s0, s1;
     poll_sum8s(P, &ws->opart[par][0][wv][32 * li], tag_of(lp, T_OPART), s0, s1);
     if (kv_pending) {
@@ -512,9 +532,9 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
       pub_local2(&ws->h1[xcd][par][wv][32 * li + r2], (float)((double)r0 + s0), (float)((double)r1 + s1), tag_of(lp, T_H1));
   };
   // AR2: x' = h1 + the sum of the 8 XCD down partials (bf16 residual in the backbone)
-  auto ar2 = [&](int lp) {
-    const int par = lp & 1, r2 = 2 * (lane & 15);
-    const float r0 = s.h1res[wv][r2], r1 = s.h1res[wv][r2 + 1];
+  auto ar2 = [&](int lp, int par, const float* hr) {
+    const int r2 = 2 * (lane & 15);
+    const float r0 = hr[r2], r1 = hr[r2 + 1];
     double s0, s1;
     poll_sum8s(P, &ws->dpart[par][0][wv][32 * li], tag_of(lp, T_DPART), s0, s1);
     if (lane < 16) {
@@ -621,14 +641,14 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
   };
   // a gathered 1024-vector (h1 or the residual after the down projection): its norm into the
   // projection input, the workgroup's rows kept in `keep`
-  auto cp_prep_vec = [&](const uint64_t* base, uint32_t tag, const bf16_t* gains, float* keep, auto&& issue) SH_INLINE {
+  auto cp_prep_vec = [&](const uint64_t* base, uint32_t tag, const bf16_t* gains, float* keep, int n, auto&& issue) SH_INLINE {
     load_gains(gains);
     float xv[16], y[16];
     gather1024(P, base, tag, xv);
     issue();
     keep_rows(keep, xv);
     normed(xv, y);
-    put_vec(y);
+    put_vec_n(n, y);
   };
   auto cp_prep_down = [&](int lp, auto&& issue) SH_INLINE {
     float v[6];
@@ -638,10 +658,10 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
 #pragma unroll
     for (int k = 0; k < 3; ++k) put_pair(2 * (lane + 64 * k), v[2 * k], v[2 * k + 1]);
   };
-  auto cp_prep_final = [&](int lp, auto&& issue) SH_INLINE {
+  auto cp_prep_final = [&](int lp, int par, auto&& issue) SH_INLINE {
     load_gains(a.final_norm);
     float xv[16];
-    gather1024(P, &ws->xl[xcd][lp & 1][wv][0], tag_of(lp, T_XL), xv);
+    gather1024(P, &ws->xl[xcd][par][wv][0], tag_of(lp, T_XL), xv);
     issue();
     float y[16];
     normed(xv, y);
@@ -657,6 +677,112 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) y[j] = rbf(y[j]);
     put_vec(y);
+  };
+
+  // ---- two-column pass of the code-predictor frame -------------------------------------------
+  // Positions 0 and 1 of every stream (generator.py:318-344 runs them as a 2-token prefill) share
+  // one pass over the weights: both inputs are known at launch (bf16(h) and emb_bb[g0]) and
+  // position 1's layer l attends to position 0's layer-l entry and its own. Column wv of the
+  // projection inputs carries position 0, column NS + wv position 1. Both columns of layer l
+  // publish with layer pass l's tags, column c into buffer parity (l & 1) ^ c, so that one poll
+  // covers both (by the exchange chain, every reader of a buffer is done before the next step's
+  // writers reach it). Position 0's last layer only writes its K/V entry.
+  auto dpar = [&](int layer, int c) { return (layer & 1) ^ c; };
+  // q/k norm + RoPE and the KV write of both positions, then position 1's attention over the two
+  // entries, in registers (lane: channels c = lane and c + 64 of each head block); position 0's
+  // attention output is its own v (one entry, weight exactly 1)
+  auto duo_prep_att = [&](int layer, auto&& issue) SH_INLINE {
+    load_qk(layer, 0);
+    float rc1[2], rsn1[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      rc1[j] = ldbf(a.cos_t + HDIM + lane + 64 * j);
+      rsn1[j] = ldbf(a.sin_t + HDIM + lane + 64 * j);
+    }
+    float v[16];   // position c: v[8 c + 2 b + {0, 1}] = channels c, c + 64 of block b (q0, q1, k, v)
+    {
+      const uint32_t o0 = ws_off(P, &ws->qkv[xcd][dpar(layer, 0)][wv][0]);
+      const uint32_t o1 = ws_off(P, &ws->qkv[xcd][dpar(layer, 1)][wv][0]);
+      poll_regs<8>(P, LROWS, tag_of(layer, T_QKV), v, [o0, o1](int i) {
+        return i < LROWS / 2 ? o0 + 16u * (uint32_t)i : o1 + 16u * (uint32_t)(i - LROWS / 2);
+      });
+    }
+    issue();
+    // norm statistics: position 0's k; position 1's q0, q1, k
+    float ss[4];
+    ss[0] = fmaf(v[4], v[4], v[5] * v[5]);
+#pragma unroll
+    for (int h = 0; h < 3; ++h) ss[1 + h] = fmaf(v[8 + 2 * h], v[8 + 2 * h], v[9 + 2 * h] * v[9 + 2 * h]);
+    group_sum_n<64>(ss);
+    float k0l, k0h;
+    {
+      const float r = rsqrt_a(ss[0] / (float)HDIM + (float)EPSD);
+      const float nl = (v[4] * r) * kn[0], nh = (v[5] * r) * kn[1];
+      k0l = nl * rc[0] - nh * rsn[0];
+      k0h = nl * rsn[1] + nh * rc[1];
+    }
+    float outl[3], outh[3];
+#pragma unroll
+    for (int h = 0; h < 3; ++h) {
+      const float r = rsqrt_a(ss[1 + h] / (float)HDIM + (float)EPSD);
+      const float gl = h < 2 ? qn[0] : kn[0], gh = h < 2 ? qn[1] : kn[1];
+      const float nl = (v[8 + 2 * h] * r) * gl, nh = (v[9 + 2 * h] * r) * gh;
+      outl[h] = nl * rc1[0] - nh * rsn1[0];
+      outh[h] = nl * rsn1[1] + nh * rc1[1];
+    }
+    const int c = lane;
+    if (li == 0) {
+      const size_t e0 = (((size_t)layer * NKVH + xcd) * (size_t)a.max_seq) * HDIM + c;
+      float* kc = reinterpret_cast<float*>(IO->kc) + e0;
+      float* vc = reinterpret_cast<float*>(IO->vc) + e0;
+      gput(kc, k0l); gput(kc + 64, k0h);
+      gput(vc, v[6]); gput(vc + 64, v[7]);
+      gput(kc + HDIM, outl[2]); gput(kc + HDIM + 64, outh[2]);
+      gput(vc + HDIM, v[14]); gput(vc + HDIM + 64, v[15]);
+      kv_pending = true;   // ordered before this wave's next slot publish (ar1)
+    }
+    // position 1: scores of heads 0, 1 against positions 0, 1
+    float d[4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      d[2 * h] = fmaf(outl[h], k0l, outh[h] * k0h);
+      d[2 * h + 1] = fmaf(outl[h], outl[2], outh[h] * outh[2]);
+    }
+    group_sum_n<64>(d);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float s0 = d[2 * h] * a.scale, s1 = d[2 * h + 1] * a.scale;
+      const float M = fmaxf(s0, s1);
+      const float p0 = __expf(s0 - M), p1 = __expf(s1 - M);
+      const float rz = rcp_f(p0 + p1);
+      put_one_n(NS + wv, 128 * h + c, fmaf(p1, v[14], p0 * v[6]) * rz);
+      put_one_n(NS + wv, 128 * h + c + 64, fmaf(p1, v[15], p0 * v[7]) * rz);
+      put_one_n(wv, 128 * h + c, v[6]);
+      put_one_n(wv, 128 * h + c + 64, v[7]);
+    }
+  };
+  // the SwiGLU outputs of both positions (of position 1 alone after the last layer's QKV)
+  auto duo_prep_down = [&](int layer, bool both, auto&& issue) SH_INLINE {
+    const uint32_t o0 = ws_off(P, &ws->inter[xcd][dpar(layer, 0)][wv][0]);
+    const uint32_t o1 = ws_off(P, &ws->inter[xcd][dpar(layer, 1)][wv][0]);
+    if (both) {
+      float v[12];
+      poll_regs<6>(P, XI, tag_of(layer, T_INTER), v, [o0, o1](int i) {
+        return i < XI / 2 ? o0 + 16u * (uint32_t)i : o1 + 16u * (uint32_t)(i - XI / 2);
+      });
+      issue();
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        put_pair_n(wv, 2 * (lane + 64 * k), v[2 * k], v[2 * k + 1]);
+        put_pair_n(NS + wv, 2 * (lane + 64 * k), v[6 + 2 * k], v[7 + 2 * k]);
+      }
+    } else {
+      float v[6];
+      poll_regs<3>(P, XI / 2, tag_of(layer, T_INTER), v, [o1](int i) { return o1 + 16u * (uint32_t)i; });
+      issue();
+#pragma unroll
+      for (int k = 0; k < 3; ++k) put_pair_n(NS + wv, 2 * (lane + 64 * k), v[2 * k], v[2 * k + 1]);
+    }
   };
 
   // ---- attention ---------------------------------------------------------------------------
@@ -985,8 +1111,8 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       const int k = 32 * (kb0 + j) + 8 * kg;
-      const u32x4 b1 = *reinterpret_cast<const u32x4*>(&s.xb[n >> 3][n & 7][k]);
-      const u32x4 b2 = *reinterpret_cast<const u32x4*>(&s.xb[2][n & 7][k]);
+      const u32x4 b1 = *reinterpret_cast<const u32x4*>(&s.xb[(n >> 3) * XPS + (n & 7) * KP + k]);
+      const u32x4 b2 = *reinterpret_cast<const u32x4*>(&s.xb[2 * XPS + (n & 7) * KP + k]);
       c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(tp[j]), as_bf8(b1), c1, 0, 0, 0);
       c2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(tp[j]), as_bf8(b2), c2, 0, 0, 0);
     }
@@ -995,6 +1121,25 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
       const float v = (c1[e] + ror8(c1[e])) + c2[e];
       if (n < 8) s.red[wv][4 * kg + e][n] = v;
     }
+  };
+  // The same over all 16 input columns (the two-column pass): one MFMA per piece, and the partial
+  // of (row, column n) is (hi + mid) + lo, as above.
+  auto gemv2 = [&](const auto& tp, int kb0) {
+    constexpr int NB = sizeof(tp) / sizeof(u32x4);
+    const int n = lane & 15, kg = lane >> 4;
+    f32x4 c0 = {0.0f, 0.0f, 0.0f, 0.0f}, c1 = {0.0f, 0.0f, 0.0f, 0.0f}, c2 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int k = 32 * (kb0 + j) + 8 * kg;
+      const u32x4 b0 = *reinterpret_cast<const u32x4*>(&s.xb[n * KP + k]);
+      const u32x4 b1 = *reinterpret_cast<const u32x4*>(&s.xb[XPS + n * KP + k]);
+      const u32x4 b2 = *reinterpret_cast<const u32x4*>(&s.xb[2 * XPS + n * KP + k]);
+      c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(tp[j]), as_bf8(b0), c0, 0, 0, 0);
+      c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(tp[j]), as_bf8(b1), c1, 0, 0, 0);
+      c2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf8(tp[j]), as_bf8(b2), c2, 0, 0, 0);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s.red[wv][4 * kg + e][n] = (c0[e] + c1[e]) + c2[e];
   };
   // sum of the partials of waves w0 .. w0 + nw - 1 (fixed order)
   auto red_sum = [&](int w0, int nw, int r, int st) {
@@ -1086,18 +1231,147 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
   TD td;
   TKV tkv;
   load_q(tq, 0);
-  if (me) prep_input0(0);
-  for (int pi = 0; pi < a.n_pos; ++pi) {
+  // the code-predictor frame runs positions 0 and 1 as one two-column pass, then position 1's head
+  const bool duo = cp && a.n_pos >= 2;
+  int npass = 0;   // layer passes begun: the first one's waits run under the entry cap
+  auto pass_begin = [&]() {
+    if (npass == 1) P.ec.spin_cap = a.spin_cap;
+    ++npass;
+  };
+  if (me) {
+    prep_input0(0, wv, s.xres[wv]);
+    if (duo) prep_input0(1, NS + wv, s.xres1[wv]);
+  }
+  for (int pi = duo ? 1 : 0; pi < a.n_pos; ++pi) {
     const int pos = BB ? IO->pos : pi;
     const bool last_pos = pi == a.n_pos - 1;
     const bool head = has_head(pi);
-    for (int layer = 0; layer < NL; ++layer) {
+    if constexpr (!BB) {
+      if (duo && pi == 1) {
+        for (int layer = 0; layer < NL; ++layer) {
+          lane = opaque(lane);
+          tid = opaque(tid);
+          const bool last_layer = layer == NL - 1;
+          pass_begin();
+          // ---- QKV, both positions
+          step_barrier();
+          stamp(0);
+          gemv2(tq.p, 4 * wv);
+          step_barrier();
+          stamp(1);
+          if (tid < 16 * 2 * NS) {
+            const int n = tid >> 4, st = n & (NS - 1), c = n / NS, r = tid & 15;
+            const float v = red_sum(0, SWAV, r, n);
+            const int lr = 16 * li + r, cc = lr & 127;
+            if (is_live(st))
+              pub_local(&ws->qkv[xcd][dpar(layer, c)][st][(lr & ~127) + 2 * (cc & 63) + (cc >> 6)], v, tag_of(layer, T_QKV));
+          }
+          stamp(14);
+          {
+            auto iss = [&]() SH_INLINE { load_o(to, layer); };
+            if (me) duo_prep_att(layer, iss);
+            else iss();
+          }
+          stamp(2 + wv);
+          ++nstep;
+          // ---- O projection (position 0's stops after its last QKV)
+          step_barrier();
+          stamp(0);
+          gemv2(to.p, 2 * (wv & 3));
+          step_barrier();
+          stamp(1);
+          {
+            const int n = tid >> 5, st = n & (NS - 1), c = n / NS, tile = (tid >> 4) & 1, r = tid & 15;
+            const float v = red_sum(4 * tile, 4, r, n);
+            if (is_live(st) && (c == 1 || !last_layer))
+              pub_cross(&ws->opart[dpar(layer, c)][xcd][st][32 * li + 16 * tile + r], v, tag_of(layer, T_OPART));
+          }
+          stamp(14);
+          {
+            auto iss = [&]() SH_INLINE { load_g(tgu, layer); };
+            if (me) {
+              // both columns' sums published before either gather
+              if (!last_layer) ar1(layer, dpar(layer, 0), s.xres[wv]);
+              ar1(layer, dpar(layer, 1), s.xres1[wv]);
+              if (!last_layer)
+                cp_prep_vec(&ws->h1[xcd][dpar(layer, 0)][wv][0], tag_of(layer, T_H1), lw(LW, layer, W_LNPOST), s.h1res[wv],
+                            wv, []() SH_INLINE {});
+              cp_prep_vec(&ws->h1[xcd][dpar(layer, 1)][wv][0], tag_of(layer, T_H1), lw(LW, layer, W_LNPOST), s.h1res1[wv],
+                          NS + wv, iss);
+            } else {
+              iss();
+            }
+          }
+          stamp(2 + wv);
+          ++nstep;
+          // ---- gate / up + SiLU
+          step_barrier();
+          stamp(0);
+          gemv2(tgu.p, 8 * (wv & 3));
+          step_barrier();
+          stamp(1);
+          if (tid < 12 * 2 * NS) {
+            const int n = tid / 12, st = n & (NS - 1), c = n / NS, r = tid - 12 * n;
+            const float gt = red_sum(0, 4, r, n), up = red_sum(4, 4, r, n);
+            const float act = gt / (1.0f + __expf(-gt)) * up;
+            if (is_live(st) && (c == 1 || !last_layer))
+              pub_local(&ws->inter[xcd][dpar(layer, c)][st][12 * li + r], act, tag_of(layer, T_INTER));
+          }
+          stamp(14);
+          {
+            auto iss = [&]() SH_INLINE { load_d(td, layer); };
+            if (me) duo_prep_down(layer, !last_layer, iss);
+            else iss();
+          }
+          stamp(2 + wv);
+          ++nstep;
+          // ---- down projection
+          step_barrier();
+          stamp(0);
+          gemv2(td.p, 3 * (wv & 3));
+          step_barrier();
+          stamp(1);
+          {
+            const int n = tid >> 5, st = n & (NS - 1), c = n / NS, tile = (tid >> 4) & 1, r = tid & 15;
+            const float v = red_sum(4 * tile, 4, r, n);
+            if (is_live(st) && (c == 1 || !last_layer))
+              pub_cross(&ws->dpart[dpar(layer, c)][xcd][st][32 * li + 16 * tile + r], v, tag_of(layer, T_DPART));
+          }
+          stamp(14);
+          {
+            // next: both positions' next-layer inputs, or position 1's final norm (the head's input)
+            auto iss = [&]() SH_INLINE {
+              if (!last_layer) load_q(tq, layer + 1);
+              else load_h(tq, head_w(1));
+            };
+            if (me) {
+              if (!last_layer) {
+                ar2(layer, dpar(layer, 0), s.h1res[wv]);
+                ar2(layer, dpar(layer, 1), s.h1res1[wv]);
+                cp_prep_vec(&ws->xl[xcd][dpar(layer, 0)][wv][0], tag_of(layer, T_XL), lw(LW, layer + 1, W_LNIN), s.xres[wv],
+                            wv, []() SH_INLINE {});
+                cp_prep_vec(&ws->xl[xcd][dpar(layer, 1)][wv][0], tag_of(layer, T_XL), lw(LW, layer + 1, W_LNIN),
+                            s.xres1[wv], NS + wv, iss);
+              } else {
+                ar2(layer, dpar(layer, 1), s.h1res1[wv]);
+                cp_prep_final(layer, dpar(layer, 1), iss);
+              }
+            } else {
+              iss();
+            }
+          }
+          stamp(2 + wv);
+          ++nstep;
+        }
+      }
+    }
+    for (int layer = 0; layer < ((!BB && duo && pi == 1) ? 0 : NL); ++layer) {
       lane = opaque(lane);
       tid = opaque(tid);
       const int lp = pi * NL + layer;
       const int par = lp & 1;
       const bool last_layer = layer == NL - 1;
-      if (lp == 1) P.ec.spin_cap = a.spin_cap;
+      pass_begin();
       // ---- QKV
       step_barrier();
       stamp(0);
@@ -1120,20 +1394,7 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
         if (me) prep_att(lp, layer, pos, iss);
         else iss();
       } else {
-        if (pi == 0 && last_layer && a.n_pos > 1) {
-          // position 0 feeds no head: of its last layer only the K/V entry is read later. The
-          // next step is position 1's layer-0 QKV; its input is prepared here.
-          auto iss = [&]() SH_INLINE { load_q(tq, 0); };
-          if (me) {
-            cp_prep_att(lp, layer, pos, iss);
-            cp_prep_input0(1, []() SH_INLINE {});
-          } else {
-            iss();
-          }
-          stamp(2 + wv);
-          ++nstep;
-          continue;
-        }
+        // (position 0 of a frame of two or more positions runs in the two-column pass above)
         auto iss = [&]() SH_INLINE { load_o(to, layer); };
         if (me) cp_prep_att(lp, layer, pos, iss);
         else iss();
@@ -1168,9 +1429,9 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
       {
         auto iss = [&]() SH_INLINE { stamp(12); load_g(tgu, layer); };
         if (me) {
-          ar1(lp);
+          ar1(lp, par, s.xres[wv]);
           stamp(11);
-          cp_prep_vec(&ws->h1[xcd][par][wv][0], tag_of(lp, T_H1), lw(LW, layer, W_LNPOST), s.h1res[wv], iss);
+          cp_prep_vec(&ws->h1[xcd][par][wv][0], tag_of(lp, T_H1), lw(LW, layer, W_LNPOST), s.h1res[wv], wv, iss);
         } else {
           iss();
         }
@@ -1214,8 +1475,8 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
           // the next layer's QKV tile goes out after the gather's last poll
           auto iss = [&]() SH_INLINE { load_q(tq, layer + 1); };
           if (me) {
-            ar2(lp);
-            cp_prep_vec(&ws->xl[xcd][par][wv][0], tag_of(lp, T_XL), lw(LW, layer + 1, W_LNIN), s.xres[wv], iss);
+            ar2(lp, par, s.h1res[wv]);
+            cp_prep_vec(&ws->xl[xcd][par][wv][0], tag_of(lp, T_XL), lw(LW, layer + 1, W_LNIN), s.xres[wv], wv, iss);
           } else {
             iss();
           }
@@ -1223,8 +1484,8 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
           if (head) load_h(tq, head_w(pi));
           else if (!last_pos) load_q(tq, 0);
           if (me) {
-            if (head || last_pos) { ar2(lp); prep_final(lp); }
-            else prep_input0(pi + 1);
+            if (head || last_pos) { ar2(lp, par, s.h1res[wv]); prep_final(lp); }
+            else prep_input0(pi + 1, wv, s.xres[wv]);
           }
         }
       } else {
@@ -1237,11 +1498,11 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
         };
         if (me) {
           if (!last_layer) {
-            ar2(lp);
-            cp_prep_vec(&ws->xl[xcd][par][wv][0], tag_of(lp, T_XL), lw(LW, layer + 1, W_LNIN), s.xres[wv], iss);
+            ar2(lp, par, s.h1res[wv]);
+            cp_prep_vec(&ws->xl[xcd][par][wv][0], tag_of(lp, T_XL), lw(LW, layer + 1, W_LNIN), s.xres[wv], wv, iss);
           } else if (head || last_pos) {
-            ar2(lp);
-            cp_prep_final(lp, iss);
+            ar2(lp, par, s.h1res[wv]);
+            cp_prep_final(lp, par, iss);
           } else {
             cp_prep_input0(pi + 1, iss);
           }
@@ -1315,7 +1576,7 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
           if (lane == 0) s.tok[wv][pi - 1] = tok;
           __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
           if constexpr (BB) {
-            if (!last_pos) prep_input0(pi + 1);
+            if (!last_pos) prep_input0(pi + 1, wv, s.xres[wv]);
           }
         }
         if constexpr (!BB) {

@@ -341,6 +341,45 @@ def test_cp_frames_streams_match_batch1(pkg, n, sample, mode):
     print(f"cp frames {n} streams: first stream groups {toks[0, 1:6].tolist()}...", flush=True)
 
 
+@pytest.mark.parametrize("n_cp_layers,n_groups", [(1, 1), (1, 15), (2, 2), (3, 15)])
+def test_shared_cp_two_column_pass(pkg, n_cp_layers, n_groups):
+    """The weight-shared code-predictor frame runs positions 0 and 1 of every stream as one
+    two-column pass (16 input columns: 8 streams x 2 positions); the second column publishes into
+    the exchange buffers of the other parity. Odd and even layer counts, a one-layer pass (its
+    only layer is position 0's last, which writes only the K/V entry) and frames of 1, 2 and 15
+    groups (a frame of 1 group ends with the pass's head). 5 streams, greedy and sampled: ids and
+    combine against the oracle (kernel policy) from the same hidden, under the last-bit rule."""
+    cfg = pkg.SyntheticConfig(n_bb_layers=1, n_cp_layers=n_cp_layers, n_groups=n_groups)
+    sd = pkg.synthetic_state_dict(seed=600 + 7 * n_cp_layers + n_groups, cfg=cfg)
+    dsd = {k: v.cuda() for k, v in sd.items()}
+    n = 5
+    dec = pkg.BatchedTTSDecoder(dsd, n, max_seq_len=16, mode="shared")
+    orc = _cp_oracle(sd, n_cp_layers)
+    g = torch.Generator().manual_seed(n_cp_layers * 100 + n_groups)
+    i32 = dict(dtype=torch.int32, device="cuda")
+    for sample in (False, True):
+        hid = torch.randn(n, 1024, generator=g).cuda()
+        g0 = torch.randint(0, 2048, (n,), generator=g, dtype=torch.int32).cuda()
+        text = torch.randn(n, 1024, generator=g).to(torch.bfloat16).cuda()
+        toks = torch.full((n, n_groups + 1), -1, **i32)
+        comb = torch.empty(n, 1024, dtype=torch.bfloat16, device="cuda")
+        kw = dict(do_sample=sample, temperature=0.8, top_k=30, seed=21, frame_step=3)
+        print(f"shared cp frame, {n_cp_layers} layers, {n_groups} groups, sample={sample}: launching", flush=True)
+        dec.cp_frames(hid, g0, text, toks, comb, **kw)
+        torch.cuda.synchronize()
+        dec.check_error()
+        for s in range(n):
+            got = toks[s].tolist()
+            ids = [got[0]] + orc.cp_frame(hid[s].cpu(), got[0], sample, kw["temperature"], kw["top_k"],
+                                          seed=kw["seed"] + s, frame_step=kw["frame_step"])
+            assert got[0] == int(g0[s])
+            if got != ids:
+                _explain_cp_difference(orc, hid[s], got[0], ids, got, sample, kw, kw["seed"] + s, f"stream {s}")
+                continue
+            assert torch.equal(comb[s].cpu(), orc.combine(ids, text[s].cpu())), f"stream {s}: combine vs oracle"
+        print(f"  stream 0: {toks[0, 1:].tolist()[:6]}", flush=True)
+
+
 @pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("sample", [False, True], ids=["greedy", "sampled"])
 def test_batched_generate_matches_single_stream(pkg, sample, mode):
