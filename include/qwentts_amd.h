@@ -97,7 +97,7 @@ hipError_t launch_tts_decode_with_embedding(
  * every later exchange, so nothing needs clearing between calls). The library orders its own
  * launches on a device, but calls that are made to overlap on one GPU (other processes,
  * graphs replayed concurrently on several streams) race on the array. */
-#define QTTS_STATIC_SCRATCH_BYTES 995584u
+#define QTTS_STATIC_SCRATCH_BYTES 1261824u
 hipError_t launch_tts_decode_with_embedding_static(
     const void* input_embedding, const TTSLayerWeights* layer_weights,
     const void* final_norm_weight, const void* cos_table, const void* sin_table,

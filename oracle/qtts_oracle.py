@@ -148,8 +148,8 @@ def rope_apply(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.T
 
 EPS_F32 = float(torch.tensor(1e-6, dtype=torch.float32))   # the reference's 1e-6f
 SCALE_F32 = float(torch.tensor(1.0 / math.sqrt(128.0), dtype=torch.float32))  # attn_scale (f32)
-MAX_CHUNKS = 8      # attention chunks per KV head in the kernels
-SUB_BB, SUB_CP = 64, 2   # chunking granularity (positions per chunk before the 8-chunk cap)
+MAX_CHUNKS = 16     # attention chunks per KV head in the kernels
+SUB_BB, SUB_CP = 64, 2   # chunking granularity (positions per chunk before the chunk cap)
 PASS_BB, PASS_CP = 64, 16  # contexts up to this length are attended whole by every workgroup
 
 
@@ -188,7 +188,7 @@ def split_attention(q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, scale: fl
     q [h, d], K/V [h, L, d] (f64). The sequence is cut as ``chunking(L, sub)``; chunk c keeps
     its max m_c, its sum l_c = sum exp(s - m_c) and its unnormalised output acc_c; the merge
     rescales by exp(m_c - M) with M the global max (the LDS split-K combine of
-    fused_decode_tts.cu:282-385, here over up to 8 chunks): out = (sum_c acc_c w_c) * (1 / Z),
+    fused_decode_tts.cu:282-385, here over up to MAX_CHUNKS chunks): out = (sum_c acc_c w_c) * (1 / Z),
     Z = sum_c l_c w_c. ``R`` is applied where the kernels store f32: the scores, l_c, acc_c and
     the merged output.
     """

@@ -29,7 +29,7 @@ constexpr int NMATH = 4;          // math waves per workgroup
 constexpr int NTHR = 64 * (NMATH + 1);  // + 1 poller wave
 constexpr int LROWS = 512;        // q(256) + k(128) + v(128) rows owned by one XCD
 constexpr int XI = INTER / NXCD;  // 384 intermediate rows per XCD
-constexpr int MAXC = 8;           // max attention chunks per KV head
+constexpr int MAXC = 16;          // max attention chunks per KV head (2 MAXC units: every workgroup of an XCD)
 constexpr int APH = 130;          // attention partial of one (chunk, head): acc[128], m, l
 constexpr int APS = 2 * APH;      // partial storage per chunk (both heads)
 constexpr int SUBP = 64;          // positions per prefetched attention sub-block

@@ -172,7 +172,7 @@ struct Lds {
   alignas(16) float xres_1[HID];   // two-column pass: position 1's residual stream
   alignas(16) float h1res_1[HID];
   alignas(16) float comb[HID];   // code-predictor frame (workgroup 0): running embedding combine
-  alignas(16) float stage[MAXC * APS > MAXV ? MAXC * APS : MAXV];
+  alignas(16) float stage[MAXV];
   uint32_t pen_bits[MAXV / 32];
   int tok[32];
   const bf16_t* embp[16];   // code-predictor embedding tables, loaded once per launch
@@ -721,31 +721,33 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
     }
   };
   // ---- poller: merge the 2C attention partials (chunk c, head h) of the XCD's KV head into
-  // s.attn (the split-K combine of fused_decode_tts.cu:282-385). First every unit's (m, l) pair,
-  // one 16-byte slot pair per unit (lane (h, c); lanes past C re-read chunk C - 1): per head the
-  // chunk weights w_c = exp(m_c - M), M = max_c m_c, and Z = sum_c l_c w_c, over the 8 chunk
-  // lanes with three exchanges. Polling only these 2C pairs keeps the wait light; the 128-value
-  // accumulators are then read once (re-reading only slots not yet landed), lane (h, j) taking
-  // dims 4j .. 4j + 3 of every chunk of head h, and merged in f64:
-  // f32((sum_c acc_c w_c) * (1 / Z)).
+  // s.attn (the split-K combine of fused_decode_tts.cu:282-385). Every unit's (m, l) pair, one
+  // 16-byte slot pair per unit (lane (h, c); lanes past C re-read chunk C - 1): per head the
+  // chunk weights w_c = exp(m_c - M), M = max_c m_c, and Z = sum_c l_c w_c, over the 16 chunk
+  // lanes with four exchanges. Lane (h, j) takes dims 4j .. 4j + 3 of every chunk of head h and
+  // merges them in f64: f32((sum_c acc_c w_c) * (1 / Z)). The (m, l) pairs and the first HC
+  // chunks' accumulators come in one poll; the accumulators of chunks HC.. (contexts beyond
+  // HC chunks) in a second read, once the first has seen every unit's (m, l) (they have about
+  // landed by then; the registers of one poll of all 16 would spill).
   auto prep_o = [&](int lp, int C) {
+    constexpr int HC = MAXC / 2;
     const int par = lp & 1;
     const uint32_t o = ws_off(P, ws->attp[xcd][par]);
     const uint32_t tg = tag_of(lp, T_ATT);
     const int h = lane >> 5, c = lane & 31;
-    // one poll of every pair this lane needs: k = 0 the (m, l) pair of unit (chunk c, head h)
-    // (lanes past C re-read chunk C - 1), k = 1 + 2 cc + e the acc dims 4 (lane & 31) + 2 e, +1
-    // of chunk cc, head h
-    float v[2 + 4 * MAXC];
-    poll_regs<1 + 2 * MAXC>(P, 64 * (1 + 2 * C), tg, v, [o, C](int i) {
+    // k = 0 the (m, l) pair of unit (chunk c, head h), k = 1 + 2 cc + e the acc dims
+    // 4 (lane & 31) + 2 e, +1 of chunk cc, head h
+    auto off = [o, C](int i, int cbase) {
       const uint32_t k = (uint32_t)i >> 6, l = (uint32_t)i & 63u;
       if (k == 0u) {
         const int cc = min((int)(l & 31u), C - 1);
         return o + 8u * (uint32_t)((2 * cc + (int)(l >> 5)) * APH + 128);
       }
-      const uint32_t kk = k - 1u;
-      return o + 8u * ((2u * (kk >> 1) + (l >> 5)) * (uint32_t)APH + 4u * (l & 31u) + 2u * (kk & 1u));
-    });
+      const uint32_t kk = k - 1u, cc = (uint32_t)cbase + (kk >> 1);
+      return o + 8u * ((2u * cc + (l >> 5)) * (uint32_t)APH + 4u * (l & 31u) + 2u * (kk & 1u));
+    };
+    float v[2 + 4 * HC];
+    poll_regs<1 + 2 * HC>(P, 64 * (1 + 2 * min(C, HC)), tg, v, [off](int i) { return off(i, 0); });
     {
       const bool ok = c < C;
       const float mc = ok ? v[0] : -INFINITY;
@@ -754,22 +756,36 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
       M = fmaxf(M, xlane_f<0>(M));
       M = fmaxf(M, xlane_f<1>(M));
       M = fmaxf(M, xlane_f<2>(M));
+      M = fmaxf(M, xlane_f<3>(M));
       const double w = ok ? exp((double)mc - (double)M) : 0.0;
       double Z = (double)lc * w;
       Z += xlane_d<0>(Z);
       Z += xlane_d<1>(Z);
       Z += xlane_d<2>(Z);
+      Z += xlane_d<3>(Z);
       if (c < MAXC) s.wts[h][c] = w;
       if (c == 0) s.wts[h][MAXC] = 1.0 / Z;
     }
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");   // the weights written above
     double a4[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-    for (int cc = 0; cc < MAXC; ++cc) {
+    for (int cc = 0; cc < HC; ++cc) {
       if (cc < C) {   // chunks past C were not polled (their registers hold no value)
         const double w = s.wts[h][cc];
 #pragma unroll
         for (int j = 0; j < 4; ++j) a4[j] = fma((double)v[2 + 4 * cc + j], w, a4[j]);
+      }
+    }
+    if (C > HC) {
+      float u[4 * HC];
+      read_pairs<2 * HC>(P, 64 * 2 * (C - HC), tg, u, [off](int i) { return off(i + 64, HC); });
+#pragma unroll
+      for (int cc = 0; cc < HC; ++cc) {
+        if (HC + cc < C) {
+          const double w = s.wts[h][HC + cc];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) a4[j] = fma((double)u[4 * cc + j], w, a4[j]);
+        }
       }
     }
     const double rz = s.wts[h][MAXC];

@@ -84,7 +84,7 @@ def test_backbone_long_context_2048(full, pkg):
     sd, dsd, tw = full
     n = 4
     orc = DecoderOracle(tw.bb_layers[:n], tw.bb_norm, 2048, "backbone", "kernel")
-    # 4-layer model so the oracle stays fast; exercises 8 chunks x 4 sub-blocks of attention
+    # 4-layer model so the oracle stays fast; exercises 16 chunks x 2 sub-blocks of attention
     sd4 = {k: v for k, v in dsd.items() if not k.startswith("talker.model.layers.") or int(k.split(".")[3]) < n}
     bbn = pkg.TTSMegakernelGenerator(model=sd4, max_seq_len=2048)
     k, v = _rand_kv(n, 2047, 31, torch.bfloat16)
@@ -103,8 +103,8 @@ def test_backbone_long_context_2048(full, pkg):
 @pytest.mark.parametrize("L", [65, 577, 4096])
 def test_backbone_context_edges(full, pkg, L):
     """Attended lengths at the edges of the attention paths: just past the one-pass local path (65:
-    2 chunks of 33), a ragged chunk split (577: 8 chunks of 73, a full and a 9-position sub-block),
-    and the maximum context (4096 = max_seq_len: 8 chunks of 512, 8 sub-blocks each)."""
+    2 chunks of 33), a ragged chunk split (577: 10 chunks of 58, the last of 55), and the maximum
+    context (4096 = max_seq_len: 16 chunks of 256, 4 sub-blocks each)."""
     sd, dsd, tw = full
     n = 2
     orc = DecoderOracle(tw.bb_layers[:n], tw.bb_norm, L, "backbone", "kernel")

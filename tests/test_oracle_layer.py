@@ -20,7 +20,7 @@ import pytest
 import torch
 
 from oracle.qtts_oracle import (DecoderOracle, TalkerWeights, head_logits, rel_l2, split_attention, chunking,
-                                local_attention, SUB_BB, SUB_CP)
+                                local_attention, MAX_CHUNKS, SUB_BB, SUB_CP)
 
 transformers = pytest.importorskip("transformers")
 from transformers import Qwen3Config  # noqa: E402
@@ -184,7 +184,7 @@ def test_split_attention_equals_single_pass_softmax(L, sub):
     ref = torch.softmax(torch.einsum("hd,hpd->hp", q, K) * scale, -1)
     ref = torch.einsum("hp,hpd->hd", ref, V)
     C, P = chunking(L, sub)
-    assert 1 <= C <= 8 and (C - 1) * P < L <= C * P
+    assert 1 <= C <= MAX_CHUNKS and (C - 1) * P < L <= C * P
     assert rel_l2(split_attention(q, K, V, scale, sub), ref) < 1e-13
     assert rel_l2(local_attention(q, K, V, scale), ref) < 1e-13
 
