@@ -253,7 +253,7 @@ def batched_frame_bytes(lengths) -> int:
     return bb + cp
 
 
-def batched_c4(pkg, sd, frames: int = 10) -> dict:
+def batched_c4(pkg, sd, frames: int = 30) -> dict:
     """Config 4: 8 independent streams with ragged attended lengths in [128, 1024]; one frame =
     per stream one backbone step (head + greedy g0) and one code-predictor frame. Both multi-stream
     kernels are timed: the weight-shared one (the figure) and the one-stream-per-XCD one."""

@@ -100,11 +100,13 @@ def test_backbone_long_context_2048(full, pkg):
     assert e < TOL
 
 
-@pytest.mark.parametrize("L", [65, 577, 4096])
+@pytest.mark.parametrize("L", [65, 513, 577, 961, 4096])
 def test_backbone_context_edges(full, pkg, L):
     """Attended lengths at the edges of the attention paths: just past the one-pass local path (65:
-    2 chunks of 33), a ragged chunk split (577: 10 chunks of 58, the last of 55), and the maximum
-    context (4096 = max_seq_len: 16 chunks of 256, 4 sub-blocks each)."""
+    2 chunks of 33), the first context past 8 chunks (513: 9 chunks of 57, the poller's second read
+    covering one chunk), a ragged chunk split (577: 10 chunks of 58, the last of 55), the first
+    context with 16 chunks (961: 16 chunks of 61, the last of 46), and the maximum context (4096 =
+    max_seq_len: 16 chunks of 256, 4 sub-blocks each)."""
     sd, dsd, tw = full
     n = 2
     orc = DecoderOracle(tw.bb_layers[:n], tw.bb_norm, L, "backbone", "kernel")
