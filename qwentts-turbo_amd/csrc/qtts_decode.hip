@@ -259,6 +259,18 @@ __device__ __forceinline__ void load_gu(TileGU& t, const TTSLayerWeights* L, int
     t.u[2 * r + 1] = wload<BB>(lw(L, layer, W_UP) + row + 512 + 8 * lane);
   }
 }
+// Rows [R0, R1) of the wave's 3 gate/up row pairs (gate and up of each row).
+template <bool BB, int R0, int R1>
+__device__ __forceinline__ void load_gu_rows(TileGU& t, const TTSLayerWeights* L, int layer, int xcd, int li, int mw, int lane) {
+#pragma unroll
+  for (int r = R0; r < R1; ++r) {
+    const size_t row = (size_t)(XI * xcd + 12 * li + 3 * mw + r) * HID;
+    t.g[2 * r] = wload<BB>(lw(L, layer, W_GATE) + row + 8 * lane);
+    t.g[2 * r + 1] = wload<BB>(lw(L, layer, W_GATE) + row + 512 + 8 * lane);
+    t.u[2 * r] = wload<BB>(lw(L, layer, W_UP) + row + 8 * lane);
+    t.u[2 * r + 1] = wload<BB>(lw(L, layer, W_UP) + row + 512 + 8 * lane);
+  }
+}
 // One half of the gate/up tile: the gate rows (PART 0) or the up rows (PART 1).
 template <bool BB, int PART>
 __device__ __forceinline__ void load_gu_half(TileGU& t, const TTSLayerWeights* L, int layer, int xcd, int li, int mw, int lane) {
@@ -276,15 +288,23 @@ __device__ __forceinline__ void load_gu_half(TileGU& t, const TTSLayerWeights* L
 }
 // The gate/up tile is the largest (12.6 MB over the GPU) and goes out right after the O partials are
 // published, while the cross-XCD sums and then the h1 all-gather are in flight: issued whole, its HBM
-// burst lands on the cross-XCD hop. The up rows go out kGuSplitSleep x 64 cycles (~1.5 us) after the gate
-// rows, so the two hops each carry half of it (CP frame 955 -> 930 us, backbone step 491 -> 488 us;
-// 24 and 96 gave no gain, 64 and 80 the same as 48).
-constexpr int kGuSplitSleep = 48;
+// burst lands on the cross-XCD hop; deferred whole, on the all-gather. Paced instead, the two hops share
+// it. Backbone: the gate rows, then the up rows 48 x 64 cycles (~1.5 us) later (step 493 -> 489 us).
+// Code predictor: a third (one row pair) at a time, 24 x 64 cycles (~0.7 us) apart (frame 955 -> 915 us;
+// halves 48 apart gave 926 us, thirds 16 apart 950 us, quarters 16 apart 919 us).
 template <bool BB>
-__device__ __forceinline__ void load_gu_split(TileGU& t, const TTSLayerWeights* L, int layer, int xcd, int li, int mw, int lane) {
-  load_gu_half<BB, 0>(t, L, layer, xcd, li, mw, lane);
-  __builtin_amdgcn_s_sleep(kGuSplitSleep);
-  load_gu_half<BB, 1>(t, L, layer, xcd, li, mw, lane);
+__device__ __forceinline__ void load_gu_paced(TileGU& t, const TTSLayerWeights* L, int layer, int xcd, int li, int mw, int lane) {
+  if constexpr (BB) {
+    load_gu_half<BB, 0>(t, L, layer, xcd, li, mw, lane);
+    __builtin_amdgcn_s_sleep(48);
+    load_gu_half<BB, 1>(t, L, layer, xcd, li, mw, lane);
+  } else {
+    load_gu_rows<BB, 0, 1>(t, L, layer, xcd, li, mw, lane);
+    __builtin_amdgcn_s_sleep(24);
+    load_gu_rows<BB, 1, 2>(t, L, layer, xcd, li, mw, lane);
+    __builtin_amdgcn_s_sleep(24);
+    load_gu_rows<BB, 2, 3>(t, L, layer, xcd, li, mw, lane);
+  }
 }
 template <bool BB>
 __device__ __forceinline__ void load_d(TileD& t, const TTSLayerWeights* L, int layer, int xcd, int li, int mw, int lane) {
@@ -1742,14 +1762,14 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           }
           if (q.local) {
             o_stage(layer);
-            load_gu_split<BB>(tgu, LW, layer, xcd, li, mw, lane);
+            load_gu_paced<BB>(tgu, LW, layer, xcd, li, mw, lane);
           } else {
             load_o<BB>(to, LW, layer, xcd, li, mw, lane);
           }
           break;
         case S_O:
           o_stage(layer);
-          load_gu_split<BB>(tgu, LW, layer, xcd, li, mw, lane);
+          load_gu_paced<BB>(tgu, LW, layer, xcd, li, mw, lane);
           break;
         case S_GU:
           gu_stage(layer);
@@ -1787,7 +1807,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
             attention_cp_local(2, std::true_type{});
             math_o(lp - NL, li, to, Col0{});
             math_o(lp, li, to, Col1{});
-            load_gu_split<BB>(tgu, LW, layer, xcd, li, mw, lane);
+            load_gu_paced<BB>(tgu, LW, layer, xcd, li, mw, lane);
           }
           break;
         case S_GU2:
