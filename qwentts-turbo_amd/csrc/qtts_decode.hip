@@ -240,6 +240,24 @@ __device__ __forceinline__ void load_qkv(TileQKV& t, const TTSLayerWeights* L, i
     t.p[2 * r + 1] = wload<BB>(row + 512 + 8 * lane);
   }
 }
+// The QKV tile one row (two loads per lane) at a time, 12 x 64 cycles (~0.4 us) apart: issued after the
+// down partials are published (or after a code-predictor head), its 8.4 MB burst otherwise lands whole on
+// the down all-reduce's cross-XCD hop (code predictor: frame 920 -> 902 us; 8 apart 919 us, halves 32 or
+// 48 apart slower; the backbone gains nothing from it).
+template <bool BB>
+__device__ __forceinline__ void load_qkv_paced(TileQKV& t, const TTSLayerWeights* L, int layer, int xcd, int li, int mw, int lane) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int lr = 16 * li + 4 * mw + r;   // local row of the XCD's 512
+    const bf16_t* row;
+    if (lr < 256) row = lw(L, layer, W_Q) + (size_t)(256 * xcd + lr) * HID;
+    else if (lr < 384) row = lw(L, layer, W_K) + (size_t)(128 * xcd + lr - 256) * HID;
+    else row = lw(L, layer, W_V) + (size_t)(128 * xcd + lr - 384) * HID;
+    t.p[2 * r] = wload<BB>(row + 8 * lane);
+    t.p[2 * r + 1] = wload<BB>(row + 512 + 8 * lane);
+    if (r < 3) __builtin_amdgcn_s_sleep(12);
+  }
+}
 template <bool BB>
 __device__ __forceinline__ void load_o(TileO& t, const TTSLayerWeights* L, int layer, int xcd, int li, int mw, int lane) {
 #pragma unroll
@@ -1778,7 +1796,8 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
         case S_DOWN:
           down_stage(layer);
           if (!last_layer) {
-            load_qkv<BB>(tq, LW, layer + 1, xcd, li, mw, lane);
+            if constexpr (BB) load_qkv<BB>(tq, LW, layer + 1, xcd, li, mw, lane);
+            else load_qkv_paced<BB>(tq, LW, layer + 1, xcd, li, mw, lane);
           } else if (q.head) {
             int row0, nrows;
             head_rows(0, row0, nrows);
@@ -1791,7 +1810,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           break;
         case S_HEAD:
           head_stage();
-          if (!q.last_pos) load_qkv<BB>(tq, LW, 0, xcd, li, mw, lane);
+          if (!q.last_pos) load_qkv_paced<BB>(tq, LW, 0, xcd, li, mw, lane);
           else tq = TileQKV{};
           break;
         case S_QKV2:
@@ -1822,7 +1841,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
             math_down(lp - NL, li, td, Col0{});
             math_down(lp, li, td, Col1{});
             if (!last_layer) {
-              load_qkv<BB>(tq, LW, layer + 1, xcd, li, mw, lane);
+              load_qkv_paced<BB>(tq, LW, layer + 1, xcd, li, mw, lane);
             } else {
               int row0, nrows;
               head_rows(0, row0, nrows);
