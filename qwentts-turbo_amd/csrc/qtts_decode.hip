@@ -334,14 +334,18 @@ __device__ __forceinline__ void load_d(TileD& t, const TTSLayerWeights* L, int l
       t.p[3 * g + j] = wload<BB>(lw(L, layer, W_DOWN) + (size_t)row * INTER + XI * xcd + 8 * ((lane & 15) + 16 * j));
   }
 }
-// rows [row0 + 0 .. nrows) of a [*, 1024] head, nrows <= 3 per wave (into the QKV tile's registers)
+// rows [row0 + 0 .. nrows) of a [*, 1024] head, nrows <= 3 per wave (into the QKV tile's registers).
+// Non-temporal in both models: a code-predictor head (4 MB) is read once per frame, and kept out of the
+// caches it leaves the 256 MB MALL to what is re-read sooner, the code predictor's layers (157 MB, 15 times
+// per frame) and the backbone's KV cache (backbone step 486 -> 483 us at L=512). The code predictor's
+// layer tiles stay temporal: non-temporal there, the frame went 900 -> 971 us (and the backbone 486 -> 472).
 template <bool BB>
 __device__ __forceinline__ void load_head(TileQKV& t, const bf16_t* W, int row0, int nrows, int lane) {
 #pragma unroll
   for (int r = 0; r < 3; ++r) {
     if (r < nrows) {
-      t.p[2 * r] = wload<BB>(W + (size_t)(row0 + r) * HID + 8 * lane);
-      t.p[2 * r + 1] = wload<BB>(W + (size_t)(row0 + r) * HID + 512 + 8 * lane);
+      t.p[2 * r] = ldw_nt(W + (size_t)(row0 + r) * HID + 8 * lane);
+      t.p[2 * r + 1] = ldw_nt(W + (size_t)(row0 + r) * HID + 512 + 8 * lane);
     }
   }
 }
