@@ -19,7 +19,8 @@
 //     (chunk, query head); the poller of every O-projection workgroup merges the chunk partials
 //     (m, l, acc). Contexts that fit one pass are attended locally by every workgroup.
 //   * Each workgroup = 4 math waves + 1 poller wave. Math waves hold their weight slices in
-//     VGPRs, the next step's tile issued one step ahead, and run the GEMVs and attention. The poller wave
+//     VGPRs (the next step's tile issued one step ahead, the two largest paced so that their HBM
+//     bursts spread over the exchanges in flight) and run the GEMVs and attention. The poller wave
 //     waits for the inputs of the next stage (tagged exchange slots, see qtts_common.h),
 //     applies the vector work (RMSNorm, q/k-norm + RoPE, KV write, split-K merge, the
 //     cross-XCD sums + residuals, token selection) and leaves ready operands in LDS. Keeping
@@ -227,7 +228,11 @@ __device__ __forceinline__ u32x4 wload(const bf16_t* p) {
   if constexpr (BB) return ldw_nt(p); else return ldw(p);
 }
 
-template <bool BB>
+// The QKV tile. SLEEP > 0 paces it one row (two loads per lane) at a time, SLEEP x 64 cycles apart: the
+// code predictor issues it after its down partials are published (or after a head), and whole, its 8.4 MB
+// burst lands on the down all-reduce's cross-XCD hop (SLEEP 12, ~0.4 us: frame 920 -> 902 us; 8 apart
+// 919 us, halves 32 or 48 apart slower; the backbone gains nothing from it).
+template <bool BB, int SLEEP = 0>
 __device__ __forceinline__ void load_qkv(TileQKV& t, const TTSLayerWeights* L, int layer, int xcd, int li, int mw, int lane) {
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -238,24 +243,9 @@ __device__ __forceinline__ void load_qkv(TileQKV& t, const TTSLayerWeights* L, i
     else row = lw(L, layer, W_V) + (size_t)(128 * xcd + lr - 384) * HID;
     t.p[2 * r] = wload<BB>(row + 8 * lane);
     t.p[2 * r + 1] = wload<BB>(row + 512 + 8 * lane);
-  }
-}
-// The QKV tile one row (two loads per lane) at a time, 12 x 64 cycles (~0.4 us) apart: issued after the
-// down partials are published (or after a code-predictor head), its 8.4 MB burst otherwise lands whole on
-// the down all-reduce's cross-XCD hop (code predictor: frame 920 -> 902 us; 8 apart 919 us, halves 32 or
-// 48 apart slower; the backbone gains nothing from it).
-template <bool BB>
-__device__ __forceinline__ void load_qkv_paced(TileQKV& t, const TTSLayerWeights* L, int layer, int xcd, int li, int mw, int lane) {
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int lr = 16 * li + 4 * mw + r;   // local row of the XCD's 512
-    const bf16_t* row;
-    if (lr < 256) row = lw(L, layer, W_Q) + (size_t)(256 * xcd + lr) * HID;
-    else if (lr < 384) row = lw(L, layer, W_K) + (size_t)(128 * xcd + lr - 256) * HID;
-    else row = lw(L, layer, W_V) + (size_t)(128 * xcd + lr - 384) * HID;
-    t.p[2 * r] = wload<BB>(row + 8 * lane);
-    t.p[2 * r + 1] = wload<BB>(row + 512 + 8 * lane);
-    if (r < 3) __builtin_amdgcn_s_sleep(12);
+    if constexpr (SLEEP > 0) {
+      if (r < 3) __builtin_amdgcn_s_sleep(SLEEP);
+    }
   }
 }
 template <bool BB>
@@ -1801,7 +1791,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           down_stage(layer);
           if (!last_layer) {
             if constexpr (BB) load_qkv<BB>(tq, LW, layer + 1, xcd, li, mw, lane);
-            else load_qkv_paced<BB>(tq, LW, layer + 1, xcd, li, mw, lane);
+            else load_qkv<BB, 12>(tq, LW, layer + 1, xcd, li, mw, lane);
           } else if (q.head) {
             int row0, nrows;
             head_rows(0, row0, nrows);
@@ -1814,7 +1804,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           break;
         case S_HEAD:
           head_stage();
-          if (!q.last_pos) load_qkv_paced<BB>(tq, LW, 0, xcd, li, mw, lane);
+          if (!q.last_pos) load_qkv<BB, 12>(tq, LW, 0, xcd, li, mw, lane);
           else tq = TileQKV{};
           break;
         case S_QKV2:
@@ -1845,7 +1835,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
             math_down(lp - NL, li, td, Col0{});
             math_down(lp, li, td, Col1{});
             if (!last_layer) {
-              load_qkv_paced<BB>(tq, LW, layer + 1, xcd, li, mw, lane);
+              load_qkv<BB, 12>(tq, LW, layer + 1, xcd, li, mw, lane);
             } else {
               int row0, nrows;
               head_rows(0, row0, nrows);
