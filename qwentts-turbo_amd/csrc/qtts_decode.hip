@@ -1402,8 +1402,8 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
   // Step schedule. One walker defines the barrier sequence; the poller wave and the math
   // waves each run it with their own action, in separate loops (so the math waves' weight
   // tiles and the poller's poll registers are never live at the same time). Math waves run
-  // the compute of step k on operands the poller prepared during step k-1 and issue the
-  // weight loads needed two steps later.
+  // the compute of step k on operands the poller prepared during step k-1 and then issue the
+  // weight tile of step k+1.
   // =====================================================================================
   enum Step { S_PRO, S_QKV, S_ATT, S_O, S_GU, S_DOWN, S_HEAD, S_QKV2, S_ATT2, S_GU2, S_DOWN2 };
   int nstep = 0;
