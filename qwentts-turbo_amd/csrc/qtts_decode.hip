@@ -314,7 +314,11 @@ __device__ __forceinline__ void load_gu_paced(TileGU& t, const TTSLayerWeights* 
     load_gu_rows<BB, 2, 3>(t, L, layer, xcd, li, mw, lane);
   }
 }
-template <bool BB>
+// The down tile: two row groups of 3 loads per lane. Code predictor: the second group ~0.3 us
+// (s_sleep 12) after the first, so that the burst does not all land on the SwiGLU all-gather
+// (frame 898 -> 891 us; 6 or 8 apart: 901 us, 16 apart: 894 us, 24 apart: 903 us; the backbone
+// gains nothing measurable).
+template <bool BB, int SLEEP = 0>
 __device__ __forceinline__ void load_d(TileD& t, const TTSLayerWeights* L, int layer, int xcd, int li, int mw, int lane) {
 #pragma unroll
   for (int g = 0; g < 2; ++g) {
@@ -322,6 +326,7 @@ __device__ __forceinline__ void load_d(TileD& t, const TTSLayerWeights* L, int l
 #pragma unroll
     for (int j = 0; j < 3; ++j)
       t.p[3 * g + j] = wload<BB>(lw(L, layer, W_DOWN) + (size_t)row * INTER + XI * xcd + 8 * ((lane & 15) + 16 * j));
+    if constexpr (SLEEP > 0) { if (g == 0) __builtin_amdgcn_s_sleep(SLEEP); }
   }
 }
 // rows [row0 + 0 .. nrows) of a [*, 1024] head, nrows <= 3 per wave (into the QKV tile's registers).
@@ -1785,7 +1790,8 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           break;
         case S_GU:
           gu_stage(layer);
-          load_d<BB>(td, LW, layer, xcd, li, mw, lane);
+          if constexpr (BB) load_d<BB>(td, LW, layer, xcd, li, mw, lane);
+          else load_d<BB, 12>(td, LW, layer, xcd, li, mw, lane);
           break;
         case S_DOWN:
           down_stage(layer);
