@@ -231,7 +231,8 @@ __device__ __forceinline__ u32x4 wload(const bf16_t* p) {
 // The QKV tile. SLEEP > 0 paces it one row (two loads per lane) at a time, SLEEP x 64 cycles apart: the
 // code predictor issues it after its down partials are published (or after a head), and whole, its 8.4 MB
 // burst lands on the down all-reduce's cross-XCD hop (SLEEP 12, ~0.4 us: frame 920 -> 902 us; 8 apart
-// 919 us, halves 32 or 48 apart slower; the backbone gains nothing from it).
+// 919 us, halves 32 or 48 apart slower). With the down tile paced too, SLEEP 16 at every site: frame
+// 892 -> 885 us (20 apart: 894 us, 24: 889 us). The backbone's QKV tile is slower paced (16: +2 us).
 template <bool BB, int SLEEP = 0>
 __device__ __forceinline__ void load_qkv(TileQKV& t, const TTSLayerWeights* L, int layer, int xcd, int li, int mw, int lane) {
 #pragma unroll
@@ -314,10 +315,10 @@ __device__ __forceinline__ void load_gu_paced(TileGU& t, const TTSLayerWeights* 
     load_gu_rows<BB, 2, 3>(t, L, layer, xcd, li, mw, lane);
   }
 }
-// The down tile: two row groups of 3 loads per lane. Code predictor: the second group ~0.3 us
-// (s_sleep 12) after the first, so that the burst does not all land on the SwiGLU all-gather
-// (frame 898 -> 891 us; 6 or 8 apart: 901 us, 16 apart: 894 us, 24 apart: 903 us; the backbone
-// gains nothing measurable).
+// The down tile: two row groups of 3 loads per lane, the second ~0.3 us (s_sleep 12) after the
+// first, so that the burst does not all land on the SwiGLU all-gather. Code predictor: frame
+// 898 -> 891 us (6 or 8 apart: 901 us, 16 apart: 894 us, 24 apart: 903 us, three pieces: 906 us);
+// backbone: step 484.0 -> 482.4 us (16 apart: 482.4, 24 apart: 484.0).
 template <bool BB, int SLEEP = 0>
 __device__ __forceinline__ void load_d(TileD& t, const TTSLayerWeights* L, int layer, int xcd, int li, int mw, int lane) {
 #pragma unroll
@@ -1790,14 +1791,13 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           break;
         case S_GU:
           gu_stage(layer);
-          if constexpr (BB) load_d<BB>(td, LW, layer, xcd, li, mw, lane);
-          else load_d<BB, 12>(td, LW, layer, xcd, li, mw, lane);
+          load_d<BB, 12>(td, LW, layer, xcd, li, mw, lane);
           break;
         case S_DOWN:
           down_stage(layer);
           if (!last_layer) {
             if constexpr (BB) load_qkv<BB>(tq, LW, layer + 1, xcd, li, mw, lane);
-            else load_qkv<BB, 12>(tq, LW, layer + 1, xcd, li, mw, lane);
+            else load_qkv<BB, 16>(tq, LW, layer + 1, xcd, li, mw, lane);
           } else if (q.head) {
             int row0, nrows;
             head_rows(0, row0, nrows);
@@ -1810,7 +1810,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           break;
         case S_HEAD:
           head_stage();
-          if (!q.last_pos) load_qkv<BB, 12>(tq, LW, 0, xcd, li, mw, lane);
+          if (!q.last_pos) load_qkv<BB, 16>(tq, LW, 0, xcd, li, mw, lane);
           else tq = TileQKV{};
           break;
         case S_QKV2:
@@ -1841,7 +1841,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
             math_down(lp - NL, li, td, Col0{});
             math_down(lp, li, td, Col1{});
             if (!last_layer) {
-              load_qkv<BB, 12>(tq, LW, layer + 1, xcd, li, mw, lane);
+              load_qkv<BB, 16>(tq, LW, layer + 1, xcd, li, mw, lane);
             } else {
               int row0, nrows;
               head_rows(0, row0, nrows);
