@@ -335,7 +335,9 @@ __device__ __forceinline__ void load_d(TileD& t, const TTSLayerWeights* L, int l
 // caches it leaves the 256 MB MALL to what is re-read sooner, the code predictor's layers (157 MB, 15 times
 // per frame) and the backbone's KV cache (backbone step 486 -> 483 us at L=512). The code predictor's
 // layer tiles stay temporal: non-temporal there, the frame went 900 -> 971 us (and the backbone 486 -> 472).
-template <bool BB>
+// SLEEP > 0: the rows after the first ~SLEEP x 64 cycles later (s_sleep 16 after a model's last down
+// publish: frame 1,358.3 -> 1,356.1 us, code predictor and backbone together; 8 apart: 1,357.6).
+template <bool BB, int SLEEP = 0>
 __device__ __forceinline__ void load_head(TileQKV& t, const bf16_t* W, int row0, int nrows, int lane) {
 #pragma unroll
   for (int r = 0; r < 3; ++r) {
@@ -343,6 +345,7 @@ __device__ __forceinline__ void load_head(TileQKV& t, const bf16_t* W, int row0,
       t.p[2 * r] = ldw_nt(W + (size_t)(row0 + r) * HID + 8 * lane);
       t.p[2 * r + 1] = ldw_nt(W + (size_t)(row0 + r) * HID + 512 + 8 * lane);
     }
+    if constexpr (SLEEP > 0) { if (r == 0) __builtin_amdgcn_s_sleep(SLEEP); }
   }
 }
 
@@ -1801,7 +1804,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
           } else if (q.head) {
             int row0, nrows;
             head_rows(0, row0, nrows);
-            load_head<BB>(tq, head_weights(pi), row0, nrows, lane);
+            load_head<BB, 16>(tq, head_weights(pi), row0, nrows, lane);
           } else if (!q.last_pos) {
             load_qkv<BB>(tq, LW, 0, xcd, li, mw, lane);
           } else {
@@ -1845,7 +1848,7 @@ __global__ void __launch_bounds__(NTHR, 1) qtts_decode_kernel(const KArgs a) {
             } else {
               int row0, nrows;
               head_rows(0, row0, nrows);
-              load_head<BB>(tq, head_weights(pi), row0, nrows, lane);
+              load_head<BB, 16>(tq, head_weights(pi), row0, nrows, lane);
             }
           }
           break;
