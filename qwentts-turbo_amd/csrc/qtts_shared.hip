@@ -641,7 +641,9 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
   };
   // a gathered 1024-vector (h1 or the residual after the down projection): its norm into the
   // projection input, the workgroup's rows kept in `keep`
-  auto cp_prep_vec = [&](const uint64_t* base, uint32_t tag, const bf16_t* gains, float* keep, int n, auto&& issue) SH_INLINE {
+  // gather a 1024-vector, keep this workgroup's rows, normalize it into projection input column n;
+  // `issue` runs after the gather's last poll, `issue2` after the vector work
+  auto cp_prep_vec2 = [&](const uint64_t* base, uint32_t tag, const bf16_t* gains, float* keep, int n, auto&& issue, auto&& issue2) SH_INLINE {
     load_gains(gains);
     float xv[16], y[16];
     gather1024(P, base, tag, xv);
@@ -649,6 +651,10 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
     keep_rows(keep, xv);
     normed(xv, y);
     put_vec_n(n, y);
+    issue2();
+  };
+  auto cp_prep_vec = [&](const uint64_t* base, uint32_t tag, const bf16_t* gains, float* keep, int n, auto&& issue) SH_INLINE {
+    cp_prep_vec2(base, tag, gains, keep, n, issue, []() SH_INLINE {});
   };
   auto cp_prep_down = [&](int lp, auto&& issue) SH_INLINE {
     float v[6];
@@ -1086,6 +1092,13 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) t.p[j] = wld(row + 32 * (8 * (wv & 3) + j) + 8 * kg);
   };
+  // half `part` of load_g's tile (K-blocks 4 part .. 4 part + 3 of the wave's 8)
+  auto load_g_half = [&](TG& t, int layer, int part) {
+    const int i = lane & 15, kg = lane >> 4, tile = wv >> 2;
+    const bf16_t* row = lw(LW, layer, tile ? W_UP : W_GATE) + (size_t)(XI * xcd + 12 * li + (i < 12 ? i : 0)) * HID;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) t.p[4 * part + j] = wld(row + 32 * (8 * (wv & 3) + 4 * part + j) + 8 * kg);
+  };
   auto load_d = [&](TD& t, int layer) {
     const int i = lane & 15, kg = lane >> 4, tile = wv >> 2;
     const bf16_t* row = lw(LW, layer, W_DOWN) + (size_t)(32 * li + 16 * tile + i) * INTER + XI * xcd;
@@ -1427,13 +1440,18 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
       }
       stamp(14);
       {
-        auto iss = [&]() SH_INLINE { stamp(12); load_g(tgu, layer); };
+        // the gate/up tile (48 KB per workgroup) in two halves, the second after the vector work:
+        // issued whole, its burst lands on the other workgroups' gathers (config 4: code-predictor
+        // launch 1,488 -> 1,459 us, backbone 858 -> 849 us; a 2 + 6 split gained nothing, 6 + 2 less)
+        auto iss = [&]() SH_INLINE { stamp(12); load_g_half(tgu, layer, 0); };
+        auto iss2 = [&]() SH_INLINE { load_g_half(tgu, layer, 1); };
         if (me) {
           ar1(lp, par, s.xres[wv]);
           stamp(11);
-          cp_prep_vec(&ws->h1[xcd][par][wv][0], tag_of(lp, T_H1), lw(LW, layer, W_LNPOST), s.h1res[wv], wv, iss);
+          cp_prep_vec2(&ws->h1[xcd][par][wv][0], tag_of(lp, T_H1), lw(LW, layer, W_LNPOST), s.h1res[wv], wv, iss, iss2);
         } else {
           iss();
+          iss2();
         }
       }
       stamp(2 + wv);
