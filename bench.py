@@ -39,7 +39,7 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch measured with rocprofv3 PMC counters on the same workload
 # (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000 KiB, both factors from a plain 512 MiB device copy);
 # the summary with the commands is profiles/qtts_decode_kernel_frame512_pmc_traffic.md.
-PMC_TRAFFIC = {"cp_frame": 2_620_173_813, "backbone_step": 987_964_735}
+PMC_TRAFFIC = {"cp_frame": 2_619_539_356, "backbone_step": 987_971_947}
 
 
 def backbone_bytes(L: int) -> int:
