@@ -19,11 +19,11 @@
 //     (chunk, query head); the poller of every O-projection workgroup merges the chunk partials
 //     (m, l, acc). Contexts that fit one pass are attended locally by every workgroup.
 //   * Each workgroup = 4 math waves + 1 poller wave. Math waves hold their weight slices in
-//     VGPRs (the next step's tile issued one step ahead, the two largest paced so that their HBM
-//     bursts spread over the exchanges in flight) and run the GEMVs and attention. The poller wave
-//     waits for the inputs of the next stage (tagged exchange slots, see qtts_common.h),
-//     applies the vector work (RMSNorm, q/k-norm + RoPE, KV write, split-K merge, the
-//     cross-XCD sums + residuals, token selection) and leaves ready operands in LDS. Keeping
+//     VGPRs (the next step's tile issued one step ahead, the QKV, gate/up, down and head tiles
+//     paced so that their HBM bursts spread over the exchanges in flight) and run the GEMVs and
+//     attention. The poller wave waits for the inputs of the next stage (tagged exchange slots,
+//     see qtts_common.h), applies the vector work (RMSNorm, q/k-norm + RoPE, KV write, split-K
+//     merge, the cross-XCD sums + residuals, token selection) and leaves ready operands in LDS. Keeping
 //     the polls on their own wave keeps them out of the math waves' in-order load queue.
 #include <hip/hip_runtime.h>
 #include <atomic>

@@ -639,10 +639,9 @@ __global__ void __launch_bounds__(STHR, 1) qtts_shared_kernel(const SArgs a) {
       kv_pending = true;   // ordered before this wave's next slot publish (ar1)
     }
   };
-  // a gathered 1024-vector (h1 or the residual after the down projection): its norm into the
-  // projection input, the workgroup's rows kept in `keep`
-  // gather a 1024-vector, keep this workgroup's rows, normalize it into projection input column n;
-  // `issue` runs after the gather's last poll, `issue2` after the vector work
+  // a gathered 1024-vector (h1 or the residual after the down projection): its norm into projection
+  // input column n, the workgroup's rows kept in `keep`; `issue` runs after the gather's last poll,
+  // `issue2` after the vector work
   auto cp_prep_vec2 = [&](const uint64_t* base, uint32_t tag, const bf16_t* gains, float* keep, int n, auto&& issue, auto&& issue2) SH_INLINE {
     load_gains(gains);
     float xv[16], y[16];
